@@ -1,0 +1,146 @@
+/*
+ * tgs_sampler.h -- C ABI of the MI355X (gfx950) decode-time sampler.
+ *
+ * One call samples a [B, V] batch of logits rows on the GPU: repetition /
+ * presence / frequency penalties from a per-row token history, per-row
+ * temperature, a grammar mask read from a per-state vocab bitmask table
+ * resident in HBM, top-k, top-p, and a categorical draw from a
+ * caller-supplied uniform.  A second entry point runs speculative-decoding
+ * verification (accept/reject plus residual resample).
+ *
+ * Plain C: no HIP or torch types.  Streams are passed as `tgs_stream`,
+ * which is HIP's hipStream_t (a pointer to struct ihipStream_t); NULL means
+ * the default stream of the handle's device.
+ *
+ * Ownership: the caller owns every input and output buffer (device
+ * pointers on the handle's device).  The handle owns its workspace and the
+ * mask table.  Calls are asynchronous on `stream`; synchronise before
+ * reading outputs.  One handle serves one host thread at a time, and calls
+ * on one handle must be ordered on one stream (they share workspace).
+ *
+ * Errors are status codes (never exceptions).  Argument errors the host can
+ * see are returned by the call; per-row conditions found on the device are
+ * written into the row's output id:
+ *     id >= 0   sampled token
+ *     id == -1  no token is allowed (all masked / -inf / NaN)   [TGS_EALLMASKED]
+ *     id == -2  invalid row parameters (see tgs_row_params)
+ *
+ * Reference interfaces replaced (paths under the reference repository):
+ *   tgs_sample       <- Server.sampleToken(from:temperature:constraint:)
+ *                       native-mac/Sources/TinyGPTServe/Serve.swift:1483-1506;
+ *                       Sample.sampleWithSchema native-mac/Sources/TinyGPT/Sample.swift:812-836;
+ *                       ModelController.runGenerate penalty + top-k
+ *                       native-mac/Sources/TinyGPTApp/ModelController.swift:262-304;
+ *                       the tg_generate sampler wasm/src/model.cpp:486-516 (C ABI precedent:
+ *                       WASM_EXPORT extern "C" + opaque handle, wasm/src/model.h:17-56)
+ *   tgs_mask_table_* <- LogitsMasker.mask(forFSM:) native-mac/Sources/TinyGPTModel/ConstrainedGen.swift:805-822
+ *                       and ServeTokenMasker.mask(for:) Serve.swift:2005-2025 (the per-step
+ *                       host-built float mask becomes a per-state bit row kept in HBM)
+ *   tgs_spec_verify  <- SpeculativeDecode.stepStochastic native-mac/Sources/TinyGPT/SpeculativeDecode.swift:121-210
+ *                       and the greedy SpeculativeDecode.step :41-98
+ */
+#ifndef TGS_SAMPLER_H
+#define TGS_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TGS_ABI_VERSION 1
+
+struct ihipStream_t;
+typedef struct ihipStream_t* tgs_stream;
+
+typedef struct tgs_ctx* tgs_handle; /* opaque, cf. TgModel in wasm/src/model.h:17-18 */
+
+typedef enum {
+  TGS_OK = 0,
+  TGS_EINVAL = -1,     /* bad argument                                    */
+  TGS_ENOMEM = -2,     /* device allocation failed                        */
+  TGS_EHIP = -3,       /* HIP runtime error (no device, launch failure)   */
+  TGS_EALLMASKED = -4, /* used by host wrappers for rows whose id is -1   */
+  TGS_ETOOBIG = -5     /* size beyond what the handle was created for     */
+} tgs_status;
+
+typedef enum { TGS_F32 = 0, TGS_BF16 = 1 } tgs_dtype;
+
+#define TGS_FLAG_GREEDY 1 /* decode this row by argmax regardless of T */
+
+/* Per-row parameters (32 bytes, device memory, one per row). */
+typedef struct {
+  float temperature;  /* <= 0 (or TGS_FLAG_GREEDY): greedy argmax; else finite > 0     */
+  int32_t top_k;      /* <= 0 or >= V: disabled                                         */
+  float top_p;        /* >= 1: disabled; must be > 0                                    */
+  float repetition;   /* CTRL penalty over distinct history ids; 1 = off; must be > 0   */
+  float presence;     /* subtracted once from every id present in the history           */
+  float frequency;    /* subtracted per occurrence of the id in the history             */
+  int32_t mask_state; /* < 0: no grammar mask; else row of the mask table               */
+  int32_t flags;      /* TGS_FLAG_GREEDY                                                */
+} tgs_row_params;
+
+/* Optional per-row diagnostics (host struct of nullable device pointers). */
+typedef struct {
+  int32_t* kept_ids;   /* [B][kept_cap] top-k set, (logit desc, id asc) order, -1 padded.
+                          Written for rows with 1 <= top_k <= 1024; other rows: -1.      */
+  float* kept_probs;   /* [B][kept_cap] normalised probability of each top-p survivor    */
+  int32_t kept_cap;
+  int32_t* counts;     /* [B][2] size of the top-k set, size of the top-p set            */
+  uint64_t* mass;      /* [B][2] S and S' in 2^-40 units (exact integer masses)           */
+  int32_t* cut_ids;    /* [B] id of the last top-p survivor                               */
+  float* post_logits;  /* [B][V] logit after penalties, mask (-inf) and temperature       */
+} tgs_debug;
+
+/* Library / status helpers (no device work). */
+int tgs_abi_version(void);
+const char* tgs_status_string(int status);
+
+/* Create a sampler on `device`.  max_batch, max_vocab and max_hist bound
+ * every later call (workspace is sized once here; calls never allocate). */
+int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int max_hist);
+void tgs_destroy(tgs_handle h);
+const char* tgs_last_error(tgs_handle h);
+
+/* Grammar mask table: n_states rows of ceil(vocab/32) uint32 words; bit v
+ * of row s (word v>>5, bit v&31) is 1 <=> token v is allowed in state s.
+ * _set replaces the table (synchronous upload); _update overwrites n rows
+ * (states[i] < current n_states). */
+int tgs_mask_table_set(tgs_handle h, const uint32_t* host_words, int n_states, int vocab);
+int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32_t* host_words,
+                          int n);
+
+/* Sample one token per row.
+ *   d_logits    [B] rows of V logits, row_stride elements apart (fp32 or bf16)
+ *   d_hist      [B][hist_cap] token history (ids outside [0,V) ignored), nullable if hist_cap == 0
+ *   d_hist_len  [B] valid history entries per row (nullable: hist_cap for every row)
+ *   d_params    [B] tgs_row_params
+ *   d_u         [B] uniforms in [0,1) (ignored by greedy rows)
+ *   d_out_ids   [B] output ids (see the id codes above)
+ *   dbg         nullable diagnostics */
+int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
+               const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
+               const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids,
+               const tgs_debug* dbg, tgs_stream stream);
+
+/* Size the speculative-verification workspace for up to max_batch sequences
+ * of up to max_k draft tokens (allocates; call once before capturing
+ * tgs_spec_verify in a graph).  tgs_spec_verify grows the workspace itself
+ * (allocating, hence synchronising) when a call exceeds the reservation. */
+int tgs_reserve_spec(tgs_handle h, int max_batch, int max_k);
+
+/* Speculative verification for B sequences with k draft tokens each.
+ *   d_target [B][k+1][V], d_draft [B][k][V] contiguous logits (fp32 or bf16)
+ *   d_draft_tok [B][k]; d_T [B] temperature (<= 0: greedy verify, else max(T,1e-5));
+ *   d_u_acc [B][k] accept uniforms; d_u_res [B] resample / bonus uniform.
+ * Outputs: d_n_acc [B] accepted draft count (-1 error), d_out [B][k+1]
+ * accepted drafts followed by the resampled or bonus token, -1 padded. */
+int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs_dtype dt,
+                    const int32_t* d_draft_tok, int B, int k, int V, const float* d_T,
+                    const float* d_u_acc, const float* d_u_res, int32_t* d_n_acc, int32_t* d_out,
+                    tgs_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TGS_SAMPLER_H */

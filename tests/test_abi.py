@@ -1,0 +1,68 @@
+"""The C ABI library: builds, loads, exports every declared entry point, and
+rejects bad arguments on the host (no GPU work).  CPU only."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tgs_sampler.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(tgs_[a-z_0-9]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import tinygpt_amd._lib as L
+
+    if not os.path.exists(L.LIB_PATH):
+        from tinygpt_amd import build
+
+        build.build()
+    return L.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    import tinygpt_amd._lib as L
+
+    names = declared_functions()
+    assert names == sorted(L.EXPORTS)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.tgs_abi_version() == 1
+    assert lib.tgs_status_string(0) == b"ok"
+    assert b"invalid" in lib.tgs_status_string(-1)
+    assert lib.tgs_status_string(12345) == b"unknown status"
+
+
+def test_create_rejects_bad_arguments(lib):
+    h = C.c_void_p()
+    assert lib.tgs_create(None, 0, 1, 1, 0) == -1
+    assert lib.tgs_create(C.byref(h), 0, 0, 100, 0) == -1
+    assert lib.tgs_create(C.byref(h), 0, 4, 300000, 0) == -1  # vocab beyond 262144
+    assert lib.tgs_create(C.byref(h), 0, 4, 100, 5000) == -1  # history beyond 4096
+    assert h.value is None
+
+
+def test_null_handle_calls_fail_cleanly(lib):
+    assert lib.tgs_sample(None, None, 0, 1, 1, 1, None, None, 0, None, None, None, None, None) == -1
+    assert lib.tgs_spec_verify(None, None, None, 0, None, 1, 1, 1, None, None, None, None, None, None) == -1
+    assert lib.tgs_mask_table_set(None, None, 0, 1) == -1
+    assert lib.tgs_last_error(None) == b"null handle"
+    lib.tgs_destroy(None)
+
+
+def test_library_has_no_cpu_sampling_path():
+    """The product sources carry no host implementation of the sampler:
+    every sampling computation is a __global__ kernel."""
+    api = open(os.path.join(ROOT, "tinygpt_amd", "csrc", "tgs_api.hip")).read()
+    for needle in ("tg_expf", "tg_q40", "qsort", "nth_element", "oracle"):
+        assert needle not in api

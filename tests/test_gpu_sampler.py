@@ -1,0 +1,215 @@
+"""GPU parity: the HIP sampler through the C ABI against the CPU oracle.
+
+Bit-exact on token ids, kept-candidate lists, the exact integer masses S and
+S', top-p cut ids, normalised probabilities of the survivors and the
+post-penalty logits.  Every case prints its name before touching the GPU.
+"""
+import numpy as np
+import pytest
+
+import gpu_harness as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(sampler, oracle, name, logits, params, u, hist=None, hist_len=None, mask_table=None,
+           kept_cap=64, post=True):
+    H.log(f"case {name}: B={logits.shape[0]} V={logits.shape[1]}")
+    g = H.run_gpu(sampler, logits, params, u, hist, hist_len, mask_table, kept_cap=kept_cap, post=post)
+    o = H.run_oracle(oracle, logits, params, u, hist, hist_len, mask_table, kept_cap=kept_cap, post=post)
+    V = logits.shape[1]
+    rep = H.compare(g, o, params, V, check_post=post, what=name)
+    H.log(f"case {name}: ok {rep}")
+    return g, o, rep
+
+
+def test_c2_llama3_shape(sampler, oracle):
+    from tinygpt_amd import workloads as W
+
+    c = W.config2()
+    _check(sampler, oracle, "c2", c["logits"], c["params"], c["u"], c["hist"], c["hist_len"])
+
+
+def test_c3_grammar_mask(sampler, oracle):
+    from tinygpt_amd import workloads as W
+
+    c = W.config3()
+    _check(sampler, oracle, "c3", c["logits"], c["params"], c["u"], mask_table=c["mask_table"])
+
+
+def test_c4_large_batch_bf16_subset(sampler, oracle):
+    from tinygpt_amd import workloads as W
+
+    c = W.config4(B=96)
+    _check(sampler, oracle, "c4-96", c["logits"], c["params"], c["u"], c["hist"], c["hist_len"],
+           kept_cap=1024, post=False)
+
+
+def test_c4_large_batch_bf16_full_ids(sampler, oracle):
+    from tinygpt_amd import workloads as W
+
+    c = W.config4()
+    H.log("case c4-full: B=1024 V=151936 bf16")
+    g = H.run_gpu(sampler, c["logits"], c["params"], c["u"], c["hist"], c["hist_len"], kept_cap=8, post=False)
+    o = H.run_oracle(oracle, c["logits"], c["params"], c["u"], c["hist"], c["hist_len"], kept_cap=8,
+                     post=False, nthreads=16)
+    H.compare(g, o, c["params"], c["V"], check_post=False, what="c4-full")
+
+
+def test_c1_decode_loop(sampler, oracle):
+    """1000 decode steps: history is the ring of the last 64 sampled ids."""
+    import tinygpt_amd as tg
+    from tinygpt_amd import workloads as W
+
+    c = W.config1_step_inputs()
+    H.log("case c1: 1000 steps B=1 V=256")
+    hist_g = list(c["hist0"])
+    hist_o = list(c["hist0"])
+    for s in range(c["logits"].shape[0]):
+        x = c["logits"][s:s + 1]
+        hg = np.int32(hist_g[-64:])[None]
+        ho = np.int32(hist_o[-64:])[None]
+        g = H.run_gpu(sampler, x, c["params"], c["u"][s:s + 1], hg, None, kept_cap=40, post=(s % 100 == 0))
+        o = H.run_oracle(oracle, x, c["params"], c["u"][s:s + 1], ho, None, kept_cap=40, post=(s % 100 == 0), nthreads=1)
+        H.compare(g, o, c["params"], 256, check_post=(s % 100 == 0), what=f"c1 step {s}")
+        hist_g.append(int(g["ids"][0]))
+        hist_o.append(int(o["ids"][0]))
+    assert hist_g == hist_o
+
+
+def _random_batch(g, B, V, oracle):
+    x = (g.standard_normal((B, V)) * g.choice([0.5, 2.0, 3.0])).astype(np.float32)
+    params = oracle.make_params(B)
+    for b in range(B):
+        params["temperature"][b] = g.choice([0.0, 0.3, 0.7, 1.0, 1.7])
+        params["top_k"][b] = g.choice([0, 1, 2, 5, 40, 64, 65, 257, 1023, 1024, 1025, V // 3, V - 1, V, V + 5])
+        params["top_p"][b] = g.choice([1.0, 0.95, 0.5, 0.1, 0.999])
+        params["repetition"][b] = g.choice([1.0, 1.1, 1.3, 0.8])
+        params["presence"][b] = g.choice([0.0, 0.5, -0.4])
+        params["frequency"][b] = g.choice([0.0, 0.3])
+        kind = b % 7
+        if kind == 1:  # ties: spikes
+            x[b, g.choice(V, size=min(8, V), replace=False)] = 9.0
+        elif kind == 2:  # coarse values: ties everywhere
+            x[b] = np.round(x[b])
+        elif kind == 3:  # special values
+            n = max(1, V // 50)
+            x[b, g.choice(V, size=n, replace=False)] = np.nan
+            x[b, g.choice(V, size=n, replace=False)] = -np.inf
+        elif kind == 4:  # all equal
+            x[b] = 1.25
+        elif kind == 5:  # ascending (adversarial for running thresholds)
+            x[b] = np.linspace(-5, 5, V, dtype=np.float32)
+    H_ = 64
+    hist = g.integers(-2, V + 2, size=(B, H_)).astype(np.int32)
+    hist_len = g.integers(0, H_ + 1, size=B).astype(np.int32)
+    u = (g.integers(0, 1 << 24, size=B) / (1 << 24)).astype(np.float32)
+    return x, params, u, hist, hist_len
+
+
+@pytest.mark.parametrize("V", [7, 256, 300, 5000, 40000, 128256])
+def test_random_rows(sampler, oracle, V):
+    g = np.random.default_rng(500 + V)
+    B = 64 if V < 100000 else 24
+    x, params, u, hist, hist_len = _random_batch(g, B, V, oracle)
+    _check(sampler, oracle, f"random V={V}", x, params, u, hist, hist_len, kept_cap=1025)
+
+
+@pytest.mark.parametrize("V", [300, 40000])
+def test_random_rows_masked(sampler, oracle, V):
+    g = np.random.default_rng(900 + V)
+    B = 48
+    x, params, u, hist, hist_len = _random_batch(g, B, V, oracle)
+    n_states = 5
+    words = (V + 31) // 32
+    table = g.integers(0, 1 << 32, size=(n_states, words), dtype=np.uint64).astype(np.uint32)
+    table[1] &= np.uint32(0x01010101)  # sparse
+    table[2] = 0                       # nothing allowed
+    table[3] = 0xFFFFFFFF              # everything allowed
+    table[4] = 0
+    table[4, 0] = 1                    # only id 0
+    params["mask_state"] = g.integers(-1, n_states + 1, size=B)  # includes an out-of-range state
+    _check(sampler, oracle, f"masked V={V}", x, params, u, hist, hist_len, mask_table=table, kept_cap=1025)
+
+
+def test_invalid_rows(sampler, oracle):
+    V, B = 300, 12
+    g = np.random.default_rng(77)
+    x = g.standard_normal((B, V)).astype(np.float32)
+    params = oracle.make_params(B, temperature=1.0, top_k=10, top_p=0.9)
+    params["temperature"][0] = np.nan
+    params["temperature"][1] = np.inf
+    params["top_p"][2] = 0.0
+    params["repetition"][3] = 0.0
+    params["presence"][4] = np.inf
+    params["mask_state"][5] = 3   # no table
+    params["temperature"][6] = 0.0
+    params["top_p"][6] = 0.0      # greedy ignores top_p
+    u = np.full(B, 0.5, np.float32)
+    u[7] = 1.0
+    u[8] = np.nan
+    hist = np.zeros((B, 4), np.int32)
+    hist_len = np.full(B, 4, np.int32)
+    hist_len[9] = 5               # beyond hist_cap
+    g_, o_, _ = _check(sampler, oracle, "invalid", x, params, u, hist, hist_len)
+    assert list(g_["ids"][:10]) == [-2, -2, -2, -2, -2, -2, int(np.argmax(x[6])), -2, -2, -2]
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 8, 16])
+def test_split_invariance(sampler, oracle, split, monkeypatch):
+    from tinygpt_amd import workloads as W
+
+    monkeypatch.setenv("TGS_SPLIT", str(split))
+    c = W.config2(B=16, seed_offset=100)
+    c["params"]["top_k"][::3] = 1024
+    c["params"]["temperature"][1::5] = 0.0
+    _check(sampler, oracle, f"split={split}", c["logits"], c["params"], c["u"], c["hist"], c["hist_len"],
+           kept_cap=1024, post=False)
+
+
+def test_unaligned_rows(sampler, oracle):
+    """Row stride V+1: rows are not 16-byte aligned, the scalar load path runs."""
+    import torch
+
+    import tinygpt_amd as tg
+
+    g = np.random.default_rng(88)
+    B, V = 8, 5001
+    big = (g.standard_normal((B, V + 1)) * 2).astype(np.float32)
+    params = oracle.make_params(B, temperature=0.9, top_k=50, top_p=0.9)
+    params["temperature"][0] = 0.0
+    params["top_k"][1] = 0
+    u = (g.integers(0, 1 << 24, size=B) / (1 << 24)).astype(np.float32)
+    H.log("case unaligned: B=8 V=5001 stride 5002")
+    sampler.set_mask_table(np.zeros((0, 1), np.uint32), 1)
+    lg = torch.from_numpy(big).cuda()[:, :V]
+    out = sampler.sample(lg, tg.params_to_device(params, "cuda:0"), torch.from_numpy(u).cuda(), vocab=V)
+    torch.cuda.synchronize()
+    o = oracle.sample_batch(np.ascontiguousarray(big[:, :V]), params, u)
+    np.testing.assert_array_equal(out.cpu().numpy(), o["ids"])
+
+
+def test_empty_batch(sampler):
+    import torch
+
+    import tinygpt_amd as tg
+
+    H.log("case empty batch")
+    lg = torch.zeros((0, 16), dtype=torch.float32, device="cuda:0")
+    out = sampler.sample(lg, tg.params_to_device(tg.make_params(0), "cuda:0"),
+                         torch.zeros(0, device="cuda:0"))
+    torch.cuda.synchronize()
+    assert out.numel() == 0
+
+
+def test_repeat_calls_are_identical(sampler, oracle):
+    """Split-row counters reset themselves: back-to-back calls agree."""
+    from tinygpt_amd import workloads as W
+
+    c = W.config2(B=32, seed_offset=7)
+    H.log("case repeat x5")
+    first = H.run_gpu(sampler, c["logits"], c["params"], c["u"], c["hist"], c["hist_len"], post=False)
+    for _ in range(4):
+        again = H.run_gpu(sampler, c["logits"], c["params"], c["u"], c["hist"], c["hist_len"], post=False)
+        np.testing.assert_array_equal(first["ids"], again["ids"])
+        np.testing.assert_array_equal(first["kept_ids"], again["kept_ids"])

@@ -1,0 +1,22 @@
+"""tinygpt_amd -- MI355X-native decode-time logits processing and sampling.
+
+The product is libtgs_sampler.so (C ABI in include/tgs_sampler.h): gfx950
+HIP kernels for penalties, temperature, the grammar mask, top-k, top-p, the
+categorical draw and speculative verification.  This package holds the
+kernels' sources (csrc/), the in-tree build, a ctypes binding (`Sampler`),
+the host-side mirror of the reference sampling API (`host`), and the
+synthetic workloads of the benchmark configurations (`workloads`).
+"""
+from ._lib import (  # noqa: F401
+    EXPORTS,
+    ROW_PARAMS_DTYPE,
+    TGS_BF16,
+    TGS_EALLMASKED,
+    TGS_EINVAL,
+    TGS_F32,
+    TGS_FLAG_GREEDY,
+    TGS_OK,
+    TgsError,
+    load,
+)
+from .sampler import Sampler, make_params, params_to_device  # noqa: F401

@@ -1,0 +1,351 @@
+// tgs_api.hip -- host side of the C ABI declared in include/tgs_sampler.h.
+//
+// The handle owns the split-row workspace (chunk candidate lists and
+// self-resetting arrival counters), the speculative workspace and the mask
+// table.  Calls validate host-visible arguments, choose the split (chunks
+// per row) from the batch size, size the dynamic LDS and launch one kernel
+// on the caller's stream.  Nothing here allocates during tgs_sample.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "tgs_device.h"
+#include "tgs_kernels.h"
+
+struct tgs_ctx {
+  int device = 0;
+  int max_batch = 0, max_vocab = 0, max_hist = 0;
+  int num_cu = 256;
+  size_t lds_limit = 65536;
+  unsigned* counters = nullptr;
+  unsigned long long* ws = nullptr;
+  int* ws_cnt = nullptr;
+  int ws_rows = 0;
+  uint32_t* mask_table = nullptr;
+  int n_states = 0, mask_vocab = 0, mask_words = 0;
+  unsigned* spec_counters = nullptr;
+  float* spec_stats = nullptr;
+  unsigned long long* spec_arg = nullptr;
+  int spec_b = 0, spec_k = -1;
+  std::string err;
+};
+
+namespace {
+
+constexpr int kMaxVocab = 262144;  // 256 speculative blocks of 1024 ids
+constexpr int kMaxHist = 4096;
+constexpr int kMaxSplit = 16;
+
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+int fail(tgs_ctx* h, int code, const std::string& msg) {
+  if (h) h->err = msg;
+  return code;
+}
+
+int hip_fail(tgs_ctx* h, hipError_t e, const char* what) {
+  return fail(h, TGS_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+int log2i(int x) {
+  int l = 0;
+  while ((1 << l) < x) l++;
+  return l;
+}
+
+void free_spec(tgs_ctx* h) {
+  if (h->spec_counters) (void)hipFree(h->spec_counters);
+  if (h->spec_stats) (void)hipFree(h->spec_stats);
+  if (h->spec_arg) (void)hipFree(h->spec_arg);
+  h->spec_counters = nullptr;
+  h->spec_stats = nullptr;
+  h->spec_arg = nullptr;
+  h->spec_b = 0;
+  h->spec_k = -1;
+}
+
+// Chunks per row: enough workgroups to cover the chip twice, chunks of at
+// least one tile, at most kMaxSplit.  TGS_SPLIT overrides (tuning).
+int choose_split(const tgs_ctx* h, int B, int V, int dtype) {
+  const int tile = dtype == TGS_BF16 ? 8192 : 4096;
+  int S = 1;
+  const char* env = std::getenv("TGS_SPLIT");
+  if (env && std::atoi(env) > 0) {
+    S = std::min(std::atoi(env), kMaxSplit);
+  } else {
+    const int target = 2 * h->num_cu;
+    while (S * 2 <= kMaxSplit && (long long)S * 2 * B <= target && (V + S * 2 - 1) / (S * 2) >= tile) S *= 2;
+  }
+  while (S > 1 && (long long)S * B > h->ws_rows) S >>= 1;
+  return S;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tgs_abi_version(void) { return TGS_ABI_VERSION; }
+
+const char* tgs_status_string(int status) {
+  switch (status) {
+    case TGS_OK: return "ok";
+    case TGS_EINVAL: return "invalid argument";
+    case TGS_ENOMEM: return "device allocation failed";
+    case TGS_EHIP: return "HIP runtime error";
+    case TGS_EALLMASKED: return "no allowed token in the row";
+    case TGS_ETOOBIG: return "size exceeds the handle's limits";
+    default: return "unknown status";
+  }
+}
+
+int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int max_hist) {
+  if (!out) return TGS_EINVAL;
+  *out = nullptr;
+  if (max_batch < 1 || max_vocab < 1 || max_vocab > kMaxVocab || max_hist < 0 || max_hist > kMaxHist)
+    return TGS_EINVAL;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return TGS_EHIP;
+  if (device < 0 || device >= ndev) return TGS_EINVAL;
+  tgs_ctx* h = new (std::nothrow) tgs_ctx;
+  if (!h) return TGS_ENOMEM;
+  h->device = device;
+  h->max_batch = max_batch;
+  h->max_vocab = max_vocab;
+  h->max_hist = max_hist;
+  DeviceGuard g(device);
+  if (!g.ok) {
+    delete h;
+    return TGS_EHIP;
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && v > 0)
+    h->num_cu = v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
+    h->lds_limit = (size_t)v;
+  h->ws_rows = std::max(max_batch, 2 * h->num_cu);
+  hipError_t e = hipMalloc(&h->counters, sizeof(unsigned) * (size_t)max_batch);
+  if (e == hipSuccess) e = hipMalloc(&h->ws, sizeof(unsigned long long) * (size_t)h->ws_rows * tgs::KMAX);
+  if (e == hipSuccess) e = hipMalloc(&h->ws_cnt, sizeof(int) * (size_t)h->ws_rows);
+  if (e == hipSuccess) e = hipMemset(h->counters, 0, sizeof(unsigned) * (size_t)max_batch);
+  if (e == hipSuccess) {
+    // raise the dynamic-LDS ceiling to the device limit; a runtime that
+    // rejects the attribute keeps its default (calls that need more fail
+    // with TGS_ETOOBIG / TGS_EHIP instead)
+    if (tgs::set_sample_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
+    e = hipDeviceSynchronize();
+  }
+  if (e != hipSuccess) {
+    tgs_destroy(h);
+    return e == hipErrorOutOfMemory ? TGS_ENOMEM : TGS_EHIP;
+  }
+  *out = h;
+  return TGS_OK;
+}
+
+void tgs_destroy(tgs_handle h) {
+  if (!h) return;
+  DeviceGuard g(h->device);
+  if (h->counters) (void)hipFree(h->counters);
+  if (h->ws) (void)hipFree(h->ws);
+  if (h->ws_cnt) (void)hipFree(h->ws_cnt);
+  if (h->mask_table) (void)hipFree(h->mask_table);
+  free_spec(h);
+  delete h;
+}
+
+const char* tgs_last_error(tgs_handle h) { return h ? h->err.c_str() : "null handle"; }
+
+int tgs_mask_table_set(tgs_handle h, const uint32_t* host_words, int n_states, int vocab) {
+  if (!h) return TGS_EINVAL;
+  if (n_states < 0 || vocab < 1 || (n_states > 0 && !host_words)) return fail(h, TGS_EINVAL, "mask table: bad arguments");
+  DeviceGuard g(h->device);
+  const int words = (vocab + 31) / 32;
+  uint32_t* dptr = nullptr;
+  const size_t bytes = sizeof(uint32_t) * (size_t)n_states * words;
+  if (n_states > 0) {
+    hipError_t e = hipMalloc(&dptr, bytes);
+    if (e != hipSuccess) return fail(h, TGS_ENOMEM, "mask table allocation failed");
+    e = hipMemcpy(dptr, host_words, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(dptr);
+      return hip_fail(h, e, "mask table upload");
+    }
+  }
+  if (h->mask_table) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(h->mask_table);
+  }
+  h->mask_table = dptr;
+  h->n_states = n_states;
+  h->mask_vocab = vocab;
+  h->mask_words = words;
+  return TGS_OK;
+}
+
+int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32_t* host_words, int n) {
+  if (!h) return TGS_EINVAL;
+  if (n < 0 || (n > 0 && (!host_states || !host_words))) return fail(h, TGS_EINVAL, "mask update: bad arguments");
+  DeviceGuard g(h->device);
+  for (int i = 0; i < n; i++) {
+    if (host_states[i] < 0 || host_states[i] >= h->n_states) return fail(h, TGS_EINVAL, "mask update: state out of range");
+    hipError_t e = hipMemcpy(h->mask_table + (size_t)host_states[i] * h->mask_words,
+                             host_words + (size_t)i * h->mask_words, sizeof(uint32_t) * h->mask_words,
+                             hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(h, e, "mask update upload");
+  }
+  return TGS_OK;
+}
+
+int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
+               const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
+               const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids,
+               const tgs_debug* dbg, tgs_stream stream) {
+  if (!h) return TGS_EINVAL;
+  if (dt != TGS_F32 && dt != TGS_BF16) return fail(h, TGS_EINVAL, "dtype");
+  if (B < 0 || V < 1 || row_stride < V) return fail(h, TGS_EINVAL, "shape");
+  if (B == 0) return TGS_OK;
+  if (B > h->max_batch || V > h->max_vocab || hist_cap > h->max_hist)
+    return fail(h, TGS_ETOOBIG, "batch, vocab or history beyond the handle's limits");
+  if (hist_cap < 0 || (hist_cap > 0 && !d_hist)) return fail(h, TGS_EINVAL, "history");
+  if (!d_logits || !d_params || !d_u || !d_out_ids) return fail(h, TGS_EINVAL, "null buffer");
+  tgs_debug dz;
+  std::memset(&dz, 0, sizeof(dz));
+  if (dbg) {
+    dz = *dbg;
+    if (dz.kept_cap < 0 || ((dz.kept_ids || dz.kept_probs) && dz.kept_cap == 0))
+      return fail(h, TGS_EINVAL, "debug kept_cap");
+  }
+  DeviceGuard g(h->device);
+  if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
+
+  const size_t esz = dt == TGS_BF16 ? 2 : 4;
+  tgs::SampleArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.logits = d_logits;
+  a.row_stride = row_stride;
+  a.B = B;
+  a.V = V;
+  a.aligned = ((uintptr_t)d_logits % 16 == 0) && (((uint64_t)row_stride * esz) % 16 == 0);
+  a.hist = d_hist;
+  a.hist_len = d_hist_len;
+  a.hist_cap = hist_cap;
+  a.params = d_params;
+  a.u = d_u;
+  a.out = d_out_ids;
+  const bool table_ok = h->mask_table && h->mask_vocab >= V;
+  a.mask_table = table_ok ? h->mask_table : nullptr;
+  a.n_states = table_ok ? h->n_states : 0;
+  a.mask_words = h->mask_words;
+  const int S = choose_split(h, B, V, dt);
+  int L = V;
+  if (S > 1) {
+    L = ((V + S - 1) / S + 1023) / 1024 * 1024;
+  }
+  a.S = (V + L - 1) / L;
+  a.L = L;
+  a.TS = hist_cap > 0 ? next_pow2(std::max(64, 2 * hist_cap)) : 0;
+  a.ts_shift = a.TS ? 32 - log2i(a.TS) : 0;
+  a.BW = hist_cap > 0 ? (L + 31) / 32 : 0;
+  a.capt = tgs::CAPB + hist_cap;
+  a.off_hash = 0;
+  a.off_bitmap = a.TS * 8;
+  a.off_cand = (a.off_bitmap + a.BW * 4 + 15) / 16 * 16;
+  const size_t lds = (size_t)a.off_cand + (size_t)a.capt * 8;
+  if (lds + sizeof(tgs::BlockScratch) > h->lds_limit)
+    return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
+  a.counters = h->counters;
+  a.ws = h->ws;
+  a.ws_cnt = h->ws_cnt;
+  a.dbg = dz;
+  const int grid = a.S == 1 ? B : ((B + 7) / 8) * 8 * a.S;
+  hipError_t e = tgs::launch_sample(a, dt, grid, lds, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
+  return TGS_OK;
+}
+
+int tgs_reserve_spec(tgs_handle h, int max_batch, int max_k) {
+  if (!h) return TGS_EINVAL;
+  if (max_batch < 1 || max_k < 0 || max_k > 64) return fail(h, TGS_EINVAL, "spec reserve");
+  if (max_batch <= h->spec_b && max_k <= h->spec_k) return TGS_OK;
+  DeviceGuard g(h->device);
+  (void)hipDeviceSynchronize();
+  const int nb = std::max(max_batch, h->spec_b);
+  const int nk = std::max(max_k, h->spec_k);
+  free_spec(h);
+  const size_t rows = (size_t)nb * (2 * nk + 1);
+  hipError_t e = hipMalloc(&h->spec_counters, sizeof(unsigned) * nb);
+  if (e == hipSuccess) e = hipMalloc(&h->spec_stats, sizeof(float) * 2 * rows);
+  if (e == hipSuccess) e = hipMalloc(&h->spec_arg, sizeof(unsigned long long) * rows);
+  if (e == hipSuccess) e = hipMemset(h->spec_counters, 0, sizeof(unsigned) * nb);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    free_spec(h);
+    return fail(h, TGS_ENOMEM, "spec workspace allocation failed");
+  }
+  h->spec_b = nb;
+  h->spec_k = nk;
+  return TGS_OK;
+}
+
+int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs_dtype dt,
+                    const int32_t* d_draft_tok, int B, int k, int V, const float* d_T,
+                    const float* d_u_acc, const float* d_u_res, int32_t* d_n_acc, int32_t* d_out,
+                    tgs_stream stream) {
+  if (!h) return TGS_EINVAL;
+  if (dt != TGS_F32 && dt != TGS_BF16) return fail(h, TGS_EINVAL, "dtype");
+  if (B < 0 || k < 0 || k > 64 || V < 1) return fail(h, TGS_EINVAL, "shape");
+  if (B == 0) return TGS_OK;
+  if (V > h->max_vocab) return fail(h, TGS_ETOOBIG, "vocab beyond the handle's limit");
+  if (!d_target || (k > 0 && (!d_draft || !d_draft_tok || !d_u_acc)) || !d_T || !d_u_res || !d_n_acc || !d_out)
+    return fail(h, TGS_EINVAL, "null buffer");
+  if (B > h->spec_b || k > h->spec_k) {
+    int rc = tgs_reserve_spec(h, B, k);
+    if (rc != TGS_OK) return rc;
+  }
+  DeviceGuard g(h->device);
+  if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
+  const size_t esz = dt == TGS_BF16 ? 2 : 4;
+  tgs::SpecArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.target = d_target;
+  a.draft = d_draft;
+  a.B = B;
+  a.k = k;
+  a.V = V;
+  a.aligned = ((uintptr_t)d_target % 16 == 0) && ((uintptr_t)d_draft % 16 == 0) && (((uint64_t)V * esz) % 16 == 0);
+  a.dtok = d_draft_tok;
+  a.T = d_T;
+  a.u_acc = d_u_acc;
+  a.u_res = d_u_res;
+  a.n_acc = d_n_acc;
+  a.out = d_out;
+  a.counters = h->spec_counters;
+  a.ws_stats = h->spec_stats;
+  a.ws_arg = h->spec_arg;
+  hipError_t e = tgs::launch_spec(a, dt, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(h, e, "spec kernel launch");
+  return TGS_OK;
+}
+
+}  // extern "C"

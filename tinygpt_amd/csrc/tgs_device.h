@@ -1,0 +1,360 @@
+// tgs_device.h -- device-side numerics and block primitives of the gfx950
+// sampler.  Everything here follows the canonical rules of the sampling
+// contract bit for bit:
+//   * tg_expf: Cody-Waite reduction x = n ln2 + r and the degree-7 Taylor
+//     polynomial of e^r (Horner, fused multiply-adds), scaled by 2^n through
+//     the exponent field; 0 below -32.
+//   * masses are exact integers q = floor(e * 2^40), so any summation order
+//     (atomics, trees, split rows) gives the same result;
+//   * order keys map floats to uint32 monotonically (-0 folded onto +0);
+//     composite keys (key(y) << 32 | ~id) order by (y desc, id asc).
+// Wavefronts are 64 lanes; blocks are NT = 256 threads (4 waves).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tgs {
+
+constexpr int NT = 256;        // threads per workgroup
+constexpr int NW = NT / 64;    // waves per workgroup
+constexpr int KMAX = 1024;     // largest top-k served by the candidate path
+constexpr int CAPB = 2048;     // candidate buffer entries (before history)
+constexpr int SPEC_BLOCK = 1024;
+
+typedef unsigned long long u64;
+
+// ------------------------------------------------------------------ numerics
+
+__device__ __forceinline__ float tg_u2f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t tg_f2u(float f) { return __float_as_uint(f); }
+
+__device__ __forceinline__ float tg_expf(float x) {
+  if (!(x >= -32.0f)) return 0.0f;
+  if (x > 88.0f) return __builtin_inff();
+  const float log2e = 0x1.715476p+0f;
+  const float ln2_hi = 0x1.62ep-1f;
+  const float ln2_lo = 0x1.0bfbe8p-15f;
+  const float shifter = 12582912.0f;
+  float t = x * log2e;
+  float n = (t + shifter) - shifter;
+  float r = __builtin_fmaf(n, -ln2_hi, x);
+  r = __builtin_fmaf(n, -ln2_lo, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  return p * tg_u2f((uint32_t)(ni + 127) << 23);
+}
+
+__device__ __forceinline__ float tg_weight(float y, float m) {
+  return (y == m) ? 1.0f : tg_expf(y - m);
+}
+
+__device__ __forceinline__ u64 tg_q40(float e) { return (u64)(e * 0x1p40f); }
+
+__device__ __forceinline__ float tg_u64_to_f32(u64 x) {
+  if (x < (1ull << 24)) return (float)(uint32_t)x;
+  int lz = __clzll((long long)x);
+  int sh = 40 - lz;
+  u64 m = x >> sh;
+  u64 rem = x & ((1ull << sh) - 1);
+  u64 half = 1ull << (sh - 1);
+  if (rem > half || (rem == half && (m & 1))) m += 1;
+  float f = (float)(uint32_t)m;
+  return f * tg_u2f((uint32_t)(sh + 127) << 23);
+}
+
+__device__ __forceinline__ uint32_t tg_key(float f) {
+  uint32_t u = tg_f2u(f);
+  if (u == 0x80000000u) u = 0;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float tg_unkey(uint32_t k) {
+  return tg_u2f((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+__device__ __forceinline__ u64 comp_key(uint32_t key, int v) {
+  return ((u64)key << 32) | (u64)(0xFFFFFFFFu - (uint32_t)v);
+}
+__device__ __forceinline__ int comp_id(u64 c) { return (int)(0xFFFFFFFFu - (uint32_t)c); }
+__device__ __forceinline__ float comp_y(u64 c) { return tg_unkey((uint32_t)(c >> 32)); }
+
+// floor(a * b / 2^24) for a < 2^64, b < 2^24 (the product fits in 88 bits).
+__device__ __forceinline__ u64 mul_shr24(u64 a, uint32_t b) {
+  u64 lo = a * (u64)b;
+  u64 hi = __umul64hi(a, (u64)b);
+  return (hi << 40) | (lo >> 24);
+}
+
+// ------------------------------------------------------------------ waves
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T x) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    T y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T x) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
+  return x;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max(T x) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    T y = __shfl_xor(x, d, 64);
+    x = y > x ? y : x;
+  }
+  return x;
+}
+
+__device__ __forceinline__ float wave_maxf(float x) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x = fmaxf(x, __shfl_xor(x, d, 64));
+  return x;
+}
+
+// ------------------------------------------------------------------ shared
+
+// Static shared scratch used by the block primitives.
+struct BlockScratch {
+  unsigned hc[256];        // radix histogram: counts
+  u64 hm[256];             // radix histogram: masses
+  u64 red64[NW];
+  unsigned red32[NW];
+  int sel, binc_i;
+  unsigned need;
+  u64 mass_above, found;
+  unsigned cnt_above;
+  int imin0, imin1;
+  unsigned nbuf;
+  int last;
+};
+
+template <typename T>
+__device__ __forceinline__ T block_sum(T x, T* red) {
+  x = wave_sum(x);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane_id() == 0) red[w] = x;
+  __syncthreads();
+  T t = 0;
+#pragma unroll
+  for (int i = 0; i < NW; i++) t += red[i];
+  return t;
+}
+
+template <typename T>
+__device__ __forceinline__ T block_max(T x, T* red) {
+  x = wave_max(x);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane_id() == 0) red[w] = x;
+  __syncthreads();
+  T t = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; i++) t = red[i] > t ? red[i] : t;
+  return t;
+}
+
+// Count-based MSB radix select over a multiset of keys (8-bit digits).
+// `en(f)` calls f(key) for every key this thread owns.  Returns a value T
+// with #{key >= T} >= kth and #{key > T'} < kth for the exact kth key T'; T
+// equals the kth largest key, or a prefix of it with zeroed low bits when
+// the keys of that prefix number exactly what is needed (then
+// #{key >= T} == kth).  kth >= 1 and the multiset holds >= kth keys.
+template <typename K, int NBITS, class Enum>
+__device__ K block_select_kth(Enum en, unsigned kth, BlockScratch& s) {
+  K prefix = 0, pmask = 0;
+  unsigned need = kth;
+  for (int shift = NBITS - 8; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += NT) s.hc[i] = 0;
+    __syncthreads();
+    en([&](K x) {
+      if ((x & pmask) == prefix) atomicAdd(&s.hc[(unsigned)(x >> shift) & 255u], 1u);
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      unsigned cs[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) cs[j] = s.hc[255 - 4 * lane - j];
+      unsigned lsum = cs[0] + cs[1] + cs[2] + cs[3];
+      unsigned cum = wave_incl_scan(lsum) - lsum;
+      int found = -1;
+      unsigned above = 0, bc = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        if (found < 0 && cs[j] > 0 && cum + cs[j] >= need) {
+          found = 255 - 4 * lane - j;
+          above = cum;
+          bc = cs[j];
+        }
+        cum += cs[j];
+      }
+      u64 bal = __ballot(found >= 0);
+      int first = __ffsll((long long)bal) - 1;
+      if (lane == first) {
+        s.sel = found;
+        s.need = need - above;
+        s.binc_i = (int)bc;
+      }
+    }
+    __syncthreads();
+    const int d = s.sel;
+    need = s.need;
+    const unsigned bc = (unsigned)s.binc_i;
+    prefix |= (K)d << shift;
+    pmask |= (K)255 << shift;
+    if (bc == need) break;
+  }
+  return prefix;
+}
+
+// Mass-based MSB radix select over unique 64-bit composite keys, each with
+// an integer mass.  Finds the element i (in descending key order) that is
+// the first with C_i >= target, where C_i is the inclusive mass prefix.
+// `en(f)` calls f(key, mass) for every key this thread owns.  Returns the
+// element's key; *before gets the mass strictly ahead of it, *rank the
+// number of elements strictly ahead of it.
+template <class Enum>
+__device__ u64 block_mass_select(Enum en, u64 target, BlockScratch& s, u64* before,
+                                 unsigned* rank) {
+  u64 prefix = 0, pmask = 0;
+  u64 mass_above = 0;
+  unsigned cnt_above = 0;
+  bool single = false;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += NT) {
+      s.hc[i] = 0;
+      s.hm[i] = 0;
+    }
+    __syncthreads();
+    en([&](u64 x, u64 q) {
+      if ((x & pmask) == prefix) {
+        const unsigned d = (unsigned)(x >> shift) & 255u;
+        atomicAdd(&s.hc[d], 1u);
+        if (q) atomicAdd(&s.hm[d], q);
+      }
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      unsigned cs[4];
+      u64 ms[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        cs[j] = s.hc[255 - 4 * lane - j];
+        ms[j] = s.hm[255 - 4 * lane - j];
+      }
+      u64 lm = ms[0] + ms[1] + ms[2] + ms[3];
+      unsigned lc = cs[0] + cs[1] + cs[2] + cs[3];
+      u64 cm = wave_incl_scan(lm) - lm + mass_above;
+      unsigned cc = wave_incl_scan(lc) - lc + cnt_above;
+      int found = -1;
+      u64 ab = 0;
+      unsigned ca = 0, bc = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        if (found < 0 && cs[j] > 0 && cm + ms[j] >= target) {
+          found = 255 - 4 * lane - j;
+          ab = cm;
+          ca = cc;
+          bc = cs[j];
+        }
+        cm += ms[j];
+        cc += cs[j];
+      }
+      u64 bal = __ballot(found >= 0);
+      int first = __ffsll((long long)bal) - 1;
+      if (lane == first) {
+        s.sel = found;
+        s.mass_above = ab;
+        s.cnt_above = ca;
+        s.binc_i = (int)bc;
+      }
+    }
+    __syncthreads();
+    const int d = s.sel;
+    mass_above = s.mass_above;
+    cnt_above = s.cnt_above;
+    const int bc = s.binc_i;
+    prefix |= (u64)d << shift;
+    pmask |= (u64)255 << shift;
+    if (bc == 1) {
+      single = shift > 0;
+      break;
+    }
+  }
+  if (single) { // one element carries this prefix: fetch its full key
+    __syncthreads();
+    en([&](u64 x, u64) {
+      if ((x & pmask) == prefix) s.found = x;
+    });
+    __syncthreads();
+    prefix = s.found;
+  }
+  *before = mass_above;
+  *rank = cnt_above;
+  return prefix;
+}
+
+// In-place descending bitonic sort of n2 (power of two) keys in LDS.
+__device__ __forceinline__ void block_bitonic_desc(u64* buf, int n2) {
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (n2 >> 1); i += NT) {
+        const int pos = 2 * i - (i & (stride - 1));
+        const int q = pos + stride;
+        const bool desc = (pos & size) == 0;
+        u64 a = buf[pos], b = buf[q];
+        if (desc ? (a < b) : (a > b)) {
+          buf[pos] = b;
+          buf[q] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Inclusive prefix sum of n <= 4*NT u64 values in LDS (in place).
+__device__ __forceinline__ void block_incl_scan_u64(u64* c, int n, u64* red) {
+  const int base = threadIdx.x * 4;
+  u64 v[4];
+  u64 run = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    v[j] = (base + j < n) ? c[base + j] : 0;
+    run += v[j];
+    v[j] = run;
+  }
+  u64 incl = wave_incl_scan(run);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane_id() == 63) red[w] = incl;
+  __syncthreads();
+  u64 off = incl - run;
+  for (int i = 0; i < w; i++) off += red[i];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    if (base + j < n) c[base + j] = v[j] + off;
+  __syncthreads();
+}
+
+}  // namespace tgs

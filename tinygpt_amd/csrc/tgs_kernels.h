@@ -1,0 +1,55 @@
+// tgs_kernels.h -- argument blocks shared by the host C ABI and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tgs_sampler.h"
+
+namespace tgs {
+
+struct SampleArgs {
+  const void* logits;
+  long long row_stride;  // elements
+  int B, V;
+  int aligned;           // rows start 16-byte aligned: vector loads
+  const int* hist;
+  const int* hist_len;
+  int hist_cap;
+  const tgs_row_params* params;
+  const float* u;
+  int* out;
+  const uint32_t* mask_table;
+  int n_states, mask_words;
+  int S, L;              // chunks per row, chunk length in ids
+  int TS, ts_shift;      // history hash slots (power of two), 32 - log2(TS)
+  int BW;                // history bitmap words per chunk
+  int capt;              // candidate buffer entries
+  int off_hash, off_bitmap, off_cand;  // dynamic LDS byte offsets
+  unsigned* counters;    // [B] split-row arrival counters (self-resetting)
+  unsigned long long* ws;  // [B*S][KMAX] chunk candidate lists
+  int* ws_cnt;           // [B*S]
+  tgs_debug dbg;
+};
+
+struct SpecArgs {
+  const void* target;
+  const void* draft;
+  int B, k, V;
+  int aligned;
+  const int* dtok;
+  const float* T;
+  const float* u_acc;
+  const float* u_res;
+  int* n_acc;
+  int* out;
+  unsigned* counters;          // [B]
+  float* ws_stats;             // [B][2k+1][2] (m, S)
+  unsigned long long* ws_arg;  // [B][2k+1] argmax composite
+};
+
+hipError_t launch_sample(const SampleArgs& a, int dtype, int grid, size_t lds, hipStream_t st);
+hipError_t set_sample_lds_limit(size_t bytes);
+hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
+
+}  // namespace tgs

@@ -1,0 +1,1204 @@
+// tgs_kernels.hip -- gfx950 kernels of the decode-time sampler.
+//
+// sample_kernel: one launch samples a [B, V] batch.  Workgroup (b, c) owns
+// chunk c of row b (S chunks per row; S = 1 for large batches).  Per row
+// the path depends on its parameters:
+//   greedy    argmax of the post-penalty, masked logits (split over chunks,
+//             merged by the last workgroup of the row);
+//   candidate sampling with 1 <= top_k <= KMAX: each chunk streams its ids
+//             once with coalesced 16-byte loads, keeps a threshold-filtered
+//             candidate buffer in LDS and emits its exact local top-k; the
+//             last workgroup of the row merges S lists, sorts the top-k and
+//             runs softmax masses, the top-p scan and the draw;
+//   full      sampling without a usable top-k: one workgroup walks the row
+//             several times (radix selections on exact integer masses).
+// Penalties: history ids are inserted into an LDS hash (id -> count) and a
+// chunk bitmap; the stream skips them and the history pass adds them back
+// with their penalised logit.  Grammar mask: one 32-bit word of the state's
+// table row per 16-byte vector of logits.
+//
+// spec_kernel: speculative verification.  One workgroup per (sequence, row)
+// computes the row maximum and canonical softmax denominator (block
+// maxima + exact 2^-40 block sums, pairwise fp32 tree); the last workgroup of
+// each sequence runs the accept/reject scan and the residual or bonus draw.
+#include "tgs_device.h"
+#include "tgs_kernels.h"
+
+namespace tgs {
+
+// ------------------------------------------------------------------ loads
+
+template <typename Tin>
+struct Elem;
+template <>
+struct Elem<float> {
+  static constexpr int EPV = 4;
+  static constexpr uint32_t NAN_BITS = 0x7FC00000u;
+  __device__ static __forceinline__ float get(const uint4& r, int e) {
+    const uint32_t w = e == 0 ? r.x : e == 1 ? r.y : e == 2 ? r.z : r.w;
+    return tg_u2f(w);
+  }
+  __device__ static __forceinline__ float scalar(const void* p, long long i) {
+    return ((const float*)p)[i];
+  }
+};
+template <>
+struct Elem<uint16_t> {  // bf16 bits
+  static constexpr int EPV = 8;
+  static constexpr uint32_t NAN_BITS = 0x7FC07FC0u;
+  __device__ static __forceinline__ float get(const uint4& r, int e) {
+    const uint32_t w = (e >> 1) == 0 ? r.x : (e >> 1) == 1 ? r.y : (e >> 1) == 2 ? r.z : r.w;
+    return tg_u2f((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
+  }
+  __device__ static __forceinline__ float scalar(const void* p, long long i) {
+    return tg_u2f((uint32_t)((const uint16_t*)p)[i] << 16);
+  }
+};
+
+// Load EPV consecutive logits starting at id v (v a multiple of EPV) from
+// row pointer rowp; ids >= vend read as NaN (never allowed).
+template <typename Tin>
+__device__ __forceinline__ uint4 load_vec(const Tin* rowp, int v, int vend, bool aligned) {
+  constexpr int EPV = Elem<Tin>::EPV;
+  if (aligned && v + EPV <= vend) return *(const uint4*)(rowp + v);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) w[i] = Elem<Tin>::NAN_BITS;
+  if (sizeof(Tin) == 4) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (v + e < vend) w[e] = ((const uint32_t*)rowp)[v + e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+      if (v + e < vend) {
+        const uint32_t h = ((const uint16_t*)rowp)[v + e];
+        w[e >> 1] = (e & 1) ? ((w[e >> 1] & 0xFFFFu) | (h << 16)) : ((w[e >> 1] & 0xFFFF0000u) | h);
+      }
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ------------------------------------------------------------------ row state
+
+struct Row {
+  int b, c;
+  int mode;  // 0 greedy, 1 candidate top-k, 2 full
+  float invT;
+  int k;
+  float top_p, rep, pres, freq, u;
+  bool use_pen;
+  int H;
+  const int* hrow;
+  const uint32_t* mrow;  // nullptr: no mask
+  int v0, v1;            // chunk id range [v0, v1)
+};
+
+// Dynamic LDS carve-up (byte offsets computed on the host).
+struct Lds {
+  int2* hash;         // [TS] (id, count), id -1 = empty
+  uint32_t* bitmap;   // [BW] history bits of the chunk
+  u64* cand;          // [capt] candidates; finalize reuses [0, 2*KMAX)
+};
+
+__device__ __forceinline__ unsigned hash_slot(int id, int shift) {
+  return ((unsigned)id * 2654435761u) >> shift;
+}
+
+__device__ void hash_build(const SampleArgs& a, const Row& r, Lds& L, bool with_bitmap) {
+  const int BW = with_bitmap ? a.BW : 0;
+  for (int i = threadIdx.x; i < a.TS; i += NT) L.hash[i] = make_int2(-1, 0);
+  for (int i = threadIdx.x; i < BW; i += NT) L.bitmap[i] = 0u;
+  __syncthreads();
+  const unsigned tmask = (unsigned)a.TS - 1u;
+  for (int j = threadIdx.x; j < r.H; j += NT) {
+    const int id = r.hrow[j];
+    if (id < r.v0 || id >= r.v1 || id >= a.V) continue;
+    unsigned h = hash_slot(id, a.ts_shift);
+    for (;;) {
+      const int old = atomicCAS(&L.hash[h].x, -1, id);
+      if (old == -1 || old == id) {
+        atomicAdd(&L.hash[h].y, 1);
+        break;
+      }
+      h = (h + 1) & tmask;
+    }
+    if (a.BW) atomicOr(&L.bitmap[(id - r.v0) >> 5], 1u << ((id - r.v0) & 31));
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ int hash_count(const int2* hash, int TS, int shift, int id) {
+  const unsigned tmask = (unsigned)TS - 1u;
+  unsigned h = hash_slot(id, shift);
+  for (;;) {
+    const int2 e = hash[h];
+    if (e.x == id) return e.y;
+    if (e.x == -1) return 0;
+    h = (h + 1) & tmask;
+  }
+}
+
+// Penalised logit of a history id (count c > 0).
+__device__ __forceinline__ float penalise(float z, int c, const Row& r) {
+  if (r.rep != 1.0f) z = (z > 0.0f) ? z / r.rep : z * r.rep;
+  z = z - r.freq * (float)c;
+  z = z - r.pres;
+  return z;
+}
+
+__device__ __forceinline__ bool mask_allows(const Row& r, int v) {
+  return r.mrow == nullptr || ((r.mrow[v >> 5] >> (v & 31)) & 1u);
+}
+
+// Key of one element: 0 when not allowed.
+__device__ __forceinline__ uint32_t elem_key(float z, bool allowed, float invT, float* y_out) {
+  const float y = z * invT;
+  const bool ok = allowed && (y > -__builtin_inff());
+  *y_out = ok ? y : -__builtin_inff();
+  return ok ? tg_key(y) : 0u;
+}
+
+// ------------------------------------------------------------------ finalize
+
+// kept candidates in L.cand[0, n) (unsorted, unique composites, n <= KMAX):
+// sort, masses, top-p, draw; writes the output id and diagnostics.
+__device__ void finalize_topk(const SampleArgs& a, const Row& r, Lds& L, int n, BlockScratch& s) {
+  const int b = r.b;
+  u64* C = L.cand + KMAX;
+  if (n <= 0) {
+    if (threadIdx.x == 0) {
+      a.out[b] = -1;
+      if (a.dbg.counts) { a.dbg.counts[2 * b] = 0; a.dbg.counts[2 * b + 1] = 0; }
+      if (a.dbg.mass) { a.dbg.mass[2 * b] = 0; a.dbg.mass[2 * b + 1] = 0; }
+      if (a.dbg.cut_ids) a.dbg.cut_ids[b] = -1;
+    }
+    if (a.dbg.kept_ids)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
+    if (a.dbg.kept_probs)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
+    return;
+  }
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (int i = n + threadIdx.x; i < n2; i += NT) L.cand[i] = 0ull;
+  __syncthreads();
+  block_bitonic_desc(L.cand, n2);
+  const float m = comp_y(L.cand[0]);
+  for (int i = threadIdx.x; i < n; i += NT) C[i] = tg_q40(tg_weight(comp_y(L.cand[i]), m));
+  __syncthreads();
+  block_incl_scan_u64(C, n, s.red64);
+  const u64 S = C[n - 1];
+  if (threadIdx.x == 0) {
+    s.imin0 = n - 1;
+    s.imin1 = 0x7FFFFFFF;
+  }
+  __syncthreads();
+  if (r.top_p < 1.0f) {
+    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
+    const u64 P = mul_shr24(S, pq);
+    int best = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += NT)
+      if (C[i] >= P && i < best) best = i;
+    if (best != 0x7FFFFFFF) atomicMin(&s.imin0, best);
+    __syncthreads();
+  }
+  const int istar = s.imin0;
+  const u64 Sp = C[istar];
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
+  const u64 t = mul_shr24(Sp, uq);
+  {
+    int best = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i <= istar; i += NT)
+      if (C[i] > t && i < best) best = i;
+    if (best != 0x7FFFFFFF) atomicMin(&s.imin1, best);
+  }
+  __syncthreads();
+  int pick = s.imin1;
+  if (pick > istar) pick = istar;
+  if (threadIdx.x == 0) {
+    a.out[b] = comp_id(L.cand[pick]);
+    if (a.dbg.counts) { a.dbg.counts[2 * b] = n; a.dbg.counts[2 * b + 1] = istar + 1; }
+    if (a.dbg.mass) { a.dbg.mass[2 * b] = S; a.dbg.mass[2 * b + 1] = Sp; }
+    if (a.dbg.cut_ids) a.dbg.cut_ids[b] = comp_id(L.cand[istar]);
+  }
+  if (a.dbg.kept_ids) {
+    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kid[i] = i < n ? comp_id(L.cand[i]) : -1;
+  }
+  if (a.dbg.kept_probs) {
+    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
+    const float fs = tg_u64_to_f32(Sp);
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) {
+      float pv = 0.0f;
+      if (i <= istar) pv = tg_u64_to_f32(C[i] - (i ? C[i - 1] : 0ull)) / fs;
+      kp[i] = pv;
+    }
+  }
+}
+
+__device__ void finalize_greedy(const SampleArgs& a, int b, u64 best) {
+  const int id = best ? comp_id(best) : -1;
+  if (threadIdx.x == 0) {
+    a.out[b] = id;
+    if (a.dbg.counts) { a.dbg.counts[2 * b] = id >= 0; a.dbg.counts[2 * b + 1] = id >= 0; }
+    if (a.dbg.mass) { a.dbg.mass[2 * b] = 0; a.dbg.mass[2 * b + 1] = 0; }
+    if (a.dbg.cut_ids) a.dbg.cut_ids[b] = id;
+  }
+  if (a.dbg.kept_ids) {
+    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kid[i] = (i == 0) ? id : -1;
+  }
+  if (a.dbg.kept_probs) {
+    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kp[i] = (i == 0 && id >= 0) ? 1.0f : 0.0f;
+  }
+}
+
+// Keep the entries >= T of buf[0, n) in place (order not preserved); returns
+// the new count.  Batches of 4*NT entries: a batch is read completely before
+// its survivors are written, and survivors only land below the batch end
+// (the output count never exceeds the number of entries read so far).
+__device__ int compact_ge(u64* buf, int n, u64 T, BlockScratch& s) {
+  __syncthreads();
+  if (threadIdx.x == 0) s.nbuf = 0;
+  __syncthreads();
+  for (int base = 0; base < n; base += 4 * NT) {
+    u64 x[4];
+    unsigned cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = base + j * NT + (int)threadIdx.x;
+      x[j] = (i < n) ? buf[i] : 0ull;
+      cnt += (i < n && x[j] >= T);
+    }
+    __syncthreads();
+    unsigned pos = cnt ? atomicAdd(&s.nbuf, cnt) : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = base + j * NT + (int)threadIdx.x;
+      if (i < n && x[j] >= T) buf[pos++] = x[j];
+    }
+  }
+  __syncthreads();
+  return (int)s.nbuf;
+}
+
+// ------------------------------------------------------------------ split merge
+
+// Chunk result handoff: returns true in the last workgroup of the row.
+__device__ bool arrive_last(const SampleArgs& a, int b, BlockScratch& s) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = atomicAdd(&a.counters[b], 1u);
+    s.last = (prev == (unsigned)a.S - 1u);
+  }
+  __syncthreads();
+  if (!s.last) return false;
+  __threadfence();
+  return true;
+}
+
+// ------------------------------------------------------------------ full path
+
+// Streams row b once, calling f(v, key, y) for every id.  Keys are
+// recomputed from global memory (the row stays hot in L2 / MALL).
+template <typename Tin, class F>
+__device__ void full_stream(const SampleArgs& a, const Row& r, const Lds& L, const Tin* rowp, F f) {
+  constexpr int EPV = Elem<Tin>::EPV;
+  const int nvec = (a.V + EPV - 1) / EPV;
+  for (int vi = threadIdx.x; vi < nvec; vi += NT) {
+    const int v = vi * EPV;
+    const uint4 raw = load_vec<Tin>(rowp, v, a.V, a.aligned);
+    const uint32_t mw = r.mrow ? r.mrow[v >> 5] : 0xFFFFFFFFu;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) {
+      const int id = v + e;
+      float z = Elem<Tin>::get(raw, e);
+      if (r.use_pen && id < a.V) {
+        const int cnt = hash_count(L.hash, a.TS, a.ts_shift, id);
+        if (cnt > 0) z = penalise(z, cnt, r);
+      }
+      float y;
+      const uint32_t key = elem_key(z, ((mw >> (id & 31)) & 1u) != 0, r.invT, &y);
+      if (id < a.V) f(id, key, y);
+    }
+  }
+}
+
+template <typename Tin>
+__device__ void full_path(const SampleArgs& a, const Row& r, Lds& L, BlockScratch& s) {
+  const int b = r.b;
+  const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
+  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)b * a.V : nullptr;
+  // pass A: maximum composite and allowed count
+  u64 best = 0;
+  unsigned nv = 0;
+  full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float y) {
+    if (post) post[v] = y;
+    if (key) {
+      nv++;
+      const u64 c = comp_key(key, v);
+      best = c > best ? c : best;
+    }
+  });
+  best = block_max(best, s.red64);
+  nv = block_sum(nv, s.red32);
+  if (nv == 0) {
+    finalize_topk(a, r, L, 0, s);
+    return;
+  }
+  const unsigned kk = (r.k >= 1 && r.k < a.V) ? ((unsigned)r.k < nv ? (unsigned)r.k : nv) : nv;
+  // pass B: top-k threshold (exact count of kk entries)
+  u64 T = 1;
+  if (kk < nv) {
+    T = block_select_kth<u64, 64>(
+        [&](auto f) {
+          full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float) {
+            if (key) f(comp_key(key, v));
+          });
+        },
+        kk, s);
+  }
+  const float m = comp_y(best);
+  // pass C: total mass of the kept set and its last element
+  u64 S = 0, minc = ~0ull;
+  full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float y) {
+    if (!key) return;
+    const u64 c = comp_key(key, v);
+    if (c < T) return;
+    S += tg_q40(tg_weight(y, m));
+    minc = c < minc ? c : minc;
+  });
+  S = block_sum(S, s.red64);
+  minc = ~block_max(~minc, s.red64);
+  auto kept_enum = [&](auto f) {
+    full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float y) {
+      if (!key) return;
+      const u64 c = comp_key(key, v);
+      if (c >= T) f(c, tg_q40(tg_weight(y, m)));
+    });
+  };
+  // pass D: top-p cut
+  u64 cutc = minc, Sp = S;
+  unsigned ntopp = kk;
+  if (r.top_p < 1.0f) {
+    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
+    const u64 P = mul_shr24(S, pq);
+    if (P == 0) {
+      cutc = best;
+      Sp = tg_q40(1.0f);
+      ntopp = 1;
+    } else {
+      u64 before;
+      unsigned rank;
+      cutc = block_mass_select(kept_enum, P, s, &before, &rank);
+      Sp = before + tg_q40(tg_weight(comp_y(cutc), m));
+      ntopp = rank + 1;
+    }
+  }
+  // pass E: draw
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
+  const u64 t = mul_shr24(Sp, uq);
+  u64 before;
+  unsigned rank;
+  const u64 pick = block_mass_select(kept_enum, t + 1, s, &before, &rank);
+  if (threadIdx.x == 0) {
+    a.out[b] = comp_id(pick);
+    if (a.dbg.counts) { a.dbg.counts[2 * b] = (int)kk; a.dbg.counts[2 * b + 1] = (int)ntopp; }
+    if (a.dbg.mass) { a.dbg.mass[2 * b] = S; a.dbg.mass[2 * b + 1] = Sp; }
+    if (a.dbg.cut_ids) a.dbg.cut_ids[b] = comp_id(cutc);
+  }
+  if (a.dbg.kept_ids)
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
+  if (a.dbg.kept_probs)
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
+}
+
+// ------------------------------------------------------------------ chunk paths
+
+template <typename Tin>
+struct Tile {
+  static constexpr int EPV = Elem<Tin>::EPV;
+  static constexpr int U = 4;                 // 16-byte vectors per thread per tile
+  static constexpr int EPT = U * EPV;         // elements per thread per tile
+  static constexpr int SIZE = NT * EPT;       // ids per tile
+};
+
+// Loads tile `t0` (first id) of the chunk into registers.
+template <typename Tin>
+__device__ __forceinline__ void tile_load(const Tin* rowp, const Row& r, int t0, bool aligned,
+                                          uint4 raw[Tile<Tin>::U], uint32_t mw[Tile<Tin>::U]) {
+  constexpr int EPV = Tile<Tin>::EPV;
+#pragma unroll
+  for (int u = 0; u < Tile<Tin>::U; u++) {
+    const int v = t0 + (u * NT + (int)threadIdx.x) * EPV;
+    raw[u] = load_vec<Tin>(rowp, v, r.v1, aligned);
+    mw[u] = (r.mrow && v < r.v1) ? r.mrow[v >> 5] : 0xFFFFFFFFu;
+  }
+}
+
+// Keys of a loaded tile; history ids (bitmap) and disallowed ids get key 0.
+template <typename Tin>
+__device__ __forceinline__ void tile_keys(const SampleArgs& a, const Row& r, const Lds& L, int t0,
+                                          const uint4 raw[Tile<Tin>::U],
+                                          const uint32_t mw[Tile<Tin>::U],
+                                          uint32_t key[Tile<Tin>::EPT], float* post) {
+  constexpr int EPV = Tile<Tin>::EPV;
+#pragma unroll
+  for (int u = 0; u < Tile<Tin>::U; u++) {
+    const int v = t0 + (u * NT + (int)threadIdx.x) * EPV;
+    uint32_t hb = 0;
+    if (r.use_pen && v < r.v1) hb = L.bitmap[(v - r.v0) >> 5];
+#pragma unroll
+    for (int e = 0; e < EPV; e++) {
+      const int id = v + e;
+      const bool hist = (hb >> ((id - r.v0) & 31)) & 1u;
+      float y;
+      const bool allowed = ((mw[u] >> (id & 31)) & 1u) && !hist;
+      uint32_t k = elem_key(Elem<Tin>::get(raw[u], e), allowed, r.invT, &y);
+      key[u * EPV + e] = k;
+      if (post && id < r.v1 && !hist) post[id] = y;
+    }
+  }
+}
+
+__device__ __forceinline__ int tile_id(int t0, int j, int EPV) {
+  const int u = j / EPV, e = j % EPV;
+  return t0 + (u * NT + (int)threadIdx.x) * EPV + e;
+}
+
+// History ids of the chunk with their penalised logits: calls f(v, key, y).
+template <typename Tin, class F>
+__device__ void history_pass(const SampleArgs& a, const Row& r, const Lds& L, const Tin* rowp, F f) {
+  for (int i = threadIdx.x; i < a.TS; i += NT) {
+    const int2 e = L.hash[i];
+    if (e.x < 0) continue;
+    const int v = e.x;
+    const float z = penalise(Elem<Tin>::scalar(rowp, v), e.y, r);
+    float y;
+    const uint32_t key = elem_key(z, mask_allows(r, v), r.invT, &y);
+    f(v, key, y);
+  }
+}
+
+template <typename Tin>
+__device__ void greedy_chunk(const SampleArgs& a, const Row& r, Lds& L, BlockScratch& s) {
+  using TL = Tile<Tin>;
+  const Tin* rowp = (const Tin*)a.logits + (long long)r.b * a.row_stride;
+  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)r.b * a.V : nullptr;
+  u64 best = 0;
+  uint4 raw[TL::U];
+  uint32_t mw[TL::U];
+  uint32_t key[TL::EPT];
+  for (int t0 = r.v0; t0 < r.v1; t0 += TL::SIZE) {
+    tile_load<Tin>(rowp, r, t0, a.aligned, raw, mw);
+    tile_keys<Tin>(a, r, L, t0, raw, mw, key, post);
+#pragma unroll
+    for (int j = 0; j < TL::EPT; j++)
+      if (key[j]) {
+        const u64 c = comp_key(key[j], tile_id(t0, j, TL::EPV));
+        best = c > best ? c : best;
+      }
+  }
+  if (r.use_pen)
+    history_pass<Tin>(a, r, L, rowp, [&](int v, uint32_t k, float y) {
+      if (post) post[v] = y;
+      if (k) {
+        const u64 c = comp_key(k, v);
+        best = c > best ? c : best;
+      }
+    });
+  best = block_max(best, s.red64);
+  if (a.S == 1) {
+    finalize_greedy(a, r.b, best);
+    return;
+  }
+  if (threadIdx.x == 0) a.ws[((long long)r.b * a.S + r.c) * KMAX] = best;
+  if (!arrive_last(a, r.b, s)) return;
+  u64 m = 0;
+  for (int c = threadIdx.x; c < a.S; c += NT) {
+    const u64 x = __atomic_load_n(&a.ws[((long long)r.b * a.S + c) * KMAX], __ATOMIC_RELAXED);
+    m = x > m ? x : m;
+  }
+  m = block_max(m, s.red64);
+  finalize_greedy(a, r.b, m);
+  if (threadIdx.x == 0) a.counters[r.b] = 0u;
+}
+
+// Initial threshold from the first tile: a key T0 with at least k keys >= T0
+// among the chunk's stream ids (k <= NT*4).
+template <int EPT>
+__device__ uint32_t first_threshold(const uint32_t key[EPT], int k, BlockScratch& s) {
+  if (k <= 64) {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) mx = key[j] > mx ? key[j] : mx;
+    // k-th largest thread maximum within each wave (bitonic over 64 lanes)
+    uint32_t x = mx;
+    const int lane = lane_id();
+    for (int size = 2; size <= 64; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint32_t y = __shfl_xor(x, stride, 64);
+        const bool lower = (lane & stride) == 0;
+        const bool desc = (lane & size) == 0;
+        // descending blocks keep the larger value in the lower lane
+        const bool take_max = (lower == desc);
+        x = take_max ? (x > y ? x : y) : (x < y ? x : y);
+      }
+    }
+    const uint32_t wk = __shfl(x, k - 1, 64);
+    return block_max(wk, s.red32);
+  }
+  // per-thread j-th largest (j = ceil(k / NT) <= 4), then the ceil(k/j)-th
+  // largest of those over the block
+  const int jj = (k + NT - 1) / NT;
+  uint32_t t4[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    uint32_t x = key[j];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t hi = x > t4[q] ? x : t4[q];
+      const uint32_t lo = x > t4[q] ? t4[q] : x;
+      t4[q] = hi;
+      x = lo;
+    }
+  }
+  const uint32_t aj = jj == 1 ? t4[0] : jj == 2 ? t4[1] : jj == 3 ? t4[2] : t4[3];
+  const unsigned r = (unsigned)((k + jj - 1) / jj);
+  return block_select_kth<uint32_t, 32>([&](auto f) { f(aj); }, r, s);
+}
+
+template <typename Tin>
+__device__ void topk_chunk(const SampleArgs& a, const Row& r, Lds& L, BlockScratch& s) {
+  using TL = Tile<Tin>;
+  const Tin* rowp = (const Tin*)a.logits + (long long)r.b * a.row_stride;
+  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)r.b * a.V : nullptr;
+  const int k = r.k;
+  if (threadIdx.x == 0) s.nbuf = 0;
+  u64 thr = 0;  // candidates: composite >= thr and key != 0
+  uint4 raw[TL::U];
+  uint32_t mw[TL::U];
+  uint32_t key[TL::EPT];
+  bool first = true;
+  for (int t0 = r.v0; t0 < r.v1; t0 += TL::SIZE) {
+    tile_load<Tin>(rowp, r, t0, a.aligned, raw, mw);
+    tile_keys<Tin>(a, r, L, t0, raw, mw, key, post);
+    if (first) {
+      thr = (u64)first_threshold<TL::EPT>(key, k, s) << 32;
+      first = false;
+    }
+    unsigned mine = 0;
+#pragma unroll
+    for (int j = 0; j < TL::EPT; j++)
+      mine += (key[j] && comp_key(key[j], tile_id(t0, j, TL::EPV)) >= thr);
+    const unsigned total = block_sum(mine, s.red32);
+    const unsigned nbuf = s.nbuf;
+    if (nbuf + total > (unsigned)CAPB) {
+      // shrink: exact k-th composite over buffer and this tile's candidates
+      const u64 thr_old = thr;
+      const u64 T = block_select_kth<u64, 64>(
+          [&](auto f) {
+            for (unsigned i = threadIdx.x; i < nbuf; i += NT) f(L.cand[i]);
+#pragma unroll
+            for (int j = 0; j < TL::EPT; j++)
+              if (key[j]) {
+                const u64 c = comp_key(key[j], tile_id(t0, j, TL::EPV));
+                if (c >= thr_old) f(c);
+              }
+          },
+          (unsigned)k, s);
+      compact_ge(L.cand, (int)nbuf, T, s);
+      thr = T;
+      mine = 0;
+#pragma unroll
+      for (int j = 0; j < TL::EPT; j++)
+        mine += (key[j] && comp_key(key[j], tile_id(t0, j, TL::EPV)) >= thr);
+    }
+    // append this thread's candidates
+    {
+      const unsigned incl = wave_incl_scan(mine);
+      unsigned base = 0;
+      if (lane_id() == 63 && incl) base = atomicAdd(&s.nbuf, incl);
+      base = __shfl(base, 63, 64) + incl - mine;
+#pragma unroll
+      for (int j = 0; j < TL::EPT; j++)
+        if (key[j]) {
+          const u64 c = comp_key(key[j], tile_id(t0, j, TL::EPV));
+          if (c >= thr) L.cand[base++] = c;
+        }
+    }
+    __syncthreads();
+  }
+  // history ids with their penalised logits
+  if (r.use_pen) {
+    history_pass<Tin>(a, r, L, rowp, [&](int v, uint32_t kk, float y) {
+      if (post) post[v] = y;
+      if (kk) {
+        const u64 c = comp_key(kk, v);
+        if (c >= thr) L.cand[atomicAdd(&s.nbuf, 1u)] = c;
+      }
+    });
+    __syncthreads();
+  }
+  int n = (int)s.nbuf;
+  __syncthreads();
+  if (n > k) {
+    const u64 T = block_select_kth<u64, 64>(
+        [&](auto f) {
+          for (int i = threadIdx.x; i < n; i += NT) f(L.cand[i]);
+        },
+        (unsigned)k, s);
+    n = compact_ge(L.cand, n, T, s);
+  }
+  if (a.S == 1) {
+    finalize_topk(a, r, L, n, s);
+    return;
+  }
+  // hand the chunk's list to the row's last workgroup
+  u64* dst = a.ws + ((long long)r.b * a.S + r.c) * KMAX;
+  for (int i = threadIdx.x; i < n; i += NT) dst[i] = L.cand[i];
+  if (threadIdx.x == 0) a.ws_cnt[r.b * a.S + r.c] = n;
+  if (!arrive_last(a, r.b, s)) return;
+  // merge
+  int total = 0;
+  for (int c = 0; c < a.S; c++) total += __atomic_load_n(&a.ws_cnt[r.b * a.S + c], __ATOMIC_RELAXED);
+  const int kk = total < k ? total : k;
+  const u64* src = a.ws + (long long)r.b * a.S * KMAX;
+  if (total <= a.capt) {
+    int off = 0;
+    for (int c = 0; c < a.S; c++) {
+      const int cnt = a.ws_cnt[r.b * a.S + c];
+      for (int i = threadIdx.x; i < cnt; i += NT) L.cand[off + i] = src[(long long)c * KMAX + i];
+      off += cnt;
+    }
+    __syncthreads();
+    n = total;
+    if (n > kk) {
+      const u64 T = block_select_kth<u64, 64>(
+          [&](auto f) {
+            for (int i = threadIdx.x; i < n; i += NT) f(L.cand[i]);
+          },
+          (unsigned)kk, s);
+      n = compact_ge(L.cand, n, T, s);
+    }
+  } else {
+    const u64 T = block_select_kth<u64, 64>(
+        [&](auto f) {
+          for (int c = 0; c < a.S; c++) {
+            const int cnt = a.ws_cnt[r.b * a.S + c];
+            for (int i = threadIdx.x; i < cnt; i += NT) f(src[(long long)c * KMAX + i]);
+          }
+        },
+        (unsigned)kk, s);
+    if (threadIdx.x == 0) s.nbuf = 0;
+    __syncthreads();
+    for (int c = 0; c < a.S; c++) {
+      const int cnt = a.ws_cnt[r.b * a.S + c];
+      for (int i = threadIdx.x; i < cnt; i += NT) {
+        const u64 x = src[(long long)c * KMAX + i];
+        if (x >= T) L.cand[atomicAdd(&s.nbuf, 1u)] = x;
+      }
+    }
+    __syncthreads();
+    n = (int)s.nbuf;
+  }
+  finalize_topk(a, r, L, n, s);
+  if (threadIdx.x == 0) a.counters[r.b] = 0u;
+}
+
+// ------------------------------------------------------------------ kernel
+
+__device__ bool row_setup(const SampleArgs& a, int b, int c, Row& r) {
+  const tgs_row_params p = a.params[b];
+  r.b = b;
+  r.c = c;
+  const float T = p.temperature;
+  if (__builtin_isnan(T)) return false;
+  const bool greedy = (p.flags & TGS_FLAG_GREEDY) || T <= 0.0f;
+  r.invT = 1.0f;
+  r.u = 0.0f;
+  if (!greedy) {
+    if (!__builtin_isfinite(T)) return false;
+    r.invT = 1.0f / T;
+    if (!__builtin_isfinite(r.invT)) return false;
+    if (__builtin_isnan(p.top_p) || p.top_p <= 0.0f) return false;
+    r.u = a.u[b];
+    if (__builtin_isnan(r.u) || r.u < 0.0f || r.u >= 1.0f) return false;
+  }
+  if (!(p.repetition > 0.0f) || !__builtin_isfinite(p.repetition)) return false;
+  if (!__builtin_isfinite(p.presence) || !__builtin_isfinite(p.frequency)) return false;
+  r.H = a.hist_len ? a.hist_len[b] : a.hist_cap;
+  if (r.H < 0 || r.H > a.hist_cap) return false;
+  r.hrow = a.hist ? a.hist + (long long)b * a.hist_cap : nullptr;
+  r.mrow = nullptr;
+  if (p.mask_state >= 0) {
+    if (p.mask_state >= a.n_states) return false;
+    r.mrow = a.mask_table + (long long)p.mask_state * a.mask_words;
+  }
+  r.k = p.top_k;
+  r.top_p = p.top_p;
+  r.rep = p.repetition;
+  r.pres = p.presence;
+  r.freq = p.frequency;
+  const bool neutral = (p.repetition == 1.0f && p.presence == 0.0f && p.frequency == 0.0f);
+  r.use_pen = (r.H > 0 && !neutral && r.hrow != nullptr);
+  if (greedy) r.mode = 0;
+  else if (p.top_k >= 1 && p.top_k <= KMAX && p.top_k < a.V) r.mode = 1;
+  else r.mode = 2;
+  return true;
+}
+
+template <typename Tin>
+__global__ __launch_bounds__(NT) void sample_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ BlockScratch s;
+  int b, c;
+  if (a.S == 1) {
+    b = blockIdx.x;
+    c = 0;
+  } else {
+    // all chunks of a row land on one XCD (workgroups round-robin over 8)
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+    b = (j / a.S) * 8 + xcd;
+    c = j % a.S;
+  }
+  if (b >= a.B) return;
+  Row r;
+  if (!row_setup(a, b, c, r)) {
+    if (c == 0 && threadIdx.x == 0) {
+      a.out[b] = -2;
+      if (a.dbg.counts) { a.dbg.counts[2 * b] = 0; a.dbg.counts[2 * b + 1] = 0; }
+      if (a.dbg.mass) { a.dbg.mass[2 * b] = 0; a.dbg.mass[2 * b + 1] = 0; }
+      if (a.dbg.cut_ids) a.dbg.cut_ids[b] = -1;
+    }
+    return;
+  }
+  Lds L;
+  L.hash = (int2*)(smem + a.off_hash);
+  L.bitmap = (uint32_t*)(smem + a.off_bitmap);
+  L.cand = (u64*)(smem + a.off_cand);
+  if (r.mode == 2) {
+    if (c != 0) return;
+    r.v0 = 0;
+    r.v1 = a.V;
+    if (r.use_pen) hash_build(a, r, L, false);  // whole row; lookups per id, no bitmap
+    full_path<Tin>(a, r, L, s);
+    return;
+  }
+  r.v0 = c * a.L;
+  r.v1 = min(a.V, r.v0 + a.L);
+  if (r.use_pen) hash_build(a, r, L, true);
+  if (r.mode == 0) greedy_chunk<Tin>(a, r, L, s);
+  else topk_chunk<Tin>(a, r, L, s);
+}
+
+// ------------------------------------------------------------------ spec verify
+
+template <typename Tin>
+struct SpecTile {
+  static constexpr int EPV = Elem<Tin>::EPV;
+  static constexpr int NV = SPEC_BLOCK / (64 * EPV);  // vectors per lane per block
+  static constexpr int EPL = NV * EPV;                // elements per lane per block
+};
+
+// element id of (vector i, element e) for this lane within block blk
+template <typename Tin>
+__device__ __forceinline__ int spec_id(int blk, int i, int e) {
+  constexpr int EPV = Elem<Tin>::EPV;
+  return blk * SPEC_BLOCK + i * 64 * EPV + lane_id() * EPV + e;
+}
+
+template <typename Tin>
+__device__ __forceinline__ void spec_load_block(const Tin* rowp, int blk, int V, bool aligned,
+                                                float invT, float y[SpecTile<Tin>::EPL]) {
+  using ST = SpecTile<Tin>;
+#pragma unroll
+  for (int i = 0; i < ST::NV; i++) {
+    const int v = spec_id<Tin>(blk, i, 0);
+    const uint4 raw = load_vec<Tin>(rowp, v, V, aligned);
+#pragma unroll
+    for (int e = 0; e < ST::EPV; e++) {
+      const float t = Elem<Tin>::get(raw, e) * invT;
+      y[i * ST::EPV + e] = (t > -__builtin_inff()) ? t : -__builtin_inff();
+    }
+  }
+}
+
+struct SpecScratch {
+  float mb[256];
+  u64 qb[256];
+  u64 argb[NW];
+  u64 wsum[256];
+};
+
+template <typename Tin>
+__device__ const Tin* spec_row_ptr(const SpecArgs& a, int b, int r) {
+  const int k = a.k;
+  if (r <= k) return (const Tin*)a.target + ((long long)b * (k + 1) + r) * a.V;
+  return (const Tin*)a.draft + ((long long)b * k + (r - k - 1)) * a.V;
+}
+
+// Row statistics: writes m, S (canonical) and the argmax composite.
+template <typename Tin>
+__device__ void spec_row_stats(const SpecArgs& a, const Tin* rowp, float invT, bool greedy,
+                               SpecScratch& ss, BlockScratch& s, float* m_out, float* S_out,
+                               u64* arg_out) {
+  using ST = SpecTile<Tin>;
+  const int nb = (a.V + SPEC_BLOCK - 1) / SPEC_BLOCK;
+  const int w = threadIdx.x >> 6;
+  u64 arg = 0;
+  for (int blk = w; blk < nb; blk += NW) {
+    float y[ST::EPL];
+    spec_load_block<Tin>(rowp, blk, a.V, a.aligned, invT, y);
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < ST::EPL; j++) mx = fmaxf(mx, y[j]);
+    mx = wave_maxf(mx);
+    if (greedy) {
+#pragma unroll
+      for (int j = 0; j < ST::EPL; j++)
+        if (y[j] > -__builtin_inff()) {
+          const u64 c = comp_key(tg_key(y[j]), spec_id<Tin>(blk, j / ST::EPV, j % ST::EPV));
+          arg = c > arg ? c : arg;
+        }
+    } else {
+      u64 q = 0;
+      if (mx > -__builtin_inff()) {
+#pragma unroll
+        for (int j = 0; j < ST::EPL; j++)
+          if (y[j] > -__builtin_inff()) q += tg_q40(tg_weight(y[j], mx));
+      }
+      q = wave_sum(q);
+      if (lane_id() == 0) {
+        ss.mb[blk] = mx;
+        ss.qb[blk] = q;
+      }
+    }
+  }
+  arg = block_max(arg, s.red64);
+  *arg_out = arg;
+  if (greedy) {
+    *m_out = 0.0f;
+    *S_out = 0.0f;
+    return;
+  }
+  __syncthreads();
+  // m and the pairwise tree over 256 (zero padded) block terms, in wave 0
+  float m = -__builtin_inff();
+  for (int i = 0; i < nb; i++) m = fmaxf(m, ss.mb[i]);
+  float S = 0.0f;
+  if (threadIdx.x < 64 && m > -__builtin_inff()) {
+    float t[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = 4 * lane_id() + j;
+      float v = 0.0f;
+      if (i < nb && ss.mb[i] > -__builtin_inff())
+        v = (tg_u64_to_f32(ss.qb[i]) * 0x1p-40f) * tg_weight(ss.mb[i], m);
+      t[j] = v;
+    }
+    float x = (t[0] + t[1]) + (t[2] + t[3]);
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) x = x + __shfl_xor(x, d, 64);
+    S = x;
+  }
+  if (threadIdx.x == 0) {
+    *m_out = m;
+    *S_out = S;
+  }
+}
+
+// id-order draw over per-element masses given by wfn(v) (must be identical
+// in both passes).  Returns the first id whose inclusive prefix exceeds
+// floor(total * uq / 2^24); total computed here.
+template <typename Tin, class W>
+__device__ int spec_draw_id_order(const SpecArgs& a, int V, uint32_t uq, W wfn, SpecScratch& ss,
+                                  BlockScratch& s, u64* total_out) {
+  using ST = SpecTile<Tin>;
+  const int nb = (V + SPEC_BLOCK - 1) / SPEC_BLOCK;
+  const int w = threadIdx.x >> 6;
+  for (int blk = w; blk < nb; blk += NW) {
+    u64 q = 0;
+#pragma unroll
+    for (int i = 0; i < ST::NV; i++)
+#pragma unroll
+      for (int e = 0; e < ST::EPV; e++) q += wfn(spec_id<Tin>(blk, i, e));
+    q = wave_sum(q);
+    if (lane_id() == 0) ss.wsum[blk] = q;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = lane_id();
+    u64 vals[4];
+    u64 ls = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = 4 * lane + j;
+      vals[j] = i < nb ? ss.wsum[i] : 0ull;
+      ls += vals[j];
+    }
+    const u64 incl = wave_incl_scan(ls);
+    const u64 total = __shfl(incl, 63, 64);
+    const u64 t = mul_shr24(total, uq);
+    u64 cum = incl - ls;
+    int found = -1;
+    u64 before = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if (found < 0 && cum + vals[j] > t) {
+        found = 4 * lane + j;
+        before = cum;
+      }
+      cum += vals[j];
+    }
+    const u64 bal = __ballot(found >= 0);
+    const int first = bal ? __ffsll((long long)bal) - 1 : -1;
+    if (lane == 0) {
+      s.sel = -1;
+      s.found = total;
+    }
+    if (first >= 0 && lane == first) {
+      s.sel = found;
+      s.mass_above = before;
+      s.need = 0;
+    }
+    if (lane == 0) s.red64[0] = t;
+  }
+  __syncthreads();
+  const int blk = s.sel;
+  *total_out = s.found;
+  if (blk < 0) return -1;
+  const u64 t = s.red64[0];
+  const u64 before = s.mass_above;
+  // scan the chosen block in id order (wave 0)
+  if (threadIdx.x < 64) {
+    u64 run = before;
+    int pick = -1;
+    for (int i = 0; i < ST::NV && pick < 0; i++) {
+      u64 ws[ST::EPV];
+      u64 ls = 0;
+#pragma unroll
+      for (int e = 0; e < ST::EPV; e++) {
+        ws[e] = wfn(spec_id<Tin>(blk, i, e));
+        ls += ws[e];
+      }
+      const u64 incl = wave_incl_scan(ls);
+      u64 cum = run + incl - ls;
+      int mine = -1;
+#pragma unroll
+      for (int e = 0; e < ST::EPV; e++) {
+        if (mine < 0 && cum + ws[e] > t) mine = spec_id<Tin>(blk, i, e);
+        cum += ws[e];
+      }
+      const u64 bal = __ballot(mine >= 0);
+      if (bal) {
+        const int first = __ffsll((long long)bal) - 1;
+        pick = __shfl(mine, first, 64);
+      }
+      run += __shfl(incl, 63, 64);
+    }
+    if (lane_id() == 0) s.imin0 = pick;
+  }
+  __syncthreads();
+  return s.imin0;
+}
+
+template <typename Tin>
+__global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
+  __shared__ BlockScratch s;
+  __shared__ SpecScratch ss;
+  const int R = 2 * a.k + 1;
+  const int b = blockIdx.x / R, r = blockIdx.x % R;
+  if (b >= a.B) return;
+  const float T = a.T[b];
+  const bool greedy = !(T > 0.0f);  // NaN handled in the verify step
+  const float Tc = T > 1e-5f ? T : 1e-5f;
+  const float invT = greedy ? 1.0f : 1.0f / Tc;
+  float* stat = a.ws_stats + ((long long)b * R + r) * 2;
+  u64* argp = a.ws_arg + (long long)b * R + r;
+  if (!(greedy && r > a.k) && !__builtin_isnan(T)) {
+    float m, S;
+    u64 arg;
+    spec_row_stats<Tin>(a, spec_row_ptr<Tin>(a, b, r), invT, greedy, ss, s, &m, &S, &arg);
+    if (threadIdx.x == 0) {
+      stat[0] = m;
+      stat[1] = S;
+      *argp = arg;
+    }
+  }
+  // handoff to the last workgroup of sequence b
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = atomicAdd(&a.counters[b], 1u);
+    s.last = (prev == (unsigned)R - 1u);
+  }
+  __syncthreads();
+  if (!s.last) return;
+  __threadfence();
+  const int k = a.k;
+  int* out = a.out + (long long)b * (k + 1);
+  const float* stats = a.ws_stats + (long long)b * R * 2;
+  const u64* args = a.ws_arg + (long long)b * R;
+  // validation (same rules as the CPU restatement)
+  bool bad = __builtin_isnan(T) || (!greedy && !(invT > 0.0f && __builtin_isfinite(invT)));
+  for (int j = 0; j < k; j++) {
+    const int d = a.dtok[(long long)b * k + j];
+    if (d < 0 || d >= a.V) bad = true;
+    if (!greedy) {
+      const float ua = a.u_acc[(long long)b * k + j];
+      if (__builtin_isnan(ua) || ua < 0.0f || ua >= 1.0f) bad = true;
+    }
+  }
+  const float ur = a.u_res[b];
+  if (!greedy && (__builtin_isnan(ur) || ur < 0.0f || ur >= 1.0f)) bad = true;
+  if (bad) {
+    for (int j = threadIdx.x; j <= k; j += NT) out[j] = j == 0 ? -2 : -1;
+    if (threadIdx.x == 0) a.n_acc[b] = -1;
+    if (threadIdx.x == 0) a.counters[b] = 0u;
+    return;
+  }
+  if (greedy) {
+    if (threadIdx.x == 0) {
+      int j;
+      for (j = 0; j <= k; j++) out[j] = -1;
+      for (j = 0; j < k; j++) {
+        const u64 c = args[j];
+        const int am = c ? comp_id(c) : -1;
+        out[j] = am;
+        if (am != a.dtok[(long long)b * k + j]) break;
+      }
+      if (j == k) out[k] = args[k] ? comp_id(args[k]) : -1;
+      a.n_acc[b] = j;
+      a.counters[b] = 0u;
+    }
+    return;
+  }
+  // stochastic accept/reject scan (thread 0), then the draw (whole block)
+  if (threadIdx.x == 0) {
+    int j;
+    int status = 0;  // 0 all accepted, 1 rejected at j, -1 empty row
+    for (j = 0; j <= k; j++) out[j] = -1;
+    for (j = 0; j < k; j++) {
+      const float mt = stats[2 * j], St = stats[2 * j + 1];
+      const float md = stats[2 * (k + 1 + j)], Sd = stats[2 * (k + 1 + j) + 1];
+      if (!(St > 0.0f) || !(Sd > 0.0f)) {
+        status = -1;
+        break;
+      }
+      const int d = a.dtok[(long long)b * k + j];
+      const Tin* tr = spec_row_ptr<Tin>(a, b, j);
+      const Tin* dr = spec_row_ptr<Tin>(a, b, k + 1 + j);
+      float yt = Elem<Tin>::scalar(tr, d) * invT;
+      float yd = Elem<Tin>::scalar(dr, d) * invT;
+      if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
+      if (!(yd > -__builtin_inff())) yd = -__builtin_inff();
+      const float pt = tg_weight(yt, mt) / St;
+      const float pd = tg_weight(yd, md) / Sd;
+      const float ratio = pt / fmaxf(pd, 1e-10f);
+      if (a.u_acc[(long long)b * k + j] < ratio) {
+        out[j] = d;
+        continue;
+      }
+      status = 1;
+      break;
+    }
+    if (status == 0) {
+      const float St = stats[2 * k + 1];
+      if (!(St > 0.0f)) status = -1;
+    }
+    s.sel = status;
+    s.binc_i = j;
+  }
+  __syncthreads();
+  const int status = s.sel, j = s.binc_i;
+  if (status < 0) {
+    if (threadIdx.x == 0) {
+      for (int i = 0; i <= k; i++) out[i] = -1;
+      a.n_acc[b] = -1;
+      a.counters[b] = 0u;
+    }
+    return;
+  }
+  const uint32_t uq = (uint32_t)(ur * 16777216.0f);
+  int pick;
+  if (status == 1) {
+    const float mt = stats[2 * j], St = stats[2 * j + 1];
+    const float md = stats[2 * (k + 1 + j)], Sd = stats[2 * (k + 1 + j) + 1];
+    const Tin* tr = spec_row_ptr<Tin>(a, b, j);
+    const Tin* dr = spec_row_ptr<Tin>(a, b, k + 1 + j);
+    const int V = a.V;
+    auto resid = [&](int v) -> u64 {
+      if (v >= V) return 0ull;
+      float yt = Elem<Tin>::scalar(tr, v) * invT;
+      float yd = Elem<Tin>::scalar(dr, v) * invT;
+      if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
+      if (!(yd > -__builtin_inff())) yd = -__builtin_inff();
+      const float pa = tg_weight(yt, mt) / St;
+      const float pb = tg_weight(yd, md) / Sd;
+      return tg_q40(fmaxf(pa - pb, 0.0f));
+    };
+    u64 R;
+    pick = spec_draw_id_order<Tin>(a, V, uq, resid, ss, s, &R);
+    if (R < 110ull) {
+      auto wt = [&](int v) -> u64 {
+        if (v >= V) return 0ull;
+        float yt = Elem<Tin>::scalar(tr, v) * invT;
+        if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
+        return tg_q40(tg_weight(yt, mt));
+      };
+      __syncthreads();
+      u64 Sq;
+      pick = spec_draw_id_order<Tin>(a, V, uq, wt, ss, s, &Sq);
+    }
+  } else {
+    const float mt = stats[2 * k];
+    const Tin* tr = spec_row_ptr<Tin>(a, b, k);
+    const int V = a.V;
+    auto wt = [&](int v) -> u64 {
+      if (v >= V) return 0ull;
+      float yt = Elem<Tin>::scalar(tr, v) * invT;
+      if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
+      return tg_q40(tg_weight(yt, mt));
+    };
+    u64 Sq;
+    pick = spec_draw_id_order<Tin>(a, V, uq, wt, ss, s, &Sq);
+  }
+  if (threadIdx.x == 0) {
+    out[j] = pick;
+    a.n_acc[b] = j;
+    a.counters[b] = 0u;
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+
+template <typename Tin>
+static hipError_t launch_sample_t(const SampleArgs& a, int grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL(sample_kernel<Tin>, dim3(grid), dim3(NT), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sample(const SampleArgs& a, int dtype, int grid, size_t lds, hipStream_t st) {
+  return dtype == 1 ? launch_sample_t<uint16_t>(a, grid, lds, st) : launch_sample_t<float>(a, grid, lds, st);
+}
+
+hipError_t set_sample_lds_limit(size_t bytes) {
+  hipError_t e = hipFuncSetAttribute((const void*)sample_kernel<float>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute((const void*)sample_kernel<uint16_t>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st) {
+  const int grid = a.B * (2 * a.k + 1);
+  if (dtype == 1) hipLaunchKernelGGL(spec_kernel<uint16_t>, dim3(grid), dim3(NT), 0, st, a);
+  else hipLaunchKernelGGL(spec_kernel<float>, dim3(grid), dim3(NT), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace tgs

@@ -1,0 +1,161 @@
+"""Device-side sampler handle over the C ABI (torch tensors in, torch out).
+
+`Sampler` owns one `tgs_handle`.  Inputs are torch tensors already on the
+handle's device; the call is asynchronous on torch's current stream (or the
+stream given).  torch provides device memory and streams only; all sampling
+arithmetic runs in the HIP kernels of libtgs_sampler.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import ROW_PARAMS_DTYPE, TGS_BF16, TGS_F32, TgsDebug, TgsError
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def make_params(n, temperature=1.0, top_k=0, top_p=1.0, repetition=1.0, presence=0.0,
+                frequency=0.0, mask_state=-1, flags=0) -> np.ndarray:
+    """Structured numpy array of tgs_row_params (broadcasts scalars/arrays)."""
+    p = np.zeros(n, dtype=ROW_PARAMS_DTYPE)
+    p["temperature"] = temperature
+    p["top_k"] = top_k
+    p["top_p"] = top_p
+    p["repetition"] = repetition
+    p["presence"] = presence
+    p["frequency"] = frequency
+    p["mask_state"] = mask_state
+    p["flags"] = flags
+    return p
+
+
+def params_to_device(params: np.ndarray, device):
+    torch = _torch()
+    raw = np.ascontiguousarray(params, dtype=ROW_PARAMS_DTYPE).view(np.uint8)
+    return torch.from_numpy(raw.copy()).to(device)
+
+
+class Sampler:
+    """One sampler handle on one GPU.
+
+    max_batch / max_vocab / max_hist bound every call; the workspace is
+    allocated once here.
+    """
+
+    def __init__(self, device: int = 0, max_batch: int = 1024, max_vocab: int = 152064,
+                 max_hist: int = 1024):
+        self._L = _lib.load()
+        self.device = device
+        h = C.c_void_p()
+        rc = self._L.tgs_create(C.byref(h), device, max_batch, max_vocab, max_hist)
+        if rc != 0:
+            raise TgsError(rc, f"tgs_create failed: {_lib.status_string(rc)}")
+        self._h = h
+        self.max_batch, self.max_vocab, self.max_hist = max_batch, max_vocab, max_hist
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._L.tgs_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc != 0:
+            msg = self._L.tgs_last_error(self._h).decode()
+            raise TgsError(rc, f"{what}: {msg}")
+
+    # ---------------------------------------------------------------- mask
+    def set_mask_table(self, words: np.ndarray, vocab: int):
+        words = np.ascontiguousarray(words, dtype=np.uint32)
+        n_states = words.shape[0] if words.size else 0
+        rc = self._L.tgs_mask_table_set(self._h, words.ctypes.data_as(C.c_void_p), n_states, vocab)
+        self._check(rc, "tgs_mask_table_set")
+
+    def update_mask_rows(self, states: np.ndarray, words: np.ndarray):
+        states = np.ascontiguousarray(states, dtype=np.int32)
+        words = np.ascontiguousarray(words, dtype=np.uint32)
+        rc = self._L.tgs_mask_table_update(self._h, states.ctypes.data_as(C.c_void_p),
+                                           words.ctypes.data_as(C.c_void_p), states.size)
+        self._check(rc, "tgs_mask_table_update")
+
+    # -------------------------------------------------------------- sample
+    def sample(self, logits, params_dev, u, hist=None, hist_len=None, out=None, vocab=None,
+               debug=None, stream=None):
+        """logits: [B, >=V] float32 or bfloat16 (row stride = logits.stride(0));
+        params_dev: uint8 tensor of B*32 bytes (see params_to_device);
+        u: float32 [B]; hist: int32 [B, hist_cap]; hist_len: int32 [B].
+        debug: dict of preallocated tensors (kept_ids, kept_probs, counts,
+        mass, cut_ids, post_logits).  Returns the int32 [B] ids tensor."""
+        torch = _torch()
+        if logits.dim() != 2 or logits.stride(1) != 1:
+            raise ValueError("logits must be [B, V] with unit stride along V")
+        B = logits.shape[0]
+        V = logits.shape[1] if vocab is None else vocab
+        if logits.dtype == torch.float32:
+            dt = TGS_F32
+        elif logits.dtype == torch.bfloat16:
+            dt = TGS_BF16
+        else:
+            raise TypeError("logits must be float32 or bfloat16")
+        if out is None:
+            out = torch.empty(B, dtype=torch.int32, device=logits.device)
+        hist_cap = 0 if hist is None else hist.shape[1]
+        dbg = None
+        if debug:
+            dbg = TgsDebug()
+            for name in ("kept_ids", "kept_probs", "counts", "mass", "cut_ids", "post_logits"):
+                t = debug.get(name)
+                setattr(dbg, name, None if t is None else t.data_ptr())
+            kc = debug.get("kept_ids", debug.get("kept_probs"))
+            dbg.kept_cap = 0 if kc is None else kc.shape[1]
+        st = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
+        rc = self._L.tgs_sample(
+            self._h, _ptr(logits), dt, B, V, logits.stride(0), _ptr(hist), _ptr(hist_len), hist_cap,
+            _ptr(params_dev), _ptr(u), _ptr(out), C.byref(dbg) if dbg is not None else None,
+            C.c_void_p(st),
+        )
+        self._check(rc, "tgs_sample")
+        return out
+
+    # -------------------------------------------------------------- spec
+    def reserve_spec(self, max_batch: int, max_k: int):
+        self._check(self._L.tgs_reserve_spec(self._h, max_batch, max_k), "tgs_reserve_spec")
+
+    def spec_verify(self, target, draft, draft_tok, T, u_acc, u_res, n_acc=None, out=None,
+                    stream=None):
+        """target [B, k+1, V], draft [B, k, V] (float32 or bfloat16, contiguous);
+        draft_tok int32 [B, k]; T float32 [B]; u_acc float32 [B, k]; u_res [B].
+        Returns (n_acc int32 [B], out int32 [B, k+1])."""
+        torch = _torch()
+        B, k1, V = target.shape
+        k = k1 - 1
+        dt = TGS_BF16 if target.dtype == torch.bfloat16 else TGS_F32
+        if not target.is_contiguous() or not draft.is_contiguous():
+            raise ValueError("target and draft must be contiguous")
+        if n_acc is None:
+            n_acc = torch.empty(B, dtype=torch.int32, device=target.device)
+        if out is None:
+            out = torch.empty(B, k + 1, dtype=torch.int32, device=target.device)
+        st = stream if stream is not None else torch.cuda.current_stream(target.device).cuda_stream
+        rc = self._L.tgs_spec_verify(
+            self._h, _ptr(target), _ptr(draft), dt, _ptr(draft_tok), B, k, V, _ptr(T), _ptr(u_acc),
+            _ptr(u_res), _ptr(n_acc), _ptr(out), C.c_void_p(st),
+        )
+        self._check(rc, "tgs_spec_verify")
+        return n_acc, out
