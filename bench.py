@@ -110,10 +110,12 @@ def main():
 
     stream = torch.cuda.Stream(device=dev)  # default priority
 
+    hints = [tg.batch_hint(s["params"], V) for s in sets]
+
     def launch(i):
         x = d[i % ROT]
         sampler.sample(x["logits"], x["params"], x["u"], hist=x["hist"], hist_len=x["hist_len"],
-                       out=x["out"], stream=stream.cuda_stream)
+                       out=x["out"], stream=stream.cuda_stream, hint=hints[i % ROT])
 
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
@@ -188,7 +190,7 @@ def main():
                    "rotating_buffers": ROT, "timing": "graph replay" if graph is not None else "eager"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "alg_bytes_per_launch": alg_bytes, "kernel": "sample_kernel<float>"},
+                     "alg_bytes_per_launch": alg_bytes, "kernel": "fast_kernel<float> + merge_kernel"},
         "cpu_baseline": cpu,
         "id_agreement": agreement,
     }

@@ -24,6 +24,7 @@
  *     id >= 0   sampled token
  *     id == -1  no token is allowed (all masked / -inf / NaN)   [TGS_EALLMASKED]
  *     id == -2  invalid row parameters (see tgs_row_params)
+ *     id == -3  row outside the tgs_batch_hint given to the call
  *
  * Reference interfaces replaced (paths under the reference repository):
  *   tgs_sample       <- Server.sampleToken(from:temperature:constraint:)
@@ -92,9 +93,25 @@ typedef struct {
   float* post_logits;  /* [B][V] logit after penalties, mask (-inf) and temperature       */
 } tgs_debug;
 
+/* Host-side summary of a batch's row parameters.  It selects kernels
+ * specialised for the batch: max_top_k <= 64 -> one-tile chunks merged in
+ * wave registers; <= 1024 -> candidate path; otherwise (or no hint) the
+ * candidate path plus the full-path kernel for rows without a usable top-k.
+ * The hint is a promise: a sampling row whose top_k exceeds max_top_k (a
+ * row without a usable top-k counts as V) gets id -3.  Greedy rows are
+ * served under any hint. */
+typedef struct {
+  int32_t max_top_k; /* max over sampling rows of top_k when 1 <= top_k < V, else V;
+                        0 when every row is greedy */
+} tgs_batch_hint;
+
 /* Library / status helpers (no device work). */
 int tgs_abi_version(void);
 const char* tgs_status_string(int status);
+
+/* Fill *out from host copies of the row parameters (greedy rows: flag set or
+ * temperature <= 0 or NaN). */
+int tgs_hint_from_params(const tgs_row_params* host_params, int B, int V, tgs_batch_hint* out);
 
 /* Create a sampler on `device`.  max_batch, max_vocab and max_hist bound
  * every later call (workspace is sized once here; calls never allocate). */
@@ -117,11 +134,12 @@ int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32
  *   d_params    [B] tgs_row_params
  *   d_u         [B] uniforms in [0,1) (ignored by greedy rows)
  *   d_out_ids   [B] output ids (see the id codes above)
+ *   hint        nullable host struct (see tgs_batch_hint)
  *   dbg         nullable diagnostics */
 int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
                const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
                const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids,
-               const tgs_debug* dbg, tgs_stream stream);
+               const tgs_batch_hint* hint, const tgs_debug* dbg, tgs_stream stream);
 
 /* Size the speculative-verification workspace for up to max_batch sequences
  * of up to max_k draft tokens (allocates; call once before capturing

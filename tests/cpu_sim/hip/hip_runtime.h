@@ -1,0 +1,227 @@
+// hip_runtime.h (CPU simulation) -- runs the sampler's HIP kernels on host
+// threads so that their memory accesses can be checked with AddressSanitizer
+// and debugged with gdb.  TEST INFRASTRUCTURE ONLY, never part of the product.
+//
+// Model: a launch runs its blocks one after another; a block is blockDim.x
+// OS threads.  __syncthreads is a barrier over the block's threads; wave
+// intrinsics (__shfl*, __ballot) exchange values among the 64 threads of a
+// wave through a per-wave buffer between two barriers.  A thread leaving
+// the kernel drops out of its barriers (exited waves do not take part in
+// later barriers on the GPU either).  __shared__ variables are static:
+// blocks never run concurrently, so one instance per kernel suffices.
+// Device memory is host memory.
+#pragma once
+
+#include <barrier>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <memory>
+#include <thread>
+#include <type_traits>
+#include <vector>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __noinline__ __attribute__((noinline))
+#define __launch_bounds__(...)
+// Static LDS variables live in one linker section so that every block can
+// start with it poisoned (LDS holds garbage at kernel start on the GPU).
+#define __shared__ static __attribute__((section("tgs_lds")))
+extern "C" unsigned char __start_tgs_lds[], __stop_tgs_lds[];
+#define __align__(x) alignas(x)
+#define TGS_DYN_SMEM(name) unsigned char* name = hipcpu::dyn_smem()
+
+struct dim3 {
+  unsigned x, y, z;
+  dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+struct uint4 {
+  uint32_t x, y, z, w;
+};
+struct int2 {
+  int x, y;
+};
+static inline uint4 make_uint4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) { return {a, b, c, d}; }
+static inline int2 make_int2(int a, int b) { return {a, b}; }
+
+typedef int hipError_t;
+typedef struct ihipStream_t* hipStream_t;
+enum {
+  hipSuccess = 0,
+  hipErrorOutOfMemory = 2,
+  hipErrorInvalidValue = 1,
+  hipMemcpyHostToDevice = 1,
+  hipMemcpyDeviceToHost = 2,
+  hipDeviceAttributeMultiprocessorCount = 1,
+  hipDeviceAttributeMaxSharedMemoryPerBlock = 2,
+  hipFuncAttributeMaxDynamicSharedMemorySize = 3,
+};
+
+namespace hipcpu {
+
+struct WaveCtx {
+  std::unique_ptr<std::barrier<>> bar;
+  uint64_t buf[64];
+};
+struct BlockCtx {
+  std::unique_ptr<std::barrier<>> bar;
+  std::vector<WaveCtx> waves;
+  std::vector<unsigned char> smem;
+};
+inline BlockCtx*& block_ctx() {
+  static BlockCtx* b = nullptr;
+  return b;
+}
+inline thread_local dim3 t_thread, t_block;
+inline dim3 g_block_dim, g_grid_dim;
+inline unsigned char* dyn_smem() { return block_ctx()->smem.data(); }
+
+inline int lane() { return (int)(t_thread.x & 63); }
+inline WaveCtx& wave() { return block_ctx()->waves[t_thread.x / 64]; }
+
+template <typename T>
+inline uint64_t to_bits(T x) {
+  uint64_t u = 0;
+  std::memcpy(&u, &x, sizeof(T));
+  return u;
+}
+template <typename T>
+inline T from_bits(uint64_t u) {
+  T x;
+  std::memcpy(&x, &u, sizeof(T));
+  return x;
+}
+template <typename T>
+inline T exchange(T x, int src) {
+  WaveCtx& w = wave();
+  w.buf[lane()] = to_bits(x);
+  w.bar->arrive_and_wait();
+  const uint64_t r = (src >= 0 && src < 64) ? w.buf[src] : w.buf[lane()];
+  w.bar->arrive_and_wait();
+  return from_bits<T>(r);
+}
+
+template <typename... Args>
+inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args... args) {
+  g_grid_dim = grid;
+  g_block_dim = block;
+  const unsigned nt = block.x;
+  for (unsigned bx = 0; bx < grid.x; bx++) {
+    BlockCtx ctx;
+    ctx.bar = std::make_unique<std::barrier<>>(nt);
+    ctx.waves.resize((nt + 63) / 64);
+    for (unsigned w = 0; w < ctx.waves.size(); w++) {
+      const unsigned n = std::min(64u, nt - 64 * w);
+      ctx.waves[w].bar = std::make_unique<std::barrier<>>(n);
+    }
+    ctx.smem.assign(shmem ? shmem : 1, 0xA5);
+    std::memset(__start_tgs_lds, 0xA5, (size_t)(__stop_tgs_lds - __start_tgs_lds));
+    block_ctx() = &ctx;
+    std::vector<std::thread> th;
+    th.reserve(nt);
+    for (unsigned t = 0; t < nt; t++)
+      th.emplace_back([&, t]() {
+        t_thread = dim3(t);
+        t_block = dim3(bx);
+        k(args...);
+        ctx.waves[t / 64].bar->arrive_and_drop();
+        ctx.bar->arrive_and_drop();
+      });
+    for (auto& x : th) x.join();
+    block_ctx() = nullptr;
+  }
+}
+
+}  // namespace hipcpu
+
+#define threadIdx (hipcpu::t_thread)
+#define blockIdx (hipcpu::t_block)
+#define blockDim (hipcpu::g_block_dim)
+#define gridDim (hipcpu::g_grid_dim)
+
+#define hipLaunchKernelGGL(k, g, b, sh, st, ...) hipcpu::launch(k, dim3(g), dim3(b), (size_t)(sh), __VA_ARGS__)
+
+inline void __syncthreads() { hipcpu::block_ctx()->bar->arrive_and_wait(); }
+inline int __lane_id() { return hipcpu::lane(); }
+
+template <typename T>
+inline T __shfl(T x, int src, int width = 64) { (void)width; return hipcpu::exchange(x, src); }
+template <typename T>
+inline T __shfl_xor(T x, int m, int width = 64) { (void)width; return hipcpu::exchange(x, hipcpu::lane() ^ m); }
+template <typename T>
+inline T __shfl_up(T x, int d, int width = 64) {
+  (void)width;
+  const int s = hipcpu::lane() - d;
+  return hipcpu::exchange(x, s < 0 ? hipcpu::lane() : s);
+}
+inline unsigned long long __ballot(int pred) {
+  hipcpu::WaveCtx& w = hipcpu::wave();
+  w.buf[hipcpu::lane()] = pred ? 1u : 0u;
+  w.bar->arrive_and_wait();
+  unsigned long long m = 0;
+  for (int i = 0; i < 64; i++)
+    if (w.buf[i]) m |= 1ull << i;
+  w.bar->arrive_and_wait();
+  return m;
+}
+
+inline int min(int a, int b) { return a < b ? a : b; }
+inline int max(int a, int b) { return a > b ? a : b; }
+inline unsigned min(unsigned a, unsigned b) { return a < b ? a : b; }
+inline unsigned max(unsigned a, unsigned b) { return a > b ? a : b; }
+inline long long min(long long a, long long b) { return a < b ? a : b; }
+inline long long max(long long a, long long b) { return a > b ? a : b; }
+
+inline int __popc(unsigned x) { return __builtin_popcount(x); }
+inline int __ffsll(long long x) { return __builtin_ffsll(x); }
+inline int __clzll(long long x) { return x ? __builtin_clzll((unsigned long long)x) : 64; }
+inline unsigned long long __umul64hi(unsigned long long a, unsigned long long b) {
+  return (unsigned long long)(((unsigned __int128)a * b) >> 64);
+}
+inline float __uint_as_float(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
+inline uint32_t __float_as_uint(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
+
+template <typename T, typename U>
+inline T atomicAdd(T* p, U v) { return __atomic_fetch_add(p, (T)v, __ATOMIC_SEQ_CST); }
+inline int atomicCAS(int* p, int cmp, int val) {
+  __atomic_compare_exchange_n(p, &cmp, val, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST);
+  return cmp;
+}
+inline unsigned atomicOr(unsigned* p, unsigned v) { return __atomic_fetch_or(p, v, __ATOMIC_SEQ_CST); }
+inline int atomicMin(int* p, int v) {
+  int cur = __atomic_load_n(p, __ATOMIC_SEQ_CST);
+  while (v < cur && !__atomic_compare_exchange_n(p, &cur, v, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST)) {
+  }
+  return cur;
+}
+
+// ---- runtime API on host memory ----
+inline int& hipcpu_last_error() {
+  static int e = 0;
+  return e;
+}
+inline hipError_t hipGetLastError() { int e = hipcpu_last_error(); hipcpu_last_error() = 0; return e; }
+inline const char* hipGetErrorString(hipError_t e) { return e ? "hipcpu error" : "no error"; }
+template <typename T>
+inline hipError_t hipMalloc(T** p, size_t n) {
+  *p = (T*)std::malloc(n ? n : 1);
+  return *p ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipFree(void* p) { std::free(p); return hipSuccess; }
+inline hipError_t hipMemset(void* p, int v, size_t n) { std::memset(p, v, n); return hipSuccess; }
+inline hipError_t hipMemcpy(void* d, const void* s, size_t n, int) { std::memcpy(d, s, n); return hipSuccess; }
+inline hipError_t hipDeviceSynchronize() { return hipSuccess; }
+inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
+inline hipError_t hipSetDevice(int) { return hipSuccess; }
+inline hipError_t hipGetDeviceCount(int* n) { *n = 1; return hipSuccess; }
+inline hipError_t hipDeviceGetAttribute(int* v, int attr, int) {
+  *v = attr == hipDeviceAttributeMultiprocessorCount ? 256 : 163840;
+  return hipSuccess;
+}
+inline hipError_t hipFuncSetAttribute(const void*, int, int) { return hipSuccess; }

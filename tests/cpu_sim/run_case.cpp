@@ -1,0 +1,100 @@
+// run_case.cpp -- drives tgs_sample / tgs_spec_verify through the C ABI on the
+// CPU simulation of the kernels (TEST INFRASTRUCTURE ONLY).
+//   run_case sample <dir>   reads <dir>/meta.txt and the raw input arrays,
+//                           writes the outputs next to them.
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+#include "../../include/tgs_sampler.h"
+
+static std::vector<char> slurp(const std::string& path) {
+  std::vector<char> v;
+  FILE* f = std::fopen(path.c_str(), "rb");
+  if (!f) return v;
+  std::fseek(f, 0, SEEK_END);
+  long n = std::ftell(f);
+  std::fseek(f, 0, SEEK_SET);
+  v.resize(n);
+  if (n && std::fread(v.data(), 1, n, f) != (size_t)n) v.clear();
+  std::fclose(f);
+  return v;
+}
+static void dump(const std::string& path, const void* p, size_t n) {
+  FILE* f = std::fopen(path.c_str(), "wb");
+  std::fwrite(p, 1, n, f);
+  std::fclose(f);
+}
+
+int main(int argc, char** argv) {
+  if (argc < 3) return 2;
+  const std::string mode = argv[1], dir = argv[2];
+  FILE* m = std::fopen((dir + "/meta.txt").c_str(), "r");
+  if (!m) return 3;
+  if (mode == "sample") {
+    int B, V, dtype, hist_cap, has_len, n_states, hint, kept_cap, post;
+    long long stride;
+    if (std::fscanf(m, "%d %d %lld %d %d %d %d %d %d %d", &B, &V, &stride, &dtype, &hist_cap, &has_len,
+                    &n_states, &hint, &kept_cap, &post) != 10)
+      return 4;
+    std::fclose(m);
+    auto logits = slurp(dir + "/logits.bin");
+    auto params = slurp(dir + "/params.bin");
+    auto u = slurp(dir + "/u.bin");
+    auto hist = slurp(dir + "/hist.bin");
+    auto hlen = slurp(dir + "/hist_len.bin");
+    auto mask = slurp(dir + "/mask.bin");
+    tgs_handle h;
+    int rc = tgs_create(&h, 0, B > 0 ? B : 1, V, hist_cap);
+    if (rc) { std::printf("create %d\n", rc); return 5; }
+    if (n_states > 0) {
+      rc = tgs_mask_table_set(h, (const uint32_t*)mask.data(), n_states, V);
+      if (rc) { std::printf("mask %d\n", rc); return 6; }
+    }
+    std::vector<int32_t> out(B), kid((size_t)B * kept_cap), counts(2 * (size_t)B), cut(B);
+    std::vector<float> kpr((size_t)B * kept_cap), postv(post ? (size_t)B * V : 1);
+    std::vector<uint64_t> mass(2 * (size_t)B);
+    tgs_debug dbg = {kid.data(), kpr.data(), kept_cap, counts.data(), mass.data(), cut.data(),
+                     post ? postv.data() : nullptr};
+    tgs_batch_hint hb = {hint};
+    rc = tgs_sample(h, logits.data(), (tgs_dtype)dtype, B, V, stride, hist_cap ? (const int32_t*)hist.data() : nullptr,
+                    has_len ? (const int32_t*)hlen.data() : nullptr, hist_cap, (const tgs_row_params*)params.data(),
+                    (const float*)u.data(), out.data(), hint >= 0 ? &hb : nullptr, &dbg, nullptr);
+    if (rc) { std::printf("sample %d %s\n", rc, tgs_last_error(h)); return 7; }
+    dump(dir + "/out_ids.bin", out.data(), out.size() * 4);
+    dump(dir + "/out_kept_ids.bin", kid.data(), kid.size() * 4);
+    dump(dir + "/out_kept_probs.bin", kpr.data(), kpr.size() * 4);
+    dump(dir + "/out_counts.bin", counts.data(), counts.size() * 4);
+    dump(dir + "/out_mass.bin", mass.data(), mass.size() * 8);
+    dump(dir + "/out_cut.bin", cut.data(), cut.size() * 4);
+    if (post) dump(dir + "/out_post.bin", postv.data(), postv.size() * 4);
+    tgs_destroy(h);
+    return 0;
+  }
+  if (mode == "spec") {
+    int B, k, V, dtype;
+    if (std::fscanf(m, "%d %d %d %d", &B, &k, &V, &dtype) != 4) return 4;
+    std::fclose(m);
+    auto tgt = slurp(dir + "/target.bin");
+    auto dft = slurp(dir + "/draft.bin");
+    auto dtok = slurp(dir + "/dtok.bin");
+    auto T = slurp(dir + "/T.bin");
+    auto ua = slurp(dir + "/u_acc.bin");
+    auto ur = slurp(dir + "/u_res.bin");
+    tgs_handle h;
+    int rc = tgs_create(&h, 0, B, V, 0);
+    if (rc) return 5;
+    std::vector<int32_t> nacc(B), out((size_t)B * (k + 1));
+    rc = tgs_spec_verify(h, tgt.data(), dft.data(), (tgs_dtype)dtype, (const int32_t*)dtok.data(), B, k, V,
+                         (const float*)T.data(), (const float*)ua.data(), (const float*)ur.data(), nacc.data(),
+                         out.data(), nullptr);
+    if (rc) { std::printf("spec %d %s\n", rc, tgs_last_error(h)); return 7; }
+    dump(dir + "/out_nacc.bin", nacc.data(), nacc.size() * 4);
+    dump(dir + "/out_spec.bin", out.data(), out.size() * 4);
+    tgs_destroy(h);
+    return 0;
+  }
+  return 2;
+}

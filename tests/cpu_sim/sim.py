@@ -1,0 +1,61 @@
+"""Runs tgs_sample through the CPU simulation of the kernels (built by the
+Makefile beside this file, under AddressSanitizer) and returns the same
+outputs as the GPU harness.  TEST INFRASTRUCTURE ONLY: a debugging aid for
+kernel memory errors, never part of the product path."""
+from __future__ import annotations
+
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+BIN = os.environ.get("TGS_SIM_BIN", os.path.join(HERE, "build", "run_case"))
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=None, kept_cap=64,
+               post=True, hint=None, split=None, timeout=600):
+    """hint: None (general kernel) or an int max_top_k."""
+    B = logits.shape[0]
+    V = logits.shape[1] if V is None else V
+    dtype = 1 if logits.dtype == np.uint16 else 0
+    hist_cap = 0 if hist is None else hist.shape[1]
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        np.ascontiguousarray(logits).tofile(os.path.join(d, "logits.bin"))
+        np.ascontiguousarray(params).tofile(os.path.join(d, "params.bin"))
+        np.asarray(u, np.float32).tofile(os.path.join(d, "u.bin"))
+        if hist is not None:
+            np.ascontiguousarray(hist, np.int32).tofile(os.path.join(d, "hist.bin"))
+        if hist_len is not None:
+            np.ascontiguousarray(hist_len, np.int32).tofile(os.path.join(d, "hist_len.bin"))
+        n_states = 0
+        if mask_table is not None:
+            n_states = mask_table.shape[0]
+            np.ascontiguousarray(mask_table, np.uint32).tofile(os.path.join(d, "mask.bin"))
+        with open(os.path.join(d, "meta.txt"), "w") as f:
+            f.write(f"{B} {V} {logits.shape[1]} {dtype} {hist_cap} {int(hist_len is not None)} {n_states} "
+                    f"{-1 if hint is None else int(hint)} {kept_cap} {int(bool(post))}\n")
+        env = dict(os.environ)
+        if split is not None:
+            env["TGS_SPLIT"] = str(split)
+        env.setdefault("ASAN_OPTIONS", "detect_leaks=0:abort_on_error=0")
+        env.setdefault("UBSAN_OPTIONS", "halt_on_error=1:print_stacktrace=1")
+        p = subprocess.run([BIN, "sample", d], capture_output=True, text=True, env=env, timeout=timeout)
+        if p.stderr.strip():
+            print(p.stderr[-12000:])
+        if p.returncode != 0:
+            raise RuntimeError(f"run_case exit {p.returncode}\n{p.stdout[-4000:]}\n{p.stderr[-12000:]}")
+        rd = lambda n, dt: np.fromfile(os.path.join(d, n), dt)
+        r = dict(ids=rd("out_ids.bin", np.int32),
+                 kept_ids=rd("out_kept_ids.bin", np.int32).reshape(B, kept_cap),
+                 kept_probs=rd("out_kept_probs.bin", np.float32).reshape(B, kept_cap),
+                 counts=rd("out_counts.bin", np.int32).reshape(B, 2),
+                 mass=rd("out_mass.bin", np.uint64).reshape(B, 2),
+                 cut_ids=rd("out_cut.bin", np.int32),
+                 post_logits=rd("out_post.bin", np.float32).reshape(B, V) if post else None)
+        return r

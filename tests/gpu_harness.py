@@ -23,7 +23,8 @@ def to_dev(a, dev="cuda:0"):
 
 
 def run_gpu(sampler, logits, params, u, hist=None, hist_len=None, mask_table=None, V=None,
-            kept_cap=64, post=True):
+            kept_cap=64, post=True, hint=None):
+    """hint: None (general kernel), "auto" (computed from params) or an int."""
     import torch
 
     import tinygpt_amd as tg
@@ -35,6 +36,8 @@ def run_gpu(sampler, logits, params, u, hist=None, hist_len=None, mask_table=Non
         sampler.set_mask_table(mask_table, V)
     else:
         sampler.set_mask_table(np.zeros((0, 1), np.uint32), 1)
+    if isinstance(hint, str):
+        hint = tg.batch_hint(params, V)
     lg = to_dev(logits)
     dbg = dict(
         kept_ids=torch.full((B, kept_cap), -7, dtype=torch.int32, device=dev),
@@ -45,7 +48,7 @@ def run_gpu(sampler, logits, params, u, hist=None, hist_len=None, mask_table=Non
         post_logits=torch.full((B, V), float("nan"), dtype=torch.float32, device=dev) if post else None,
     )
     out = sampler.sample(lg, tg.params_to_device(params, dev), to_dev(np.asarray(u, np.float32)),
-                         hist=to_dev(hist), hist_len=to_dev(hist_len), vocab=V, debug=dbg)
+                         hist=to_dev(hist), hist_len=to_dev(hist_len), vocab=V, debug=dbg, hint=hint)
     torch.cuda.synchronize()
     r = {k: (v.cpu().numpy() if v is not None else None) for k, v in dbg.items()}
     r["ids"] = out.cpu().numpy()

@@ -53,11 +53,29 @@ def test_create_rejects_bad_arguments(lib):
 
 
 def test_null_handle_calls_fail_cleanly(lib):
-    assert lib.tgs_sample(None, None, 0, 1, 1, 1, None, None, 0, None, None, None, None, None) == -1
+    assert lib.tgs_sample(None, None, 0, 1, 1, 1, None, None, 0, None, None, None, None, None, None) == -1
     assert lib.tgs_spec_verify(None, None, None, 0, None, 1, 1, 1, None, None, None, None, None, None) == -1
     assert lib.tgs_mask_table_set(None, None, 0, 1) == -1
     assert lib.tgs_last_error(None) == b"null handle"
     lib.tgs_destroy(None)
+
+
+def test_hint_from_params(lib):
+    import numpy as np
+
+    import tinygpt_amd as tg
+
+    V = 1000
+    p = tg.make_params(4, temperature=[0.0, 0.7, 1.0, 0.5], top_k=[0, 50, 7, 3])
+    assert tg.batch_hint(p, V) == 50
+    p["top_k"][3] = 0  # top-k disabled on a sampling row: the full row
+    assert tg.batch_hint(p, V) == V
+    p["top_k"][3] = V + 3
+    assert tg.batch_hint(p, V) == V
+    p = tg.make_params(3, temperature=0.0, top_k=0)
+    assert tg.batch_hint(p, V) == 0  # all greedy
+    p = tg.make_params(2, temperature=[np.nan, 0.9], top_k=[5, 9], flags=[0, 1])
+    assert tg.batch_hint(p, V) == 0  # NaN rows are invalid, flagged rows greedy
 
 
 def test_library_has_no_cpu_sampling_path():

@@ -1,0 +1,95 @@
+"""The product HIP kernels, compiled for the host against the CPU simulation
+in tests/cpu_sim (one OS thread per GPU thread, 64-lane waves, LDS poisoned
+at every workgroup start) under AddressSanitizer and UBSan, checked against
+the oracle.  Every memory access of the kernels on these batches is bounds
+checked; a sanitizer report fails the test.  CPU only."""
+import os
+import shutil
+import sys
+
+import numpy as np
+import pytest
+
+import gpu_harness as H
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "cpu_sim"))
+
+pytestmark = pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+
+
+@pytest.fixture(scope="module")
+def sim():
+    import sim as S
+
+    S.build()
+    return S
+
+
+def _batch(seed, B, V, oracle):
+    from test_gpu_sampler import _random_batch
+
+    return _random_batch(np.random.default_rng(seed), B, V, oracle)
+
+
+def _check(sim, oracle, x, params, u, hist, hist_len, mask=None, hint=None, split=None, kept_cap=1025):
+    r = sim.run_sample(x, params, u, hist, hist_len, mask_table=mask, kept_cap=kept_cap, hint=hint, split=split)
+    o = oracle.sample_batch(x, params, u, hist=hist, hist_len=hist_len, mask_table=mask, kept_cap=kept_cap,
+                            want_post=True)
+    return r, o, H.compare(r, o, params, x.shape[1], what="sim")
+
+
+def test_general_and_full_kernels(sim, oracle):
+    x, params, u, hist, hist_len = _batch(11, 16, 256, oracle)
+    _check(sim, oracle, x, params, u, hist, hist_len)
+
+
+def test_fast_kernel_with_hint(sim, oracle):
+    import tinygpt_amd as tg
+
+    x, params, u, hist, hist_len = _batch(12, 12, 300, oracle)
+    params["top_k"] = np.random.default_rng(1).choice([1, 2, 5, 40, 63, 64], size=12)
+    _check(sim, oracle, x, params, u, hist, hist_len, hint=tg.batch_hint(params, 300))
+
+
+def test_split_rows_and_merge(sim, oracle):
+    x, params, u, hist, hist_len = _batch(13, 4, 5000, oracle)
+    _check(sim, oracle, x, params, u, hist, hist_len, split=3)
+
+
+def test_grammar_mask(sim, oracle):
+    V = 300
+    g = np.random.default_rng(14)
+    x, params, u, hist, hist_len = _batch(14, 8, V, oracle)
+    table = g.integers(0, 1 << 32, size=(4, (V + 31) // 32), dtype=np.uint64).astype(np.uint32)
+    table[1] = 0
+    table[2, 0] = 1
+    params["mask_state"] = np.array([0, 1, 2, 3, -1, 4, 0, 3])  # 4: out of range, id -2
+    _check(sim, oracle, x, params, u, hist, hist_len, mask=table)
+
+
+def test_bf16_rows(sim, oracle):
+    from tinygpt_amd import workloads as W
+
+    x, params, u, hist, hist_len = _batch(15, 8, 1000, oracle)
+    xb = W.f32_to_bf16_bits(x)
+    _check(sim, oracle, xb, params, u, hist, hist_len)
+
+
+def test_rows_outside_the_hint_get_minus_3(sim, oracle):
+    g = np.random.default_rng(55)
+    B, V = 8, 3000
+    x = g.standard_normal((B, V)).astype(np.float32)
+    params = oracle.make_params(B, temperature=0.9, top_k=10, top_p=0.9)
+    params["top_k"][3] = 50    # above the hint, fast kernel
+    params["top_k"][5] = 0     # no usable top-k: full path not launched
+    params["temperature"][6] = 0.0  # greedy: served under any hint
+    u = np.full(B, 0.3, np.float32)
+    o = oracle.sample_batch(x, params, u)
+    for hint in (10, 200):
+        r = sim.run_sample(x, params, u, hint=hint, post=False)
+        expect = o["ids"].copy()
+        expect[5] = -3
+        if hint < 50:
+            expect[3] = -3
+        np.testing.assert_array_equal(r["ids"], expect)

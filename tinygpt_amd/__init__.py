@@ -19,4 +19,4 @@ from ._lib import (  # noqa: F401
     TgsError,
     load,
 )
-from .sampler import Sampler, make_params, params_to_device  # noqa: F401
+from .sampler import Sampler, batch_hint, make_params, params_to_device  # noqa: F401

@@ -30,6 +30,7 @@ TGS_FLAG_GREEDY = 1
 EXPORTS = (
     "tgs_abi_version",
     "tgs_status_string",
+    "tgs_hint_from_params",
     "tgs_create",
     "tgs_destroy",
     "tgs_last_error",
@@ -65,6 +66,10 @@ class TgsDebug(C.Structure):
         ("cut_ids", C.c_void_p),
         ("post_logits", C.c_void_p),
     ]
+
+
+class TgsHint(C.Structure):
+    _fields_ = [("max_top_k", C.c_int32)]
 
 
 class TgsError(RuntimeError):
@@ -106,7 +111,10 @@ def load() -> C.CDLL:
     L.tgs_mask_table_update.restype = I
     L.tgs_mask_table_update.argtypes = [P, P, P, I]
     L.tgs_sample.restype = I
-    L.tgs_sample.argtypes = [P, P, I, I, I, C.c_int64, P, P, I, P, P, P, C.POINTER(TgsDebug), P]
+    L.tgs_hint_from_params.restype = I
+    L.tgs_hint_from_params.argtypes = [P, I, I, C.POINTER(TgsHint)]
+    L.tgs_sample.argtypes = [P, P, I, I, I, C.c_int64, P, P, I, P, P, P, C.POINTER(TgsHint),
+                             C.POINTER(TgsDebug), P]
     L.tgs_reserve_spec.restype = I
     L.tgs_reserve_spec.argtypes = [P, I, I]
     L.tgs_spec_verify.restype = I

@@ -1,10 +1,11 @@
 // tgs_api.hip -- host side of the C ABI declared in include/tgs_sampler.h.
 //
-// The handle owns the split-row workspace (chunk candidate lists and
-// self-resetting arrival counters), the speculative workspace and the mask
-// table.  Calls validate host-visible arguments, choose the split (chunks
-// per row) from the batch size, size the dynamic LDS and launch one kernel
-// on the caller's stream.  Nothing here allocates during tgs_sample.
+// The handle owns the split-row workspace (chunk candidate lists), the
+// speculative workspace and the mask table.  Calls validate host-visible
+// arguments, pick the kernel variant from the batch hint and the split
+// (chunks per row) from the batch size, size the dynamic LDS and launch on
+// the caller's stream (chunk kernel, then the merge kernel when rows are
+// split).  Nothing here allocates during tgs_sample.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -23,13 +24,11 @@ struct tgs_ctx {
   int max_batch = 0, max_vocab = 0, max_hist = 0;
   int num_cu = 256;
   size_t lds_limit = 65536;
-  unsigned* counters = nullptr;
   unsigned long long* ws = nullptr;
   int* ws_cnt = nullptr;
-  int ws_rows = 0;
+  int ws_rows = 0;  // chunk lists of KMAX entries the workspace holds
   uint32_t* mask_table = nullptr;
   int n_states = 0, mask_vocab = 0, mask_words = 0;
-  unsigned* spec_counters = nullptr;
   float* spec_stats = nullptr;
   unsigned long long* spec_arg = nullptr;
   int spec_b = 0, spec_k = -1;
@@ -75,27 +74,25 @@ int log2i(int x) {
 }
 
 void free_spec(tgs_ctx* h) {
-  if (h->spec_counters) (void)hipFree(h->spec_counters);
   if (h->spec_stats) (void)hipFree(h->spec_stats);
   if (h->spec_arg) (void)hipFree(h->spec_arg);
-  h->spec_counters = nullptr;
   h->spec_stats = nullptr;
   h->spec_arg = nullptr;
   h->spec_b = 0;
   h->spec_k = -1;
 }
 
-// Chunks per row: enough workgroups to cover the chip twice, chunks of at
-// least one tile, at most kMaxSplit.  TGS_SPLIT overrides (tuning).
-int choose_split(const tgs_ctx* h, int B, int V, int dtype) {
-  const int tile = dtype == TGS_BF16 ? 8192 : 4096;
+// Chunks per row: about four workgroups per CU, chunks of at least one
+// 8192-id tile, at most kMaxSplit.  TGS_SPLIT overrides (tuning).
+int choose_split(const tgs_ctx* h, int B, int V) {
+  const int tile = 8192;
   int S = 1;
   const char* env = std::getenv("TGS_SPLIT");
   if (env && std::atoi(env) > 0) {
     S = std::min(std::atoi(env), kMaxSplit);
   } else {
-    const int target = 2 * h->num_cu;
-    while (S * 2 <= kMaxSplit && (long long)S * 2 * B <= target && (V + S * 2 - 1) / (S * 2) >= tile) S *= 2;
+    const int target = 4 * h->num_cu;
+    while (S * 2 <= kMaxSplit && (long long)S * 2 * B <= target && (V + S * 2 - 1) / (S * 2) >= tile / 2) S *= 2;
   }
   while (S > 1 && (long long)S * B > h->ws_rows) S >>= 1;
   return S;
@@ -117,6 +114,20 @@ const char* tgs_status_string(int status) {
     case TGS_ETOOBIG: return "size exceeds the handle's limits";
     default: return "unknown status";
   }
+}
+
+int tgs_hint_from_params(const tgs_row_params* p, int B, int V, tgs_batch_hint* out) {
+  if (!out || B < 0 || V < 1 || (B > 0 && !p)) return TGS_EINVAL;
+  int mk = 0;
+  for (int b = 0; b < B; b++) {
+    const float T = p[b].temperature;
+    const bool greedy = (p[b].flags & TGS_FLAG_GREEDY) || !(T > 0.0f);
+    if (greedy) continue;
+    const int k = (p[b].top_k >= 1 && p[b].top_k < V) ? p[b].top_k : V;
+    mk = std::max(mk, k);
+  }
+  out->max_top_k = mk;
+  return TGS_OK;
 }
 
 int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int max_hist) {
@@ -143,11 +154,9 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
     h->num_cu = v;
   if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
     h->lds_limit = (size_t)v;
-  h->ws_rows = std::max(max_batch, 2 * h->num_cu);
-  hipError_t e = hipMalloc(&h->counters, sizeof(unsigned) * (size_t)max_batch);
-  if (e == hipSuccess) e = hipMalloc(&h->ws, sizeof(unsigned long long) * (size_t)h->ws_rows * tgs::KMAX);
-  if (e == hipSuccess) e = hipMalloc(&h->ws_cnt, sizeof(int) * (size_t)h->ws_rows);
-  if (e == hipSuccess) e = hipMemset(h->counters, 0, sizeof(unsigned) * (size_t)max_batch);
+  h->ws_rows = std::max(max_batch, 4 * h->num_cu);
+  hipError_t e = hipMalloc(&h->ws, sizeof(unsigned long long) * (size_t)h->ws_rows * tgs::KMAX);
+  if (e == hipSuccess) e = hipMalloc(&h->ws_cnt, sizeof(int) * (size_t)h->ws_rows * (tgs::KMAX / 64));
   if (e == hipSuccess) {
     // raise the dynamic-LDS ceiling to the device limit; a runtime that
     // rejects the attribute keeps its default (calls that need more fail
@@ -166,7 +175,6 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
 void tgs_destroy(tgs_handle h) {
   if (!h) return;
   DeviceGuard g(h->device);
-  if (h->counters) (void)hipFree(h->counters);
   if (h->ws) (void)hipFree(h->ws);
   if (h->ws_cnt) (void)hipFree(h->ws_cnt);
   if (h->mask_table) (void)hipFree(h->mask_table);
@@ -220,7 +228,7 @@ int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32
 int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
                const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
                const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids,
-               const tgs_debug* dbg, tgs_stream stream) {
+               const tgs_batch_hint* hint, const tgs_debug* dbg, tgs_stream stream) {
   if (!h) return TGS_EINVAL;
   if (dt != TGS_F32 && dt != TGS_BF16) return fail(h, TGS_EINVAL, "dtype");
   if (B < 0 || V < 1 || row_stride < V) return fail(h, TGS_EINVAL, "shape");
@@ -257,10 +265,27 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   a.mask_table = table_ok ? h->mask_table : nullptr;
   a.n_states = table_ok ? h->n_states : 0;
   a.mask_words = h->mask_words;
-  const int S = choose_split(h, B, V, dt);
-  int L = V;
-  if (S > 1) {
+  // Kernels: the fast chunk kernel when every row is greedy or has
+  // top_k <= 64 (one-tile chunks); the general chunk kernel otherwise, plus
+  // the full-path kernel when the hint allows rows without a usable top-k.
+  const int mk = hint ? hint->max_top_k : 0x7FFFFFFF;
+  bool fast = mk <= 64 && mk < V;
+  a.full_rows = (mk > tgs::KMAX || mk >= V) ? 1 : 0;
+  a.hint_k = mk;
+  int S = 1, L = V;
+  if (fast) {
+    const int tile = 8192;
+    const int smin = (V + tile - 1) / tile;
+    S = std::max(smin, choose_split(h, B, V));
+    if ((long long)S * B * 64 > (long long)h->ws_rows * tgs::KMAX) fast = false;
+  }
+  if (fast) {
     L = ((V + S - 1) / S + 1023) / 1024 * 1024;
+    a.ws_stride = 64;
+  } else {
+    S = choose_split(h, B, V);
+    L = S > 1 ? ((V + S - 1) / S + 1023) / 1024 * 1024 : V;
+    a.ws_stride = tgs::KMAX;
   }
   a.S = (V + L - 1) / L;
   a.L = L;
@@ -274,12 +299,10 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   const size_t lds = (size_t)a.off_cand + (size_t)a.capt * 8;
   if (lds + sizeof(tgs::BlockScratch) > h->lds_limit)
     return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
-  a.counters = h->counters;
   a.ws = h->ws;
   a.ws_cnt = h->ws_cnt;
   a.dbg = dz;
-  const int grid = a.S == 1 ? B : ((B + 7) / 8) * 8 * a.S;
-  hipError_t e = tgs::launch_sample(a, dt, grid, lds, (hipStream_t)stream);
+  hipError_t e = tgs::launch_sample(a, dt, fast, lds, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
   return TGS_OK;
 }
@@ -294,10 +317,8 @@ int tgs_reserve_spec(tgs_handle h, int max_batch, int max_k) {
   const int nk = std::max(max_k, h->spec_k);
   free_spec(h);
   const size_t rows = (size_t)nb * (2 * nk + 1);
-  hipError_t e = hipMalloc(&h->spec_counters, sizeof(unsigned) * nb);
-  if (e == hipSuccess) e = hipMalloc(&h->spec_stats, sizeof(float) * 2 * rows);
+  hipError_t e = hipMalloc(&h->spec_stats, sizeof(float) * 2 * rows);
   if (e == hipSuccess) e = hipMalloc(&h->spec_arg, sizeof(unsigned long long) * rows);
-  if (e == hipSuccess) e = hipMemset(h->spec_counters, 0, sizeof(unsigned) * nb);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     free_spec(h);
@@ -340,7 +361,6 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
   a.u_res = d_u_res;
   a.n_acc = d_n_acc;
   a.out = d_out;
-  a.counters = h->spec_counters;
   a.ws_stats = h->spec_stats;
   a.ws_arg = h->spec_arg;
   hipError_t e = tgs::launch_spec(a, dt, (hipStream_t)stream);

@@ -14,6 +14,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Dynamic LDS of a kernel (a CPU simulation of the kernels for debugging
+// defines its own form).
+#ifndef TGS_DYN_SMEM
+#define TGS_DYN_SMEM(name) extern __shared__ __align__(16) unsigned char name[]
+#endif
+
 namespace tgs {
 
 constexpr int NT = 256;        // threads per workgroup
@@ -179,7 +185,7 @@ __device__ __forceinline__ T block_max(T x, T* red) {
 // the keys of that prefix number exactly what is needed (then
 // #{key >= T} == kth).  kth >= 1 and the multiset holds >= kth keys.
 template <typename K, int NBITS, class Enum>
-__device__ K block_select_kth(Enum en, unsigned kth, BlockScratch& s) {
+__device__ __forceinline__ K block_select_kth(Enum en, unsigned kth, BlockScratch& s) {
   K prefix = 0, pmask = 0;
   unsigned need = kth;
   for (int shift = NBITS - 8; shift >= 0; shift -= 8) {
@@ -233,7 +239,7 @@ __device__ K block_select_kth(Enum en, unsigned kth, BlockScratch& s) {
 // element's key; *before gets the mass strictly ahead of it, *rank the
 // number of elements strictly ahead of it.
 template <class Enum>
-__device__ u64 block_mass_select(Enum en, u64 target, BlockScratch& s, u64* before,
+__device__ __forceinline__ u64 block_mass_select(Enum en, u64 target, BlockScratch& s, u64* before,
                                  unsigned* rank) {
   u64 prefix = 0, pmask = 0;
   u64 mass_above = 0;
@@ -355,6 +361,49 @@ __device__ __forceinline__ void block_incl_scan_u64(u64* c, int n, u64* red) {
   for (int j = 0; j < 4; j++)
     if (base + j < n) c[base + j] = v[j] + off;
   __syncthreads();
+}
+
+}  // namespace tgs
+
+namespace tgs {
+
+// ------------------------------------------------------------------ wave sorts
+// One value per lane; "sorted" means descending with lane 0 holding the max.
+
+template <typename T>
+__device__ __forceinline__ T tmax(T a, T b) { return a > b ? a : b; }
+template <typename T>
+__device__ __forceinline__ T tmin(T a, T b) { return a < b ? a : b; }
+
+// Bitonic sort of 64 values across the lanes of a wave (descending).
+template <typename T>
+__device__ __forceinline__ T wave_sort_desc(T x) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const T y = __shfl_xor(x, stride, 64);
+      const bool lower = (lane & stride) == 0;
+      const bool desc = (lane & size) == 0;
+      x = (lower == desc) ? tmax(x, y) : tmin(x, y);
+    }
+  }
+  return x;
+}
+
+// a and b sorted descending across lanes: the 64 largest of their union,
+// sorted descending (max with the reversed b is bitonic, then 6 merge steps).
+template <typename T>
+__device__ __forceinline__ T wave_merge_top64(T a, T b) {
+  const int lane = lane_id();
+  T c = tmax(a, __shfl(b, 63 - lane, 64));
+#pragma unroll
+  for (int stride = 32; stride > 0; stride >>= 1) {
+    const T y = __shfl_xor(c, stride, 64);
+    c = ((lane & stride) == 0) ? tmax(c, y) : tmin(c, y);
+  }
+  return c;
 }
 
 }  // namespace tgs

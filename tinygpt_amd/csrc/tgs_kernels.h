@@ -26,9 +26,11 @@ struct SampleArgs {
   int BW;                // history bitmap words per chunk
   int capt;              // candidate buffer entries
   int off_hash, off_bitmap, off_cand;  // dynamic LDS byte offsets
-  unsigned* counters;    // [B] split-row arrival counters (self-resetting)
-  unsigned long long* ws;  // [B*S][KMAX] chunk candidate lists
+  unsigned long long* ws;  // [B*S][ws_stride] chunk candidate lists
+  int ws_stride;         // entries per chunk list (64 fast variant, KMAX otherwise)
   int* ws_cnt;           // [B*S]
+  int full_rows;         // 1: full_kernel runs after the chunk kernels
+  int hint_k;            // the launch hint's max_top_k (INT_MAX without a hint)
   tgs_debug dbg;
 };
 
@@ -43,12 +45,14 @@ struct SpecArgs {
   const float* u_res;
   int* n_acc;
   int* out;
-  unsigned* counters;          // [B]
   float* ws_stats;             // [B][2k+1][2] (m, S)
   unsigned long long* ws_arg;  // [B][2k+1] argmax composite
 };
 
-hipError_t launch_sample(const SampleArgs& a, int dtype, int grid, size_t lds, hipStream_t st);
+// Launches the chunk kernel (fast: the one-tile top_k <= 64 kernel), the
+// merge kernel when rows are split (a.S > 1) and the full-path kernel when
+// a.full_rows is set, in that order on stream st.
+hipError_t launch_sample(const SampleArgs& a, int dtype, bool fast, size_t lds, hipStream_t st);
 hipError_t set_sample_lds_limit(size_t bytes);
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
 

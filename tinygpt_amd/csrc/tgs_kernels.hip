@@ -1,26 +1,38 @@
 // tgs_kernels.hip -- gfx950 kernels of the decode-time sampler.
 //
-// sample_kernel: one launch samples a [B, V] batch.  Workgroup (b, c) owns
-// chunk c of row b (S chunks per row; S = 1 for large batches).  Per row
-// the path depends on its parameters:
-//   greedy    argmax of the post-penalty, masked logits (split over chunks,
-//             merged by the last workgroup of the row);
-//   candidate sampling with 1 <= top_k <= KMAX: each chunk streams its ids
-//             once with coalesced 16-byte loads, keeps a threshold-filtered
-//             candidate buffer in LDS and emits its exact local top-k; the
-//             last workgroup of the row merges S lists, sorts the top-k and
-//             runs softmax masses, the top-p scan and the draw;
-//   full      sampling without a usable top-k: one workgroup walks the row
-//             several times (radix selections on exact integer masses).
-// Penalties: history ids are inserted into an LDS hash (id -> count) and a
-// chunk bitmap; the stream skips them and the history pass adds them back
-// with their penalised logit.  Grammar mask: one 32-bit word of the state's
-// table row per 16-byte vector of logits.
+// Sampling a [B, V] batch takes one to three launches on the caller's
+// stream:
 //
-// spec_kernel: speculative verification.  One workgroup per (sequence, row)
-// computes the row maximum and canonical softmax denominator (block
-// maxima + exact 2^-40 block sums, pairwise fp32 tree); the last workgroup of
-// each sequence runs the accept/reject scan and the residual or bonus draw.
+//   chunk_kernel  workgroup (b, c) owns chunk c of row b (S chunks per row).
+//                 It issues all 16-byte loads of its first tile up front,
+//                 builds the row's history hash (id -> count) and chunk bitmap
+//                 in LDS while they are in flight, then keys every id
+//                 (penalised ids are skipped and re-added with their
+//                 penalised logit), keeps a threshold-filtered candidate
+//                 buffer in LDS and reduces it to the chunk's exact top-k
+//                 (sorted) or its argmax.  With S == 1 the same workgroup
+//                 finishes the row: softmax masses, top-p scan and draw.
+//   merge_kernel  (S > 1 only) one workgroup per row merges the S sorted
+//                 chunk lists -- for k <= 64 entirely in wave registers
+//                 (bitonic top-64 merges) -- and finishes the row.
+//
+// The kernel boundary is the handoff between chunks: cross-workgroup
+// fences cost a full L2 writeback per workgroup on this part, a second
+// launch costs one dispatch.
+//
+//   full_kernel   (only when the batch may hold them) rows that sample
+//                 without a usable top-k (k disabled or above KMAX): one
+//                 workgroup per row makes several passes over the row with
+//                 radix selections on exact integer masses.
+//
+// Every device function is inlined into its kernel: no kernel makes calls,
+// so none needs a call stack or passes pointers to private memory.
+//
+// spec_stats_kernel / spec_verify_kernel: speculative verification.  One
+// workgroup per (sequence, row) computes the row maximum and canonical
+// softmax denominator (block maxima, exact 2^-40 block sums, pairwise fp32
+// tree); one workgroup per sequence then runs the accept/reject scan and
+// the residual or bonus draw.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 
@@ -94,624 +106,7 @@ struct Row {
   int v0, v1;            // chunk id range [v0, v1)
 };
 
-// Dynamic LDS carve-up (byte offsets computed on the host).
-struct Lds {
-  int2* hash;         // [TS] (id, count), id -1 = empty
-  uint32_t* bitmap;   // [BW] history bits of the chunk
-  u64* cand;          // [capt] candidates; finalize reuses [0, 2*KMAX)
-};
-
-__device__ __forceinline__ unsigned hash_slot(int id, int shift) {
-  return ((unsigned)id * 2654435761u) >> shift;
-}
-
-__device__ void hash_build(const SampleArgs& a, const Row& r, Lds& L, bool with_bitmap) {
-  const int BW = with_bitmap ? a.BW : 0;
-  for (int i = threadIdx.x; i < a.TS; i += NT) L.hash[i] = make_int2(-1, 0);
-  for (int i = threadIdx.x; i < BW; i += NT) L.bitmap[i] = 0u;
-  __syncthreads();
-  const unsigned tmask = (unsigned)a.TS - 1u;
-  for (int j = threadIdx.x; j < r.H; j += NT) {
-    const int id = r.hrow[j];
-    if (id < r.v0 || id >= r.v1 || id >= a.V) continue;
-    unsigned h = hash_slot(id, a.ts_shift);
-    for (;;) {
-      const int old = atomicCAS(&L.hash[h].x, -1, id);
-      if (old == -1 || old == id) {
-        atomicAdd(&L.hash[h].y, 1);
-        break;
-      }
-      h = (h + 1) & tmask;
-    }
-    if (a.BW) atomicOr(&L.bitmap[(id - r.v0) >> 5], 1u << ((id - r.v0) & 31));
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ int hash_count(const int2* hash, int TS, int shift, int id) {
-  const unsigned tmask = (unsigned)TS - 1u;
-  unsigned h = hash_slot(id, shift);
-  for (;;) {
-    const int2 e = hash[h];
-    if (e.x == id) return e.y;
-    if (e.x == -1) return 0;
-    h = (h + 1) & tmask;
-  }
-}
-
-// Penalised logit of a history id (count c > 0).
-__device__ __forceinline__ float penalise(float z, int c, const Row& r) {
-  if (r.rep != 1.0f) z = (z > 0.0f) ? z / r.rep : z * r.rep;
-  z = z - r.freq * (float)c;
-  z = z - r.pres;
-  return z;
-}
-
-__device__ __forceinline__ bool mask_allows(const Row& r, int v) {
-  return r.mrow == nullptr || ((r.mrow[v >> 5] >> (v & 31)) & 1u);
-}
-
-// Key of one element: 0 when not allowed.
-__device__ __forceinline__ uint32_t elem_key(float z, bool allowed, float invT, float* y_out) {
-  const float y = z * invT;
-  const bool ok = allowed && (y > -__builtin_inff());
-  *y_out = ok ? y : -__builtin_inff();
-  return ok ? tg_key(y) : 0u;
-}
-
-// ------------------------------------------------------------------ finalize
-
-// kept candidates in L.cand[0, n) (unsorted, unique composites, n <= KMAX):
-// sort, masses, top-p, draw; writes the output id and diagnostics.
-__device__ void finalize_topk(const SampleArgs& a, const Row& r, Lds& L, int n, BlockScratch& s) {
-  const int b = r.b;
-  u64* C = L.cand + KMAX;
-  if (n <= 0) {
-    if (threadIdx.x == 0) {
-      a.out[b] = -1;
-      if (a.dbg.counts) { a.dbg.counts[2 * b] = 0; a.dbg.counts[2 * b + 1] = 0; }
-      if (a.dbg.mass) { a.dbg.mass[2 * b] = 0; a.dbg.mass[2 * b + 1] = 0; }
-      if (a.dbg.cut_ids) a.dbg.cut_ids[b] = -1;
-    }
-    if (a.dbg.kept_ids)
-      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
-    if (a.dbg.kept_probs)
-      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
-    return;
-  }
-  int n2 = 1;
-  while (n2 < n) n2 <<= 1;
-  for (int i = n + threadIdx.x; i < n2; i += NT) L.cand[i] = 0ull;
-  __syncthreads();
-  block_bitonic_desc(L.cand, n2);
-  const float m = comp_y(L.cand[0]);
-  for (int i = threadIdx.x; i < n; i += NT) C[i] = tg_q40(tg_weight(comp_y(L.cand[i]), m));
-  __syncthreads();
-  block_incl_scan_u64(C, n, s.red64);
-  const u64 S = C[n - 1];
-  if (threadIdx.x == 0) {
-    s.imin0 = n - 1;
-    s.imin1 = 0x7FFFFFFF;
-  }
-  __syncthreads();
-  if (r.top_p < 1.0f) {
-    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
-    const u64 P = mul_shr24(S, pq);
-    int best = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += NT)
-      if (C[i] >= P && i < best) best = i;
-    if (best != 0x7FFFFFFF) atomicMin(&s.imin0, best);
-    __syncthreads();
-  }
-  const int istar = s.imin0;
-  const u64 Sp = C[istar];
-  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
-  const u64 t = mul_shr24(Sp, uq);
-  {
-    int best = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i <= istar; i += NT)
-      if (C[i] > t && i < best) best = i;
-    if (best != 0x7FFFFFFF) atomicMin(&s.imin1, best);
-  }
-  __syncthreads();
-  int pick = s.imin1;
-  if (pick > istar) pick = istar;
-  if (threadIdx.x == 0) {
-    a.out[b] = comp_id(L.cand[pick]);
-    if (a.dbg.counts) { a.dbg.counts[2 * b] = n; a.dbg.counts[2 * b + 1] = istar + 1; }
-    if (a.dbg.mass) { a.dbg.mass[2 * b] = S; a.dbg.mass[2 * b + 1] = Sp; }
-    if (a.dbg.cut_ids) a.dbg.cut_ids[b] = comp_id(L.cand[istar]);
-  }
-  if (a.dbg.kept_ids) {
-    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kid[i] = i < n ? comp_id(L.cand[i]) : -1;
-  }
-  if (a.dbg.kept_probs) {
-    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
-    const float fs = tg_u64_to_f32(Sp);
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) {
-      float pv = 0.0f;
-      if (i <= istar) pv = tg_u64_to_f32(C[i] - (i ? C[i - 1] : 0ull)) / fs;
-      kp[i] = pv;
-    }
-  }
-}
-
-__device__ void finalize_greedy(const SampleArgs& a, int b, u64 best) {
-  const int id = best ? comp_id(best) : -1;
-  if (threadIdx.x == 0) {
-    a.out[b] = id;
-    if (a.dbg.counts) { a.dbg.counts[2 * b] = id >= 0; a.dbg.counts[2 * b + 1] = id >= 0; }
-    if (a.dbg.mass) { a.dbg.mass[2 * b] = 0; a.dbg.mass[2 * b + 1] = 0; }
-    if (a.dbg.cut_ids) a.dbg.cut_ids[b] = id;
-  }
-  if (a.dbg.kept_ids) {
-    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kid[i] = (i == 0) ? id : -1;
-  }
-  if (a.dbg.kept_probs) {
-    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kp[i] = (i == 0 && id >= 0) ? 1.0f : 0.0f;
-  }
-}
-
-// Keep the entries >= T of buf[0, n) in place (order not preserved); returns
-// the new count.  Batches of 4*NT entries: a batch is read completely before
-// its survivors are written, and survivors only land below the batch end
-// (the output count never exceeds the number of entries read so far).
-__device__ int compact_ge(u64* buf, int n, u64 T, BlockScratch& s) {
-  __syncthreads();
-  if (threadIdx.x == 0) s.nbuf = 0;
-  __syncthreads();
-  for (int base = 0; base < n; base += 4 * NT) {
-    u64 x[4];
-    unsigned cnt = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int i = base + j * NT + (int)threadIdx.x;
-      x[j] = (i < n) ? buf[i] : 0ull;
-      cnt += (i < n && x[j] >= T);
-    }
-    __syncthreads();
-    unsigned pos = cnt ? atomicAdd(&s.nbuf, cnt) : 0u;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int i = base + j * NT + (int)threadIdx.x;
-      if (i < n && x[j] >= T) buf[pos++] = x[j];
-    }
-  }
-  __syncthreads();
-  return (int)s.nbuf;
-}
-
-// ------------------------------------------------------------------ split merge
-
-// Chunk result handoff: returns true in the last workgroup of the row.
-__device__ bool arrive_last(const SampleArgs& a, int b, BlockScratch& s) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&a.counters[b], 1u);
-    s.last = (prev == (unsigned)a.S - 1u);
-  }
-  __syncthreads();
-  if (!s.last) return false;
-  __threadfence();
-  return true;
-}
-
-// ------------------------------------------------------------------ full path
-
-// Streams row b once, calling f(v, key, y) for every id.  Keys are
-// recomputed from global memory (the row stays hot in L2 / MALL).
-template <typename Tin, class F>
-__device__ void full_stream(const SampleArgs& a, const Row& r, const Lds& L, const Tin* rowp, F f) {
-  constexpr int EPV = Elem<Tin>::EPV;
-  const int nvec = (a.V + EPV - 1) / EPV;
-  for (int vi = threadIdx.x; vi < nvec; vi += NT) {
-    const int v = vi * EPV;
-    const uint4 raw = load_vec<Tin>(rowp, v, a.V, a.aligned);
-    const uint32_t mw = r.mrow ? r.mrow[v >> 5] : 0xFFFFFFFFu;
-#pragma unroll
-    for (int e = 0; e < EPV; e++) {
-      const int id = v + e;
-      float z = Elem<Tin>::get(raw, e);
-      if (r.use_pen && id < a.V) {
-        const int cnt = hash_count(L.hash, a.TS, a.ts_shift, id);
-        if (cnt > 0) z = penalise(z, cnt, r);
-      }
-      float y;
-      const uint32_t key = elem_key(z, ((mw >> (id & 31)) & 1u) != 0, r.invT, &y);
-      if (id < a.V) f(id, key, y);
-    }
-  }
-}
-
-template <typename Tin>
-__device__ void full_path(const SampleArgs& a, const Row& r, Lds& L, BlockScratch& s) {
-  const int b = r.b;
-  const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
-  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)b * a.V : nullptr;
-  // pass A: maximum composite and allowed count
-  u64 best = 0;
-  unsigned nv = 0;
-  full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float y) {
-    if (post) post[v] = y;
-    if (key) {
-      nv++;
-      const u64 c = comp_key(key, v);
-      best = c > best ? c : best;
-    }
-  });
-  best = block_max(best, s.red64);
-  nv = block_sum(nv, s.red32);
-  if (nv == 0) {
-    finalize_topk(a, r, L, 0, s);
-    return;
-  }
-  const unsigned kk = (r.k >= 1 && r.k < a.V) ? ((unsigned)r.k < nv ? (unsigned)r.k : nv) : nv;
-  // pass B: top-k threshold (exact count of kk entries)
-  u64 T = 1;
-  if (kk < nv) {
-    T = block_select_kth<u64, 64>(
-        [&](auto f) {
-          full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float) {
-            if (key) f(comp_key(key, v));
-          });
-        },
-        kk, s);
-  }
-  const float m = comp_y(best);
-  // pass C: total mass of the kept set and its last element
-  u64 S = 0, minc = ~0ull;
-  full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float y) {
-    if (!key) return;
-    const u64 c = comp_key(key, v);
-    if (c < T) return;
-    S += tg_q40(tg_weight(y, m));
-    minc = c < minc ? c : minc;
-  });
-  S = block_sum(S, s.red64);
-  minc = ~block_max(~minc, s.red64);
-  auto kept_enum = [&](auto f) {
-    full_stream<Tin>(a, r, L, rowp, [&](int v, uint32_t key, float y) {
-      if (!key) return;
-      const u64 c = comp_key(key, v);
-      if (c >= T) f(c, tg_q40(tg_weight(y, m)));
-    });
-  };
-  // pass D: top-p cut
-  u64 cutc = minc, Sp = S;
-  unsigned ntopp = kk;
-  if (r.top_p < 1.0f) {
-    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
-    const u64 P = mul_shr24(S, pq);
-    if (P == 0) {
-      cutc = best;
-      Sp = tg_q40(1.0f);
-      ntopp = 1;
-    } else {
-      u64 before;
-      unsigned rank;
-      cutc = block_mass_select(kept_enum, P, s, &before, &rank);
-      Sp = before + tg_q40(tg_weight(comp_y(cutc), m));
-      ntopp = rank + 1;
-    }
-  }
-  // pass E: draw
-  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
-  const u64 t = mul_shr24(Sp, uq);
-  u64 before;
-  unsigned rank;
-  const u64 pick = block_mass_select(kept_enum, t + 1, s, &before, &rank);
-  if (threadIdx.x == 0) {
-    a.out[b] = comp_id(pick);
-    if (a.dbg.counts) { a.dbg.counts[2 * b] = (int)kk; a.dbg.counts[2 * b + 1] = (int)ntopp; }
-    if (a.dbg.mass) { a.dbg.mass[2 * b] = S; a.dbg.mass[2 * b + 1] = Sp; }
-    if (a.dbg.cut_ids) a.dbg.cut_ids[b] = comp_id(cutc);
-  }
-  if (a.dbg.kept_ids)
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
-  if (a.dbg.kept_probs)
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
-}
-
-// ------------------------------------------------------------------ chunk paths
-
-template <typename Tin>
-struct Tile {
-  static constexpr int EPV = Elem<Tin>::EPV;
-  static constexpr int U = 4;                 // 16-byte vectors per thread per tile
-  static constexpr int EPT = U * EPV;         // elements per thread per tile
-  static constexpr int SIZE = NT * EPT;       // ids per tile
-};
-
-// Loads tile `t0` (first id) of the chunk into registers.
-template <typename Tin>
-__device__ __forceinline__ void tile_load(const Tin* rowp, const Row& r, int t0, bool aligned,
-                                          uint4 raw[Tile<Tin>::U], uint32_t mw[Tile<Tin>::U]) {
-  constexpr int EPV = Tile<Tin>::EPV;
-#pragma unroll
-  for (int u = 0; u < Tile<Tin>::U; u++) {
-    const int v = t0 + (u * NT + (int)threadIdx.x) * EPV;
-    raw[u] = load_vec<Tin>(rowp, v, r.v1, aligned);
-    mw[u] = (r.mrow && v < r.v1) ? r.mrow[v >> 5] : 0xFFFFFFFFu;
-  }
-}
-
-// Keys of a loaded tile; history ids (bitmap) and disallowed ids get key 0.
-template <typename Tin>
-__device__ __forceinline__ void tile_keys(const SampleArgs& a, const Row& r, const Lds& L, int t0,
-                                          const uint4 raw[Tile<Tin>::U],
-                                          const uint32_t mw[Tile<Tin>::U],
-                                          uint32_t key[Tile<Tin>::EPT], float* post) {
-  constexpr int EPV = Tile<Tin>::EPV;
-#pragma unroll
-  for (int u = 0; u < Tile<Tin>::U; u++) {
-    const int v = t0 + (u * NT + (int)threadIdx.x) * EPV;
-    uint32_t hb = 0;
-    if (r.use_pen && v < r.v1) hb = L.bitmap[(v - r.v0) >> 5];
-#pragma unroll
-    for (int e = 0; e < EPV; e++) {
-      const int id = v + e;
-      const bool hist = (hb >> ((id - r.v0) & 31)) & 1u;
-      float y;
-      const bool allowed = ((mw[u] >> (id & 31)) & 1u) && !hist;
-      uint32_t k = elem_key(Elem<Tin>::get(raw[u], e), allowed, r.invT, &y);
-      key[u * EPV + e] = k;
-      if (post && id < r.v1 && !hist) post[id] = y;
-    }
-  }
-}
-
-__device__ __forceinline__ int tile_id(int t0, int j, int EPV) {
-  const int u = j / EPV, e = j % EPV;
-  return t0 + (u * NT + (int)threadIdx.x) * EPV + e;
-}
-
-// History ids of the chunk with their penalised logits: calls f(v, key, y).
-template <typename Tin, class F>
-__device__ void history_pass(const SampleArgs& a, const Row& r, const Lds& L, const Tin* rowp, F f) {
-  for (int i = threadIdx.x; i < a.TS; i += NT) {
-    const int2 e = L.hash[i];
-    if (e.x < 0) continue;
-    const int v = e.x;
-    const float z = penalise(Elem<Tin>::scalar(rowp, v), e.y, r);
-    float y;
-    const uint32_t key = elem_key(z, mask_allows(r, v), r.invT, &y);
-    f(v, key, y);
-  }
-}
-
-template <typename Tin>
-__device__ void greedy_chunk(const SampleArgs& a, const Row& r, Lds& L, BlockScratch& s) {
-  using TL = Tile<Tin>;
-  const Tin* rowp = (const Tin*)a.logits + (long long)r.b * a.row_stride;
-  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)r.b * a.V : nullptr;
-  u64 best = 0;
-  uint4 raw[TL::U];
-  uint32_t mw[TL::U];
-  uint32_t key[TL::EPT];
-  for (int t0 = r.v0; t0 < r.v1; t0 += TL::SIZE) {
-    tile_load<Tin>(rowp, r, t0, a.aligned, raw, mw);
-    tile_keys<Tin>(a, r, L, t0, raw, mw, key, post);
-#pragma unroll
-    for (int j = 0; j < TL::EPT; j++)
-      if (key[j]) {
-        const u64 c = comp_key(key[j], tile_id(t0, j, TL::EPV));
-        best = c > best ? c : best;
-      }
-  }
-  if (r.use_pen)
-    history_pass<Tin>(a, r, L, rowp, [&](int v, uint32_t k, float y) {
-      if (post) post[v] = y;
-      if (k) {
-        const u64 c = comp_key(k, v);
-        best = c > best ? c : best;
-      }
-    });
-  best = block_max(best, s.red64);
-  if (a.S == 1) {
-    finalize_greedy(a, r.b, best);
-    return;
-  }
-  if (threadIdx.x == 0) a.ws[((long long)r.b * a.S + r.c) * KMAX] = best;
-  if (!arrive_last(a, r.b, s)) return;
-  u64 m = 0;
-  for (int c = threadIdx.x; c < a.S; c += NT) {
-    const u64 x = __atomic_load_n(&a.ws[((long long)r.b * a.S + c) * KMAX], __ATOMIC_RELAXED);
-    m = x > m ? x : m;
-  }
-  m = block_max(m, s.red64);
-  finalize_greedy(a, r.b, m);
-  if (threadIdx.x == 0) a.counters[r.b] = 0u;
-}
-
-// Initial threshold from the first tile: a key T0 with at least k keys >= T0
-// among the chunk's stream ids (k <= NT*4).
-template <int EPT>
-__device__ uint32_t first_threshold(const uint32_t key[EPT], int k, BlockScratch& s) {
-  if (k <= 64) {
-    uint32_t mx = 0;
-#pragma unroll
-    for (int j = 0; j < EPT; j++) mx = key[j] > mx ? key[j] : mx;
-    // k-th largest thread maximum within each wave (bitonic over 64 lanes)
-    uint32_t x = mx;
-    const int lane = lane_id();
-    for (int size = 2; size <= 64; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        const uint32_t y = __shfl_xor(x, stride, 64);
-        const bool lower = (lane & stride) == 0;
-        const bool desc = (lane & size) == 0;
-        // descending blocks keep the larger value in the lower lane
-        const bool take_max = (lower == desc);
-        x = take_max ? (x > y ? x : y) : (x < y ? x : y);
-      }
-    }
-    const uint32_t wk = __shfl(x, k - 1, 64);
-    return block_max(wk, s.red32);
-  }
-  // per-thread j-th largest (j = ceil(k / NT) <= 4), then the ceil(k/j)-th
-  // largest of those over the block
-  const int jj = (k + NT - 1) / NT;
-  uint32_t t4[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    uint32_t x = key[j];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const uint32_t hi = x > t4[q] ? x : t4[q];
-      const uint32_t lo = x > t4[q] ? t4[q] : x;
-      t4[q] = hi;
-      x = lo;
-    }
-  }
-  const uint32_t aj = jj == 1 ? t4[0] : jj == 2 ? t4[1] : jj == 3 ? t4[2] : t4[3];
-  const unsigned r = (unsigned)((k + jj - 1) / jj);
-  return block_select_kth<uint32_t, 32>([&](auto f) { f(aj); }, r, s);
-}
-
-template <typename Tin>
-__device__ void topk_chunk(const SampleArgs& a, const Row& r, Lds& L, BlockScratch& s) {
-  using TL = Tile<Tin>;
-  const Tin* rowp = (const Tin*)a.logits + (long long)r.b * a.row_stride;
-  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)r.b * a.V : nullptr;
-  const int k = r.k;
-  if (threadIdx.x == 0) s.nbuf = 0;
-  u64 thr = 0;  // candidates: composite >= thr and key != 0
-  uint4 raw[TL::U];
-  uint32_t mw[TL::U];
-  uint32_t key[TL::EPT];
-  bool first = true;
-  for (int t0 = r.v0; t0 < r.v1; t0 += TL::SIZE) {
-    tile_load<Tin>(rowp, r, t0, a.aligned, raw, mw);
-    tile_keys<Tin>(a, r, L, t0, raw, mw, key, post);
-    if (first) {
-      thr = (u64)first_threshold<TL::EPT>(key, k, s) << 32;
-      first = false;
-    }
-    unsigned mine = 0;
-#pragma unroll
-    for (int j = 0; j < TL::EPT; j++)
-      mine += (key[j] && comp_key(key[j], tile_id(t0, j, TL::EPV)) >= thr);
-    const unsigned total = block_sum(mine, s.red32);
-    const unsigned nbuf = s.nbuf;
-    if (nbuf + total > (unsigned)CAPB) {
-      // shrink: exact k-th composite over buffer and this tile's candidates
-      const u64 thr_old = thr;
-      const u64 T = block_select_kth<u64, 64>(
-          [&](auto f) {
-            for (unsigned i = threadIdx.x; i < nbuf; i += NT) f(L.cand[i]);
-#pragma unroll
-            for (int j = 0; j < TL::EPT; j++)
-              if (key[j]) {
-                const u64 c = comp_key(key[j], tile_id(t0, j, TL::EPV));
-                if (c >= thr_old) f(c);
-              }
-          },
-          (unsigned)k, s);
-      compact_ge(L.cand, (int)nbuf, T, s);
-      thr = T;
-      mine = 0;
-#pragma unroll
-      for (int j = 0; j < TL::EPT; j++)
-        mine += (key[j] && comp_key(key[j], tile_id(t0, j, TL::EPV)) >= thr);
-    }
-    // append this thread's candidates
-    {
-      const unsigned incl = wave_incl_scan(mine);
-      unsigned base = 0;
-      if (lane_id() == 63 && incl) base = atomicAdd(&s.nbuf, incl);
-      base = __shfl(base, 63, 64) + incl - mine;
-#pragma unroll
-      for (int j = 0; j < TL::EPT; j++)
-        if (key[j]) {
-          const u64 c = comp_key(key[j], tile_id(t0, j, TL::EPV));
-          if (c >= thr) L.cand[base++] = c;
-        }
-    }
-    __syncthreads();
-  }
-  // history ids with their penalised logits
-  if (r.use_pen) {
-    history_pass<Tin>(a, r, L, rowp, [&](int v, uint32_t kk, float y) {
-      if (post) post[v] = y;
-      if (kk) {
-        const u64 c = comp_key(kk, v);
-        if (c >= thr) L.cand[atomicAdd(&s.nbuf, 1u)] = c;
-      }
-    });
-    __syncthreads();
-  }
-  int n = (int)s.nbuf;
-  __syncthreads();
-  if (n > k) {
-    const u64 T = block_select_kth<u64, 64>(
-        [&](auto f) {
-          for (int i = threadIdx.x; i < n; i += NT) f(L.cand[i]);
-        },
-        (unsigned)k, s);
-    n = compact_ge(L.cand, n, T, s);
-  }
-  if (a.S == 1) {
-    finalize_topk(a, r, L, n, s);
-    return;
-  }
-  // hand the chunk's list to the row's last workgroup
-  u64* dst = a.ws + ((long long)r.b * a.S + r.c) * KMAX;
-  for (int i = threadIdx.x; i < n; i += NT) dst[i] = L.cand[i];
-  if (threadIdx.x == 0) a.ws_cnt[r.b * a.S + r.c] = n;
-  if (!arrive_last(a, r.b, s)) return;
-  // merge
-  int total = 0;
-  for (int c = 0; c < a.S; c++) total += __atomic_load_n(&a.ws_cnt[r.b * a.S + c], __ATOMIC_RELAXED);
-  const int kk = total < k ? total : k;
-  const u64* src = a.ws + (long long)r.b * a.S * KMAX;
-  if (total <= a.capt) {
-    int off = 0;
-    for (int c = 0; c < a.S; c++) {
-      const int cnt = a.ws_cnt[r.b * a.S + c];
-      for (int i = threadIdx.x; i < cnt; i += NT) L.cand[off + i] = src[(long long)c * KMAX + i];
-      off += cnt;
-    }
-    __syncthreads();
-    n = total;
-    if (n > kk) {
-      const u64 T = block_select_kth<u64, 64>(
-          [&](auto f) {
-            for (int i = threadIdx.x; i < n; i += NT) f(L.cand[i]);
-          },
-          (unsigned)kk, s);
-      n = compact_ge(L.cand, n, T, s);
-    }
-  } else {
-    const u64 T = block_select_kth<u64, 64>(
-        [&](auto f) {
-          for (int c = 0; c < a.S; c++) {
-            const int cnt = a.ws_cnt[r.b * a.S + c];
-            for (int i = threadIdx.x; i < cnt; i += NT) f(src[(long long)c * KMAX + i]);
-          }
-        },
-        (unsigned)kk, s);
-    if (threadIdx.x == 0) s.nbuf = 0;
-    __syncthreads();
-    for (int c = 0; c < a.S; c++) {
-      const int cnt = a.ws_cnt[r.b * a.S + c];
-      for (int i = threadIdx.x; i < cnt; i += NT) {
-        const u64 x = src[(long long)c * KMAX + i];
-        if (x >= T) L.cand[atomicAdd(&s.nbuf, 1u)] = x;
-      }
-    }
-    __syncthreads();
-    n = (int)s.nbuf;
-  }
-  finalize_topk(a, r, L, n, s);
-  if (threadIdx.x == 0) a.counters[r.b] = 0u;
-}
-
-// ------------------------------------------------------------------ kernel
-
-__device__ bool row_setup(const SampleArgs& a, int b, int c, Row& r) {
+__device__ __forceinline__ bool row_setup(const SampleArgs& a, int b, int c, Row& r) {
   const tgs_row_params p = a.params[b];
   r.b = b;
   r.c = c;
@@ -748,51 +143,918 @@ __device__ bool row_setup(const SampleArgs& a, int b, int c, Row& r) {
   if (greedy) r.mode = 0;
   else if (p.top_k >= 1 && p.top_k <= KMAX && p.top_k < a.V) r.mode = 1;
   else r.mode = 2;
+  r.v0 = 0;
+  r.v1 = a.V;
   return true;
 }
 
-template <typename Tin>
-__global__ __launch_bounds__(NT) void sample_kernel(SampleArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ BlockScratch s;
-  int b, c;
-  if (a.S == 1) {
-    b = blockIdx.x;
-    c = 0;
-  } else {
-    // all chunks of a row land on one XCD (workgroups round-robin over 8)
-    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
-    b = (j / a.S) * 8 + xcd;
-    c = j % a.S;
+// A sampling row outside the launch hint: top-k above hint_k, or no usable
+// top-k while the full-path kernel is not launched.  Such rows get id -3.
+__device__ __forceinline__ bool outside_hint(const SampleArgs& a, const Row& r) {
+  return (r.mode == 1 && r.k > a.hint_k) || (r.mode == 2 && !a.full_rows);
+}
+
+// ------------------------------------------------------------------ history
+
+__device__ __forceinline__ unsigned hash_slot(int id, int shift) {
+  return ((unsigned)id * 2654435761u) >> shift;
+}
+
+// Insert the row's history ids that fall in [r.v0, r.v1) into the LDS hash
+// (id -> count) and, when BW > 0, the chunk bitmap.
+__device__ __forceinline__ void hash_build(const SampleArgs& a, const Row& r, int2* hash,
+                                           uint32_t* bitmap, int BW) {
+  for (int i = threadIdx.x; i < a.TS; i += NT) hash[i] = make_int2(-1, 0);
+  for (int i = threadIdx.x; i < BW; i += NT) bitmap[i] = 0u;
+  __syncthreads();
+  const unsigned tmask = (unsigned)a.TS - 1u;
+  for (int j = threadIdx.x; j < r.H; j += NT) {
+    const int id = r.hrow[j];
+    if (id < r.v0 || id >= r.v1 || id >= a.V) continue;
+    unsigned h = hash_slot(id, a.ts_shift);
+    for (;;) {
+      const int old = atomicCAS(&hash[h].x, -1, id);
+      if (old == -1 || old == id) {
+        atomicAdd(&hash[h].y, 1);
+        break;
+      }
+      h = (h + 1) & tmask;
+    }
+    if (BW) atomicOr(&bitmap[(id - r.v0) >> 5], 1u << ((id - r.v0) & 31));
   }
+  __syncthreads();
+}
+
+__device__ __forceinline__ int hash_count(const int2* hash, int TS, int shift, int id) {
+  const unsigned tmask = (unsigned)TS - 1u;
+  unsigned h = hash_slot(id, shift);
+  for (;;) {
+    const int2 e = hash[h];
+    if (e.x == id) return e.y;
+    if (e.x == -1) return 0;
+    h = (h + 1) & tmask;
+  }
+}
+
+// Penalised logit of a history id (count c > 0): CTRL repetition, then
+// frequency per occurrence, then presence.
+__device__ __forceinline__ float penalise(float z, int c, const Row& r) {
+  if (r.rep != 1.0f) z = (z > 0.0f) ? z / r.rep : z * r.rep;
+  z = z - r.freq * (float)c;
+  z = z - r.pres;
+  return z;
+}
+
+__device__ __forceinline__ bool mask_allows(const Row& r, int v) {
+  return r.mrow == nullptr || ((r.mrow[v >> 5] >> (v & 31)) & 1u);
+}
+
+// Key of one element (0 when not allowed); *y_out gets the canonical logit.
+__device__ __forceinline__ uint32_t elem_key(float z, bool allowed, float invT, float* y_out) {
+  const float y = z * invT;
+  const bool ok = allowed && (y > -__builtin_inff());
+  *y_out = ok ? y : -__builtin_inff();
+  return ok ? tg_key(y) : 0u;
+}
+
+// ------------------------------------------------------------------ finalize
+
+__device__ __forceinline__ void write_row_diag(const SampleArgs& a, int b, int n1, int n2, u64 S, u64 Sp, int cut) {
+  if (a.dbg.counts) { a.dbg.counts[2 * b] = n1; a.dbg.counts[2 * b + 1] = n2; }
+  if (a.dbg.mass) { a.dbg.mass[2 * b] = S; a.dbg.mass[2 * b + 1] = Sp; }
+  if (a.dbg.cut_ids) a.dbg.cut_ids[b] = cut;
+}
+
+// Called by one whole wave: x is this lane's entry of the kept list sorted
+// by (logit desc, id asc) (lane i = rank i), n in [1, 64] valid entries.
+__device__ __forceinline__ void wave_finalize(const SampleArgs& a, const Row& r, u64 x, int n) {
+  const int lane = lane_id();
+  const int b = r.b;
+  const float y = comp_y(x);
+  const float m = __shfl(y, 0, 64);
+  const u64 q = lane < n ? tg_q40(tg_weight(y, m)) : 0ull;
+  const u64 C = wave_incl_scan(q);
+  const u64 S = __shfl(C, n - 1, 64);
+  int istar = n - 1;
+  if (r.top_p < 1.0f) {
+    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
+    const u64 P = mul_shr24(S, pq);
+    const u64 bal = __ballot(lane < n && C >= P);
+    istar = __ffsll((long long)bal) - 1;
+  }
+  const u64 Sp = __shfl(C, istar, 64);
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
+  const u64 t = mul_shr24(Sp, uq);
+  const u64 bal2 = __ballot(lane <= istar && C > t);
+  const int pick = bal2 ? __ffsll((long long)bal2) - 1 : istar;
+  const u64 xp = __shfl(x, pick, 64);
+  const u64 xc = __shfl(x, istar, 64);
+  if (lane == 0) {
+    a.out[b] = comp_id(xp);
+    write_row_diag(a, b, n, istar + 1, S, Sp, comp_id(xc));
+  }
+  if (a.dbg.kept_ids) {
+    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
+    for (int i = lane; i < a.dbg.kept_cap; i += 64) kid[i] = (i < n) ? comp_id(x) : -1;
+  }
+  if (a.dbg.kept_probs) {
+    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
+    const float fs = tg_u64_to_f32(Sp);
+    for (int i = lane; i < a.dbg.kept_cap; i += 64) kp[i] = (i <= istar) ? tg_u64_to_f32(q) / fs : 0.0f;
+  }
+}
+
+// kept candidates in cand[0, n) (unsorted, unique composites, n <= KMAX):
+// sort, masses, top-p, draw.  cand must hold 2*KMAX entries.
+__device__ __forceinline__ void finalize_topk(const SampleArgs& a, const Row& r, u64* cand, int n,
+                                              BlockScratch& s) {
+  const int b = r.b;
+  u64* C = cand + KMAX;
+  if (n > KMAX) n = KMAX;  // never taken: callers pass exact top-k sets (k <= KMAX)
+  if (n <= 0) {
+    if (threadIdx.x == 0) {
+      a.out[b] = -1;
+      write_row_diag(a, b, 0, 0, 0, 0, -1);
+    }
+    if (a.dbg.kept_ids)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
+    if (a.dbg.kept_probs)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
+    return;
+  }
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (int i = n + threadIdx.x; i < n2; i += NT) cand[i] = 0ull;
+  __syncthreads();
+  block_bitonic_desc(cand, n2);
+  const float m = comp_y(cand[0]);
+  for (int i = threadIdx.x; i < n; i += NT) C[i] = tg_q40(tg_weight(comp_y(cand[i]), m));
+  __syncthreads();
+  block_incl_scan_u64(C, n, s.red64);
+  const u64 S = C[n - 1];
+  if (threadIdx.x == 0) {
+    s.imin0 = n - 1;
+    s.imin1 = 0x7FFFFFFF;
+  }
+  __syncthreads();
+  if (r.top_p < 1.0f) {
+    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
+    const u64 P = mul_shr24(S, pq);
+    int best = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += NT)
+      if (C[i] >= P && i < best) best = i;
+    if (best != 0x7FFFFFFF) atomicMin(&s.imin0, best);
+    __syncthreads();
+  }
+  const int istar = s.imin0;
+  const u64 Sp = C[istar];
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
+  const u64 t = mul_shr24(Sp, uq);
+  {
+    int best = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i <= istar; i += NT)
+      if (C[i] > t && i < best) best = i;
+    if (best != 0x7FFFFFFF) atomicMin(&s.imin1, best);
+  }
+  __syncthreads();
+  int pick = s.imin1;
+  if (pick > istar) pick = istar;
+  if (threadIdx.x == 0) {
+    a.out[b] = comp_id(cand[pick]);
+    write_row_diag(a, b, n, istar + 1, S, Sp, comp_id(cand[istar]));
+  }
+  if (a.dbg.kept_ids) {
+    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kid[i] = i < n ? comp_id(cand[i]) : -1;
+  }
+  if (a.dbg.kept_probs) {
+    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
+    const float fs = tg_u64_to_f32(Sp);
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) {
+      float pv = 0.0f;
+      if (i <= istar) pv = tg_u64_to_f32(C[i] - (i ? C[i - 1] : 0ull)) / fs;
+      kp[i] = pv;
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void finalize_greedy(const SampleArgs& a, int b, u64 best) {
+  const int id = best ? comp_id(best) : -1;
+  if (threadIdx.x == 0) {
+    a.out[b] = id;
+    write_row_diag(a, b, id >= 0, id >= 0, 0, 0, id);
+  }
+  if (a.dbg.kept_ids) {
+    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kid[i] = (i == 0) ? id : -1;
+  }
+  if (a.dbg.kept_probs) {
+    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kp[i] = (i == 0 && id >= 0) ? 1.0f : 0.0f;
+  }
+}
+
+// Keep the entries >= T of buf[0, n) in place (order not preserved); returns
+// the new count.  Batches of 4*NT entries: a batch is read completely before
+// its survivors are written, and survivors only land below the batch end
+// (the output count never exceeds the number of entries read so far).
+__device__ __forceinline__ int compact_ge(u64* buf, int n, u64 T, BlockScratch& s) {
+  __syncthreads();
+  if (threadIdx.x == 0) s.nbuf = 0;
+  __syncthreads();
+  for (int base = 0; base < n; base += 4 * NT) {
+    u64 x[4];
+    unsigned cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = base + j * NT + (int)threadIdx.x;
+      x[j] = (i < n) ? buf[i] : 0ull;
+      cnt += (i < n && x[j] >= T);
+    }
+    __syncthreads();
+    unsigned pos = cnt ? atomicAdd(&s.nbuf, cnt) : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = base + j * NT + (int)threadIdx.x;
+      if (i < n && x[j] >= T) buf[pos++] = x[j];
+    }
+  }
+  __syncthreads();
+  return (int)s.nbuf;
+}
+
+// ------------------------------------------------------------------ full path
+
+// Streams row b once, calling f(v, key, y) for every id.  Keys are
+// recomputed from global memory (the row stays hot in L2 / MALL).
+template <typename Tin, class F>
+__device__ __forceinline__ void full_stream(const SampleArgs& a, const Row& r, const int2* hash,
+                                            const Tin* rowp, F f) {
+  constexpr int EPV = Elem<Tin>::EPV;
+  const int nvec = (a.V + EPV - 1) / EPV;
+  for (int vi = threadIdx.x; vi < nvec; vi += NT) {
+    const int v = vi * EPV;
+    const uint4 raw = load_vec<Tin>(rowp, v, a.V, a.aligned);
+    const uint32_t mw = r.mrow ? r.mrow[v >> 5] : 0xFFFFFFFFu;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) {
+      const int id = v + e;
+      float z = Elem<Tin>::get(raw, e);
+      if (r.use_pen && id < a.V) {
+        const int cnt = hash_count(hash, a.TS, a.ts_shift, id);
+        if (cnt > 0) z = penalise(z, cnt, r);
+      }
+      float y;
+      const uint32_t key = elem_key(z, ((mw >> (id & 31)) & 1u) != 0, r.invT, &y);
+      if (id < a.V) f(id, key, y);
+    }
+  }
+}
+
+template <typename Tin>
+__device__ __forceinline__ void full_path(const SampleArgs& a, const Row& r, const int2* hash, u64* cand, BlockScratch& s) {
+  const int b = r.b;
+  const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
+  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)b * a.V : nullptr;
+  // pass A: maximum composite and allowed count
+  u64 best = 0;
+  unsigned nv = 0;
+  full_stream<Tin>(a, r, hash, rowp, [&](int v, uint32_t key, float y) {
+    if (post) post[v] = y;
+    if (key) {
+      nv++;
+      const u64 c = comp_key(key, v);
+      best = c > best ? c : best;
+    }
+  });
+  best = block_max(best, s.red64);
+  nv = block_sum(nv, s.red32);
+  if (nv == 0) {
+    finalize_topk(a, r, cand, 0, s);
+    return;
+  }
+  const unsigned kk = (r.k >= 1 && r.k < a.V) ? ((unsigned)r.k < nv ? (unsigned)r.k : nv) : nv;
+  // pass B: top-k threshold (exact count of kk entries)
+  u64 T = 1;
+  if (kk < nv) {
+    T = block_select_kth<u64, 64>(
+        [&](auto f) {
+          full_stream<Tin>(a, r, hash, rowp, [&](int v, uint32_t key, float) {
+            if (key) f(comp_key(key, v));
+          });
+        },
+        kk, s);
+  }
+  const float m = comp_y(best);
+  // pass C: total mass of the kept set and its last element
+  u64 S = 0, minc = ~0ull;
+  full_stream<Tin>(a, r, hash, rowp, [&](int v, uint32_t key, float y) {
+    if (!key) return;
+    const u64 c = comp_key(key, v);
+    if (c < T) return;
+    S += tg_q40(tg_weight(y, m));
+    minc = c < minc ? c : minc;
+  });
+  S = block_sum(S, s.red64);
+  minc = ~block_max(~minc, s.red64);
+  auto kept_enum = [&](auto f) {
+    full_stream<Tin>(a, r, hash, rowp, [&](int v, uint32_t key, float y) {
+      if (!key) return;
+      const u64 c = comp_key(key, v);
+      if (c >= T) f(c, tg_q40(tg_weight(y, m)));
+    });
+  };
+  // pass D: top-p cut
+  u64 cutc = minc, Sp = S;
+  unsigned ntopp = kk;
+  if (r.top_p < 1.0f) {
+    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
+    const u64 P = mul_shr24(S, pq);
+    if (P == 0) {
+      cutc = best;
+      Sp = tg_q40(1.0f);
+      ntopp = 1;
+    } else {
+      u64 before;
+      unsigned rank;
+      cutc = block_mass_select(kept_enum, P, s, &before, &rank);
+      Sp = before + tg_q40(tg_weight(comp_y(cutc), m));
+      ntopp = rank + 1;
+    }
+  }
+  // pass E: draw
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
+  const u64 t = mul_shr24(Sp, uq);
+  u64 before;
+  unsigned rank;
+  const u64 pick = block_mass_select(kept_enum, t + 1, s, &before, &rank);
+  if (threadIdx.x == 0) {
+    a.out[b] = comp_id(pick);
+    write_row_diag(a, b, (int)kk, (int)ntopp, S, Sp, comp_id(cutc));
+  }
+  if (a.dbg.kept_ids)
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
+  if (a.dbg.kept_probs)
+    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
+}
+
+// ------------------------------------------------------------------ chunk paths
+
+template <typename Tin>
+struct Tile {
+  static constexpr int EPV = Elem<Tin>::EPV;
+  static constexpr int EPT = 32;          // elements per thread per tile
+  static constexpr int U = EPT / EPV;     // 16-byte vectors per thread per tile
+  static constexpr int SIZE = NT * EPT;   // ids per tile (8192)
+};
+
+__device__ __forceinline__ int tile_id(int t0, int j, int EPV) {
+  const int u = j / EPV, e = j % EPV;
+  return t0 + (u * NT + (int)threadIdx.x) * EPV + e;
+}
+
+template <typename Tin>
+__device__ __forceinline__ void tile_load(const Tin* rowp, const Row& r, int t0, bool aligned,
+                                          uint4 (&raw)[Tile<Tin>::U], uint32_t (&mw)[Tile<Tin>::U]) {
+  constexpr int EPV = Tile<Tin>::EPV;
+  constexpr int U = Tile<Tin>::U;
+  if (aligned && t0 + Tile<Tin>::SIZE <= r.v1) {  // whole tile inside the chunk: plain vector loads
+#pragma unroll
+    for (int u = 0; u < U; u++) raw[u] = *(const uint4*)(rowp + t0 + (u * NT + (int)threadIdx.x) * EPV);
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; u++) raw[u] = load_vec<Tin>(rowp, t0 + (u * NT + (int)threadIdx.x) * EPV, r.v1, aligned);
+  }
+  if (r.mrow) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int v = t0 + (u * NT + (int)threadIdx.x) * EPV;
+      mw[u] = r.mrow[(v < r.v1 ? v : r.v1 - 1) >> 5];
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; u++) mw[u] = 0xFFFFFFFFu;
+  }
+}
+
+// Keys of a loaded tile; history ids (bitmap) and disallowed ids get key 0.
+// Ids past the chunk end were loaded as NaN and get key 0 as well.
+template <typename Tin>
+__device__ __forceinline__ void tile_keys(const Row& r, const uint32_t* bitmap, int bw, int t0,
+                                          const uint4 (&raw)[Tile<Tin>::U],
+                                          const uint32_t (&mw)[Tile<Tin>::U],
+                                          uint32_t (&key)[Tile<Tin>::EPT], float* post) {
+  constexpr int EPV = Tile<Tin>::EPV;
+  constexpr int U = Tile<Tin>::U;
+  uint32_t hb[U];
+  if (r.use_pen) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int v = t0 + (u * NT + (int)threadIdx.x) * EPV;
+      const int w = (v - r.v0) >> 5;
+      hb[u] = bitmap[w < bw ? w : bw - 1];
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; u++) hb[u] = 0u;
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int v = t0 + (u * NT + (int)threadIdx.x) * EPV;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) {
+      const int id = v + e;
+      const bool hist = (hb[u] >> ((id - r.v0) & 31)) & 1u;
+      float y;
+      const bool allowed = ((mw[u] >> (id & 31)) & 1u) && !hist;
+      key[u * EPV + e] = elem_key(Elem<Tin>::get(raw[u], e), allowed, r.invT, &y);
+      if (post && id < r.v1 && !hist) post[id] = y;
+    }
+  }
+}
+
+// History ids of the chunk with their penalised logits: calls f(v, key, y).
+template <typename Tin, class F>
+__device__ __forceinline__ void history_pass(const SampleArgs& a, const Row& r, const int2* hash,
+                                             const Tin* rowp, F f) {
+  for (int i = threadIdx.x; i < a.TS; i += NT) {
+    const int2 e = hash[i];
+    if (e.x < 0) continue;
+    const int v = e.x;
+    const float z = penalise(Elem<Tin>::scalar(rowp, v), e.y, r);
+    float y;
+    const uint32_t key = elem_key(z, mask_allows(r, v), r.invT, &y);
+    f(v, key, y);
+  }
+}
+
+// Lower bound T0 (a key) with at least k stream keys >= T0 in this tile.
+template <int EPT>
+__device__ __forceinline__ uint32_t first_threshold(const uint32_t (&key)[EPT], int k, BlockScratch& s) {
+  if (k <= 64) {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) mx = key[j] > mx ? key[j] : mx;
+    // the k-th largest thread maximum of a wave has k keys above it
+    const uint32_t srt = wave_sort_desc(mx);
+    const uint32_t wk = __shfl(srt, k - 1, 64);
+    return block_max(wk, s.red32);
+  }
+  // per-thread j-th largest (j = ceil(k / NT) <= 4), then the ceil(k/j)-th
+  // largest of those over the block
+  const int jj = (k + NT - 1) / NT;
+  uint32_t t4[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    uint32_t x = key[j];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t hi = x > t4[q] ? x : t4[q];
+      const uint32_t lo = x > t4[q] ? t4[q] : x;
+      t4[q] = hi;
+      x = lo;
+    }
+  }
+  const uint32_t aj = jj == 1 ? t4[0] : jj == 2 ? t4[1] : jj == 3 ? t4[2] : t4[3];
+  const unsigned rk = (unsigned)((k + jj - 1) / jj);
+  return block_select_kth<uint32_t, 32>([&](auto f) { f(aj); }, rk, s);
+}
+
+// Bit j set <=> element j of this thread's tile is a candidate: allowed and
+// composite (key, id) >= thr, tested on 32-bit halves.
+template <int EPT, int EPV>
+__device__ __forceinline__ uint32_t cand_mask(const uint32_t (&key)[EPT], int t0, u64 thr) {
+  const uint32_t tk = (uint32_t)(thr >> 32), tl = (uint32_t)thr;
+  uint32_t cm = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const uint32_t lo = 0xFFFFFFFFu - (uint32_t)tile_id(t0, j, EPV);
+    const bool c = key[j] != 0u && (key[j] > tk || (key[j] == tk && lo >= tl));
+    cm |= (uint32_t)c << j;
+  }
+  return cm;
+}
+
+template <typename Tin>
+__device__ __forceinline__ void greedy_chunk(const SampleArgs& a, const Row& r, const int2* hash,
+                                             const uint32_t* bitmap, BlockScratch& s,
+                                             uint4 (&raw)[Tile<Tin>::U], uint32_t (&mw)[Tile<Tin>::U]) {
+  using TL = Tile<Tin>;
+  const Tin* rowp = (const Tin*)a.logits + (long long)r.b * a.row_stride;
+  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)r.b * a.V : nullptr;
+  u64 best = 0;
+  uint32_t key[TL::EPT];
+  for (int t0 = r.v0; t0 < r.v1; t0 += TL::SIZE) {
+    tile_keys<Tin>(r, bitmap, a.BW, t0, raw, mw, key, post);
+    if (t0 + TL::SIZE < r.v1) tile_load<Tin>(rowp, r, t0 + TL::SIZE, a.aligned, raw, mw);
+#pragma unroll
+    for (int j = 0; j < TL::EPT; j++)
+      if (key[j]) {
+        const u64 c = comp_key(key[j], tile_id(t0, j, TL::EPV));
+        best = c > best ? c : best;
+      }
+  }
+  if (r.use_pen)
+    history_pass<Tin>(a, r, hash, rowp, [&](int v, uint32_t k, float y) {
+      if (post) post[v] = y;
+      if (k) {
+        const u64 c = comp_key(k, v);
+        best = c > best ? c : best;
+      }
+    });
+  best = block_max(best, s.red64);
+  if (a.S == 1) {
+    finalize_greedy(a, r.b, best);
+    return;
+  }
+  if (threadIdx.x == 0) {
+    a.ws[((long long)r.b * a.S + r.c) * a.ws_stride] = best;
+    a.ws_cnt[r.b * a.S + r.c] = best ? 1 : 0;
+  }
+}
+
+template <typename Tin>
+__device__ __forceinline__ void topk_chunk(const SampleArgs& a, const Row& r, const int2* hash,
+                                           const uint32_t* bitmap, u64* cand, BlockScratch& s,
+                                           uint4 (&raw)[Tile<Tin>::U], uint32_t (&mw)[Tile<Tin>::U]) {
+  using TL = Tile<Tin>;
+  const Tin* rowp = (const Tin*)a.logits + (long long)r.b * a.row_stride;
+  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)r.b * a.V : nullptr;
+  const int k = r.k;
+  if (threadIdx.x == 0) s.nbuf = 0;
+  u64 thr = 0;  // candidates: composite >= thr and key != 0
+  uint32_t key[TL::EPT];
+  bool first = true;
+  for (int t0 = r.v0; t0 < r.v1; t0 += TL::SIZE) {
+    tile_keys<Tin>(r, bitmap, a.BW, t0, raw, mw, key, post);
+    if (t0 + TL::SIZE < r.v1) tile_load<Tin>(rowp, r, t0 + TL::SIZE, a.aligned, raw, mw);
+    if (first) {
+      thr = (u64)first_threshold<TL::EPT>(key, k, s) << 32;
+      first = false;
+    }
+    uint32_t cm = cand_mask<TL::EPT, TL::EPV>(key, t0, thr);
+    const unsigned total = block_sum((unsigned)__popc(cm), s.red32);
+    const unsigned nbuf = s.nbuf;
+    if (nbuf + total > (unsigned)CAPB) {
+      // shrink: exact k-th composite over the buffer and this tile's candidates
+      const uint32_t cm_old = cm;
+      const u64 T = block_select_kth<u64, 64>(
+          [&](auto f) {
+            for (unsigned i = threadIdx.x; i < nbuf; i += NT) f(cand[i]);
+#pragma unroll
+            for (int j = 0; j < TL::EPT; j++)
+              if ((cm_old >> j) & 1u) f(comp_key(key[j], tile_id(t0, j, TL::EPV)));
+          },
+          (unsigned)k, s);
+      compact_ge(cand, (int)nbuf, T, s);
+      thr = T;
+      cm = cand_mask<TL::EPT, TL::EPV>(key, t0, thr);
+    }
+    {
+      const unsigned mine = (unsigned)__popc(cm);
+      const unsigned incl = wave_incl_scan(mine);
+      unsigned base = 0;
+      if (lane_id() == 63 && incl) base = atomicAdd(&s.nbuf, incl);
+      base = __shfl(base, 63, 64) + incl - mine;
+#pragma unroll
+      for (int j = 0; j < TL::EPT; j++)
+        if ((cm >> j) & 1u) {
+          if (base < (unsigned)a.capt) cand[base] = comp_key(key[j], tile_id(t0, j, TL::EPV));
+          base++;
+        }
+    }
+    __syncthreads();
+  }
+  if (r.use_pen) {
+    history_pass<Tin>(a, r, hash, rowp, [&](int v, uint32_t kk, float y) {
+      if (post) post[v] = y;
+      if (kk) {
+        const u64 c = comp_key(kk, v);
+        if (c >= thr) {
+          const unsigned p = atomicAdd(&s.nbuf, 1u);
+          if (p < (unsigned)a.capt) cand[p] = c;
+        }
+      }
+    });
+    __syncthreads();
+  }
+  int n = min((int)s.nbuf, a.capt);
+  if (k <= 64) {
+    if (n > 64) {
+      const u64 T = block_select_kth<u64, 64>(
+          [&](auto f) {
+            for (int i = threadIdx.x; i < n; i += NT) f(cand[i]);
+          },
+          (unsigned)k, s);
+      n = compact_ge(cand, n, T, s);  // exactly k <= 64
+    }
+    if (threadIdx.x < 64) {
+      const int lane = lane_id();
+      u64 x = lane < n ? cand[lane] : 0ull;
+      x = wave_sort_desc(x);
+      const int nk = n < k ? n : k;
+      if (a.S == 1) {
+        if (nk > 0) wave_finalize(a, r, x, nk);
+      } else {
+        if (lane < nk) a.ws[((long long)r.b * a.S + r.c) * a.ws_stride + lane] = x;
+        if (lane == 0) a.ws_cnt[r.b * a.S + r.c] = nk;
+      }
+    }
+    if (a.S == 1 && n == 0) finalize_topk(a, r, cand, 0, s);
+    return;
+  }
+  // k > 64: exact top-k via radix selection in LDS
+  if (n > k) {
+    const u64 T = block_select_kth<u64, 64>(
+        [&](auto f) {
+          for (int i = threadIdx.x; i < n; i += NT) f(cand[i]);
+        },
+        (unsigned)k, s);
+    n = compact_ge(cand, n, T, s);
+  }
+  if (a.S == 1) {
+    finalize_topk(a, r, cand, n, s);
+    return;
+  }
+  u64* dst = a.ws + ((long long)r.b * a.S + r.c) * a.ws_stride;
+  for (int i = threadIdx.x; i < n; i += NT) dst[i] = cand[i];
+  if (threadIdx.x == 0) a.ws_cnt[r.b * a.S + r.c] = n;
+}
+
+// ------------------------------------------------------------------ kernels
+
+// Greedy rows and rows with 1 <= top_k <= KMAX, one workgroup per (row,
+// chunk).  Rows that need the full path are left to full_kernel when
+// a.full_rows is set and get id -3 (outside the launch hint) otherwise.
+template <typename Tin>
+__global__ __launch_bounds__(NT) void chunk_kernel(SampleArgs a) {
+  TGS_DYN_SMEM(smem);
+  __shared__ BlockScratch s;
+  int2* hash = (int2*)(smem + a.off_hash);
+  uint32_t* bitmap = (uint32_t*)(smem + a.off_bitmap);
+  u64* cand = (u64*)(smem + a.off_cand);
+  const int b = blockIdx.x / a.S, c = blockIdx.x % a.S;
   if (b >= a.B) return;
   Row r;
   if (!row_setup(a, b, c, r)) {
     if (c == 0 && threadIdx.x == 0) {
       a.out[b] = -2;
-      if (a.dbg.counts) { a.dbg.counts[2 * b] = 0; a.dbg.counts[2 * b + 1] = 0; }
-      if (a.dbg.mass) { a.dbg.mass[2 * b] = 0; a.dbg.mass[2 * b + 1] = 0; }
-      if (a.dbg.cut_ids) a.dbg.cut_ids[b] = -1;
+      write_row_diag(a, b, 0, 0, 0, 0, -1);
     }
     return;
   }
-  Lds L;
-  L.hash = (int2*)(smem + a.off_hash);
-  L.bitmap = (uint32_t*)(smem + a.off_bitmap);
-  L.cand = (u64*)(smem + a.off_cand);
-  if (r.mode == 2) {
-    if (c != 0) return;
-    r.v0 = 0;
-    r.v1 = a.V;
-    if (r.use_pen) hash_build(a, r, L, false);  // whole row; lookups per id, no bitmap
-    full_path<Tin>(a, r, L, s);
+  if (outside_hint(a, r)) {
+    if (c == 0 && threadIdx.x == 0) {
+      a.out[b] = -3;
+      write_row_diag(a, b, 0, 0, 0, 0, -1);
+    }
+    return;
+  }
+  if (r.mode == 2) return;  // full_kernel
+  r.v0 = c * a.L;
+  r.v1 = min(a.V, r.v0 + a.L);
+  const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
+  uint4 raw[Tile<Tin>::U];
+  uint32_t mw[Tile<Tin>::U];
+  tile_load<Tin>(rowp, r, r.v0, a.aligned, raw, mw);  // in flight during the history build
+  if (r.use_pen) hash_build(a, r, hash, bitmap, a.BW);
+  if (r.mode == 0) greedy_chunk<Tin>(a, r, hash, bitmap, s, raw, mw);
+  else topk_chunk<Tin>(a, r, hash, bitmap, cand, s, raw, mw);
+}
+
+// Rows that need the full path (top_k disabled or above KMAX), one
+// workgroup per row; every other row returns at once.
+template <typename Tin>
+__global__ __launch_bounds__(NT) void full_kernel(SampleArgs a) {
+  TGS_DYN_SMEM(smem);
+  __shared__ BlockScratch s;
+  int2* hash = (int2*)(smem + a.off_hash);
+  u64* cand = (u64*)(smem + a.off_cand);
+  const int b = blockIdx.x;
+  if (b >= a.B) return;
+  Row r;
+  if (!row_setup(a, b, 0, r) || r.mode != 2) return;
+  if (r.use_pen) hash_build(a, r, hash, nullptr, 0);  // whole row, lookups per id
+  full_path<Tin>(a, r, hash, cand, s);
+}
+
+// Fast chunk kernel: every chunk is one tile (L <= 8192) and every row is
+// greedy or samples with top_k <= 64 (the launch hint guarantees it; rows
+// outside it get id -3).
+template <typename Tin>
+__global__ __launch_bounds__(NT) void fast_kernel(SampleArgs a) {
+  using TL = Tile<Tin>;
+  TGS_DYN_SMEM(smem);
+  __shared__ BlockScratch s;
+  int2* hash = (int2*)(smem + a.off_hash);
+  uint32_t* bitmap = (uint32_t*)(smem + a.off_bitmap);
+  u64* cand = (u64*)(smem + a.off_cand);
+  const int b = blockIdx.x / a.S, c = blockIdx.x % a.S;
+  if (b >= a.B) return;
+  Row r;
+  const bool valid = row_setup(a, b, c, r);
+  if (!valid || outside_hint(a, r)) {
+    if (c == 0 && threadIdx.x == 0) {
+      a.out[b] = valid ? -3 : -2;  // -3: row outside the launch hint
+      write_row_diag(a, b, 0, 0, 0, 0, -1);
+    }
     return;
   }
   r.v0 = c * a.L;
   r.v1 = min(a.V, r.v0 + a.L);
-  if (r.use_pen) hash_build(a, r, L, true);
-  if (r.mode == 0) greedy_chunk<Tin>(a, r, L, s);
-  else topk_chunk<Tin>(a, r, L, s);
+  const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
+  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)b * a.V : nullptr;
+  uint4 raw[TL::U];
+  uint32_t mw[TL::U];
+  tile_load<Tin>(rowp, r, r.v0, a.aligned, raw, mw);
+  if (r.use_pen) hash_build(a, r, hash, bitmap, a.BW);
+  uint32_t key[TL::EPT];
+  tile_keys<Tin>(r, bitmap, a.BW, r.v0, raw, mw, key, post);
+  if (r.mode == 0) {
+    u64 best = 0;
+#pragma unroll
+    for (int j = 0; j < TL::EPT; j++)
+      if (key[j]) {
+        const u64 cc = comp_key(key[j], tile_id(r.v0, j, TL::EPV));
+        best = cc > best ? cc : best;
+      }
+    if (r.use_pen)
+      history_pass<Tin>(a, r, hash, rowp, [&](int v, uint32_t kk, float y) {
+        if (post) post[v] = y;
+        if (kk) {
+          const u64 cc = comp_key(kk, v);
+          best = cc > best ? cc : best;
+        }
+      });
+    best = block_max(best, s.red64);
+    if (a.S == 1) {
+      finalize_greedy(a, b, best);
+    } else if (threadIdx.x == 0) {
+      a.ws[((long long)b * a.S + c) * a.ws_stride] = best;
+      a.ws_cnt[b * a.S + c] = best ? 1 : 0;
+    }
+    return;
+  }
+  const int k = r.k;
+  if (threadIdx.x == 0) s.nbuf = 0;
+  u64 thr = (u64)first_threshold<TL::EPT>(key, k, s) << 32;
+  uint32_t cm = cand_mask<TL::EPT, TL::EPV>(key, r.v0, thr);
+  if (block_sum((unsigned)__popc(cm), s.red32) > (unsigned)CAPB) {
+    // more ties at the threshold than the buffer holds: exact k-th composite
+    // of the tile (unique composites), leaving exactly k <= 64 candidates
+    const uint32_t cm_old = cm;
+    thr = block_select_kth<u64, 64>(
+        [&](auto f) {
+#pragma unroll
+          for (int j = 0; j < TL::EPT; j++)
+            if ((cm_old >> j) & 1u) f(comp_key(key[j], tile_id(r.v0, j, TL::EPV)));
+        },
+        (unsigned)k, s);
+    cm = cand_mask<TL::EPT, TL::EPV>(key, r.v0, thr);
+  }
+  {
+    const unsigned mine = (unsigned)__popc(cm);
+    const unsigned incl = wave_incl_scan(mine);
+    unsigned base = 0;
+    if (lane_id() == 63 && incl) base = atomicAdd(&s.nbuf, incl);
+    base = __shfl(base, 63, 64) + incl - mine;
+#pragma unroll
+    for (int j = 0; j < TL::EPT; j++)
+      if ((cm >> j) & 1u) {
+        const unsigned p = base + (unsigned)__popc(cm & ((1u << j) - 1u));
+        if (p < (unsigned)a.capt) cand[p] = comp_key(key[j], tile_id(r.v0, j, TL::EPV));
+      }
+  }
+  __syncthreads();
+  if (r.use_pen) {
+    history_pass<Tin>(a, r, hash, rowp, [&](int v, uint32_t kk, float y) {
+      if (post) post[v] = y;
+      if (kk) {
+        const u64 cc = comp_key(kk, v);
+        if (cc >= thr) {
+          const unsigned p = atomicAdd(&s.nbuf, 1u);
+          if (p < (unsigned)a.capt) cand[p] = cc;
+        }
+      }
+    });
+    __syncthreads();
+  }
+  int n = min((int)s.nbuf, a.capt);
+  if (n > 64) {
+    const u64 T = block_select_kth<u64, 64>(
+        [&](auto f) {
+          for (int i = threadIdx.x; i < n; i += NT) f(cand[i]);
+        },
+        (unsigned)k, s);
+    n = compact_ge(cand, n, T, s);  // exactly k <= 64
+  }
+  if (threadIdx.x < 64) {
+    const int lane = lane_id();
+    u64 x = lane < n ? cand[lane] : 0ull;
+    x = wave_sort_desc(x);
+    const int nk = n < k ? n : k;
+    if (a.S == 1) {
+      if (nk > 0) wave_finalize(a, r, x, nk);
+    } else {
+      if (lane < nk) a.ws[((long long)b * a.S + c) * a.ws_stride + lane] = x;
+      if (lane == 0) a.ws_cnt[b * a.S + c] = nk;
+    }
+  }
+  if (a.S == 1 && n == 0) finalize_topk(a, r, cand, 0, s);
+}
+
+// One workgroup per row: merge the S chunk results of greedy and candidate
+// rows and finish them.
+__global__ __launch_bounds__(NT) void merge_kernel(SampleArgs a) {
+  TGS_DYN_SMEM(smem);
+  __shared__ BlockScratch s;
+  __shared__ u64 wl[NW][64];
+  u64* cand = (u64*)(smem + a.off_cand);
+  const int b = blockIdx.x;
+  if (b >= a.B) return;
+  Row r;
+  if (!row_setup(a, b, 0, r) || r.mode == 2 || outside_hint(a, r)) return;
+  const int S = a.S;
+  const int WS = a.ws_stride;
+  const u64* src = a.ws + (long long)b * S * WS;
+  const int* cnt = a.ws_cnt + (long long)b * S;
+  if (r.mode == 0) {
+    u64 m = 0;
+    for (int c = threadIdx.x; c < S; c += NT) {
+      const u64 x = src[(long long)c * WS];
+      m = x > m ? x : m;
+    }
+    m = block_max(m, s.red64);
+    finalize_greedy(a, b, m);
+    return;
+  }
+  const int k = r.k;
+  int total = 0;
+  for (int c = 0; c < S; c++) total += cnt[c];
+  const int kk = total < k ? total : k;
+  if (k <= 64) {
+    const int w = threadIdx.x >> 6, lane = lane_id();
+    u64 acc = 0;
+    for (int c = w; c < S; c += NW) {
+      const int nc = cnt[c];
+      const u64 x = lane < nc ? src[(long long)c * WS + lane] : 0ull;
+      acc = wave_merge_top64(acc, x);
+    }
+    wl[w][lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+      acc = wl[0][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; w2++) acc = wave_merge_top64(acc, wl[w2][lane]);
+      if (kk > 0) wave_finalize(a, r, acc, kk);
+    }
+    if (kk == 0) finalize_topk(a, r, cand, 0, s);
+    return;
+  }
+  int n;
+  if (total <= a.capt) {
+    int off = 0;
+    for (int c = 0; c < S; c++) {
+      const int nc = cnt[c];
+      for (int i = threadIdx.x; i < nc; i += NT) cand[off + i] = src[(long long)c * WS + i];
+      off += nc;
+    }
+    __syncthreads();
+    n = total;
+    if (n > kk) {
+      const u64 T = block_select_kth<u64, 64>(
+          [&](auto f) {
+            for (int i = threadIdx.x; i < n; i += NT) f(cand[i]);
+          },
+          (unsigned)kk, s);
+      n = compact_ge(cand, n, T, s);
+    }
+  } else {
+    const u64 T = block_select_kth<u64, 64>(
+        [&](auto f) {
+          for (int c = 0; c < S; c++) {
+            const int nc = cnt[c];
+            for (int i = threadIdx.x; i < nc; i += NT) f(src[(long long)c * WS + i]);
+          }
+        },
+        (unsigned)kk, s);
+    if (threadIdx.x == 0) s.nbuf = 0;
+    __syncthreads();
+    for (int c = 0; c < S; c++) {
+      const int nc = cnt[c];
+      for (int i = threadIdx.x; i < nc; i += NT) {
+        const u64 x = src[(long long)c * WS + i];
+        if (x >= T) {
+          const unsigned p = atomicAdd(&s.nbuf, 1u);
+          if (p < (unsigned)a.capt) cand[p] = x;
+        }
+      }
+    }
+    __syncthreads();
+    n = min((int)s.nbuf, a.capt);
+  }
+  finalize_topk(a, r, cand, n, s);
 }
 
 // ------------------------------------------------------------------ spec verify
@@ -804,7 +1066,7 @@ struct SpecTile {
   static constexpr int EPL = NV * EPV;                // elements per lane per block
 };
 
-// element id of (vector i, element e) for this lane within block blk
+// id of (vector i, element e) for this lane within block blk
 template <typename Tin>
 __device__ __forceinline__ int spec_id(int blk, int i, int e) {
   constexpr int EPV = Elem<Tin>::EPV;
@@ -813,50 +1075,55 @@ __device__ __forceinline__ int spec_id(int blk, int i, int e) {
 
 template <typename Tin>
 __device__ __forceinline__ void spec_load_block(const Tin* rowp, int blk, int V, bool aligned,
-                                                float invT, float y[SpecTile<Tin>::EPL]) {
+                                                float invT, float (&y)[SpecTile<Tin>::EPL]) {
   using ST = SpecTile<Tin>;
+  uint4 raw[ST::NV];
 #pragma unroll
-  for (int i = 0; i < ST::NV; i++) {
-    const int v = spec_id<Tin>(blk, i, 0);
-    const uint4 raw = load_vec<Tin>(rowp, v, V, aligned);
+  for (int i = 0; i < ST::NV; i++) raw[i] = load_vec<Tin>(rowp, spec_id<Tin>(blk, i, 0), V, aligned);
+#pragma unroll
+  for (int i = 0; i < ST::NV; i++)
 #pragma unroll
     for (int e = 0; e < ST::EPV; e++) {
-      const float t = Elem<Tin>::get(raw, e) * invT;
+      const float t = Elem<Tin>::get(raw[i], e) * invT;
       y[i * ST::EPV + e] = (t > -__builtin_inff()) ? t : -__builtin_inff();
     }
-  }
 }
 
 struct SpecScratch {
   float mb[256];
   u64 qb[256];
-  u64 argb[NW];
   u64 wsum[256];
 };
 
 template <typename Tin>
-__device__ const Tin* spec_row_ptr(const SpecArgs& a, int b, int r) {
+__device__ __forceinline__ const Tin* spec_row_ptr(const SpecArgs& a, int b, int r) {
   const int k = a.k;
   if (r <= k) return (const Tin*)a.target + ((long long)b * (k + 1) + r) * a.V;
   return (const Tin*)a.draft + ((long long)b * k + (r - k - 1)) * a.V;
 }
 
-// Row statistics: writes m, S (canonical) and the argmax composite.
+// Row statistics: m, S (canonical) and the argmax composite (greedy rows).
 template <typename Tin>
-__device__ void spec_row_stats(const SpecArgs& a, const Tin* rowp, float invT, bool greedy,
-                               SpecScratch& ss, BlockScratch& s, float* m_out, float* S_out,
-                               u64* arg_out) {
+__global__ __launch_bounds__(NT) void spec_stats_kernel(SpecArgs a) {
   using ST = SpecTile<Tin>;
+  __shared__ BlockScratch s;
+  __shared__ SpecScratch ss;
+  const int R = 2 * a.k + 1;
+  const int b = blockIdx.x / R, r = blockIdx.x % R;
+  if (b >= a.B) return;
+  const float T = a.T[b];
+  if (__builtin_isnan(T)) return;  // reported by the verify kernel
+  const bool greedy = !(T > 0.0f);
+  if (greedy && r > a.k) return;  // draft rows unused by greedy verification
+  const float Tc = T > 1e-5f ? T : 1e-5f;
+  const float invT = greedy ? 1.0f : 1.0f / Tc;
+  const Tin* rowp = spec_row_ptr<Tin>(a, b, r);
   const int nb = (a.V + SPEC_BLOCK - 1) / SPEC_BLOCK;
   const int w = threadIdx.x >> 6;
   u64 arg = 0;
   for (int blk = w; blk < nb; blk += NW) {
     float y[ST::EPL];
     spec_load_block<Tin>(rowp, blk, a.V, a.aligned, invT, y);
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int j = 0; j < ST::EPL; j++) mx = fmaxf(mx, y[j]);
-    mx = wave_maxf(mx);
     if (greedy) {
 #pragma unroll
       for (int j = 0; j < ST::EPL; j++)
@@ -864,59 +1131,64 @@ __device__ void spec_row_stats(const SpecArgs& a, const Tin* rowp, float invT, b
           const u64 c = comp_key(tg_key(y[j]), spec_id<Tin>(blk, j / ST::EPV, j % ST::EPV));
           arg = c > arg ? c : arg;
         }
-    } else {
-      u64 q = 0;
-      if (mx > -__builtin_inff()) {
+      continue;
+    }
+    float mx = -__builtin_inff();
 #pragma unroll
-        for (int j = 0; j < ST::EPL; j++)
-          if (y[j] > -__builtin_inff()) q += tg_q40(tg_weight(y[j], mx));
-      }
-      q = wave_sum(q);
-      if (lane_id() == 0) {
-        ss.mb[blk] = mx;
-        ss.qb[blk] = q;
-      }
+    for (int j = 0; j < ST::EPL; j++) mx = fmaxf(mx, y[j]);
+    mx = wave_maxf(mx);
+    u64 q = 0;
+    if (mx > -__builtin_inff()) {
+#pragma unroll
+      for (int j = 0; j < ST::EPL; j++)
+        if (y[j] > -__builtin_inff()) q += tg_q40(tg_weight(y[j], mx));
+    }
+    q = wave_sum(q);
+    if (lane_id() == 0) {
+      ss.mb[blk] = mx;
+      ss.qb[blk] = q;
     }
   }
-  arg = block_max(arg, s.red64);
-  *arg_out = arg;
+  float* stat = a.ws_stats + ((long long)b * R + r) * 2;
   if (greedy) {
-    *m_out = 0.0f;
-    *S_out = 0.0f;
+    arg = block_max(arg, s.red64);
+    if (threadIdx.x == 0) a.ws_arg[(long long)b * R + r] = arg;
     return;
   }
   __syncthreads();
   // m and the pairwise tree over 256 (zero padded) block terms, in wave 0
-  float m = -__builtin_inff();
-  for (int i = 0; i < nb; i++) m = fmaxf(m, ss.mb[i]);
-  float S = 0.0f;
-  if (threadIdx.x < 64 && m > -__builtin_inff()) {
-    float t[4];
+  if (threadIdx.x < 64) {
+    float m = -__builtin_inff();
+    for (int i = 0; i < nb; i++) m = fmaxf(m, ss.mb[i]);
+    float S = 0.0f;
+    if (m > -__builtin_inff()) {
+      float t[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int i = 4 * lane_id() + j;
-      float v = 0.0f;
-      if (i < nb && ss.mb[i] > -__builtin_inff())
-        v = (tg_u64_to_f32(ss.qb[i]) * 0x1p-40f) * tg_weight(ss.mb[i], m);
-      t[j] = v;
+      for (int j = 0; j < 4; j++) {
+        const int i = 4 * lane_id() + j;
+        float v = 0.0f;
+        if (i < nb && ss.mb[i] > -__builtin_inff())
+          v = (tg_u64_to_f32(ss.qb[i]) * 0x1p-40f) * tg_weight(ss.mb[i], m);
+        t[j] = v;
+      }
+      float x = (t[0] + t[1]) + (t[2] + t[3]);
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) x = x + __shfl_xor(x, d, 64);
+      S = x;
     }
-    float x = (t[0] + t[1]) + (t[2] + t[3]);
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) x = x + __shfl_xor(x, d, 64);
-    S = x;
-  }
-  if (threadIdx.x == 0) {
-    *m_out = m;
-    *S_out = S;
+    if (threadIdx.x == 0) {
+      stat[0] = m;
+      stat[1] = S;
+    }
   }
 }
 
-// id-order draw over per-element masses given by wfn(v) (must be identical
-// in both passes).  Returns the first id whose inclusive prefix exceeds
-// floor(total * uq / 2^24); total computed here.
+// id-order draw over per-element masses wfn(v) (identical in both passes):
+// returns the first id whose inclusive prefix exceeds floor(total * uq / 2^24)
+// (-1 if the total is 0); *total_out gets the total.
 template <typename Tin, class W>
-__device__ int spec_draw_id_order(const SpecArgs& a, int V, uint32_t uq, W wfn, SpecScratch& ss,
-                                  BlockScratch& s, u64* total_out) {
+__device__ __forceinline__ int spec_draw_id_order(int V, uint32_t uq, W wfn, SpecScratch& ss,
+                                                  BlockScratch& s, u64* total_out) {
   using ST = SpecTile<Tin>;
   const int nb = (V + SPEC_BLOCK - 1) / SPEC_BLOCK;
   const int w = threadIdx.x >> 6;
@@ -959,13 +1231,12 @@ __device__ int spec_draw_id_order(const SpecArgs& a, int V, uint32_t uq, W wfn, 
     if (lane == 0) {
       s.sel = -1;
       s.found = total;
+      s.red64[0] = t;
     }
     if (first >= 0 && lane == first) {
       s.sel = found;
       s.mass_above = before;
-      s.need = 0;
     }
-    if (lane == 0) s.red64[0] = t;
   }
   __syncthreads();
   const int blk = s.sel;
@@ -973,7 +1244,6 @@ __device__ int spec_draw_id_order(const SpecArgs& a, int V, uint32_t uq, W wfn, 
   if (blk < 0) return -1;
   const u64 t = s.red64[0];
   const u64 before = s.mass_above;
-  // scan the chosen block in id order (wave 0)
   if (threadIdx.x < 64) {
     u64 run = before;
     int pick = -1;
@@ -1007,38 +1277,16 @@ __device__ int spec_draw_id_order(const SpecArgs& a, int V, uint32_t uq, W wfn, 
 }
 
 template <typename Tin>
-__global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
+__global__ __launch_bounds__(NT) void spec_verify_kernel(SpecArgs a) {
   __shared__ BlockScratch s;
   __shared__ SpecScratch ss;
   const int R = 2 * a.k + 1;
-  const int b = blockIdx.x / R, r = blockIdx.x % R;
+  const int b = blockIdx.x;
   if (b >= a.B) return;
   const float T = a.T[b];
-  const bool greedy = !(T > 0.0f);  // NaN handled in the verify step
+  const bool greedy = !(T > 0.0f);
   const float Tc = T > 1e-5f ? T : 1e-5f;
   const float invT = greedy ? 1.0f : 1.0f / Tc;
-  float* stat = a.ws_stats + ((long long)b * R + r) * 2;
-  u64* argp = a.ws_arg + (long long)b * R + r;
-  if (!(greedy && r > a.k) && !__builtin_isnan(T)) {
-    float m, S;
-    u64 arg;
-    spec_row_stats<Tin>(a, spec_row_ptr<Tin>(a, b, r), invT, greedy, ss, s, &m, &S, &arg);
-    if (threadIdx.x == 0) {
-      stat[0] = m;
-      stat[1] = S;
-      *argp = arg;
-    }
-  }
-  // handoff to the last workgroup of sequence b
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&a.counters[b], 1u);
-    s.last = (prev == (unsigned)R - 1u);
-  }
-  __syncthreads();
-  if (!s.last) return;
-  __threadfence();
   const int k = a.k;
   int* out = a.out + (long long)b * (k + 1);
   const float* stats = a.ws_stats + (long long)b * R * 2;
@@ -1058,7 +1306,6 @@ __global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
   if (bad) {
     for (int j = threadIdx.x; j <= k; j += NT) out[j] = j == 0 ? -2 : -1;
     if (threadIdx.x == 0) a.n_acc[b] = -1;
-    if (threadIdx.x == 0) a.counters[b] = 0u;
     return;
   }
   if (greedy) {
@@ -1073,7 +1320,6 @@ __global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
       }
       if (j == k) out[k] = args[k] ? comp_id(args[k]) : -1;
       a.n_acc[b] = j;
-      a.counters[b] = 0u;
     }
     return;
   }
@@ -1115,22 +1361,22 @@ __global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
   }
   __syncthreads();
   const int status = s.sel, j = s.binc_i;
+  __syncthreads();
   if (status < 0) {
     if (threadIdx.x == 0) {
       for (int i = 0; i <= k; i++) out[i] = -1;
       a.n_acc[b] = -1;
-      a.counters[b] = 0u;
     }
     return;
   }
   const uint32_t uq = (uint32_t)(ur * 16777216.0f);
+  const int V = a.V;
   int pick;
   if (status == 1) {
     const float mt = stats[2 * j], St = stats[2 * j + 1];
     const float md = stats[2 * (k + 1 + j)], Sd = stats[2 * (k + 1 + j) + 1];
     const Tin* tr = spec_row_ptr<Tin>(a, b, j);
     const Tin* dr = spec_row_ptr<Tin>(a, b, k + 1 + j);
-    const int V = a.V;
     auto resid = [&](int v) -> u64 {
       if (v >= V) return 0ull;
       float yt = Elem<Tin>::scalar(tr, v) * invT;
@@ -1141,9 +1387,9 @@ __global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
       const float pb = tg_weight(yd, md) / Sd;
       return tg_q40(fmaxf(pa - pb, 0.0f));
     };
-    u64 R;
-    pick = spec_draw_id_order<Tin>(a, V, uq, resid, ss, s, &R);
-    if (R < 110ull) {
+    u64 Rm;
+    pick = spec_draw_id_order<Tin>(V, uq, resid, ss, s, &Rm);
+    if (Rm < 110ull) {  // residual mass <= 1e-10: draw from the target row
       auto wt = [&](int v) -> u64 {
         if (v >= V) return 0ull;
         float yt = Elem<Tin>::scalar(tr, v) * invT;
@@ -1152,12 +1398,11 @@ __global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
       };
       __syncthreads();
       u64 Sq;
-      pick = spec_draw_id_order<Tin>(a, V, uq, wt, ss, s, &Sq);
+      pick = spec_draw_id_order<Tin>(V, uq, wt, ss, s, &Sq);
     }
   } else {
     const float mt = stats[2 * k];
     const Tin* tr = spec_row_ptr<Tin>(a, b, k);
-    const int V = a.V;
     auto wt = [&](int v) -> u64 {
       if (v >= V) return 0ull;
       float yt = Elem<Tin>::scalar(tr, v) * invT;
@@ -1165,39 +1410,61 @@ __global__ __launch_bounds__(NT) void spec_kernel(SpecArgs a) {
       return tg_q40(tg_weight(yt, mt));
     };
     u64 Sq;
-    pick = spec_draw_id_order<Tin>(a, V, uq, wt, ss, s, &Sq);
+    pick = spec_draw_id_order<Tin>(V, uq, wt, ss, s, &Sq);
   }
   if (threadIdx.x == 0) {
     out[j] = pick;
     a.n_acc[b] = j;
-    a.counters[b] = 0u;
   }
 }
 
 // ------------------------------------------------------------------ launchers
 
-template <typename Tin>
-static hipError_t launch_sample_t(const SampleArgs& a, int grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL(sample_kernel<Tin>, dim3(grid), dim3(NT), lds, st, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_sample(const SampleArgs& a, int dtype, int grid, size_t lds, hipStream_t st) {
-  return dtype == 1 ? launch_sample_t<uint16_t>(a, grid, lds, st) : launch_sample_t<float>(a, grid, lds, st);
+hipError_t launch_sample(const SampleArgs& a, int dtype, bool fast, size_t lds, hipStream_t st) {
+  const dim3 g(a.B * a.S), blk(NT);
+  if (dtype == 1) {
+    if (fast) hipLaunchKernelGGL(fast_kernel<uint16_t>, g, blk, lds, st, a);
+    else hipLaunchKernelGGL(chunk_kernel<uint16_t>, g, blk, lds, st, a);
+  } else {
+    if (fast) hipLaunchKernelGGL(fast_kernel<float>, g, blk, lds, st, a);
+    else hipLaunchKernelGGL(chunk_kernel<float>, g, blk, lds, st, a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (a.S > 1) {
+    hipLaunchKernelGGL(merge_kernel, dim3(a.B), blk, lds, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (a.full_rows) {
+    if (dtype == 1) hipLaunchKernelGGL(full_kernel<uint16_t>, dim3(a.B), blk, lds, st, a);
+    else hipLaunchKernelGGL(full_kernel<float>, dim3(a.B), blk, lds, st, a);
+    e = hipGetLastError();
+  }
+  return e;
 }
 
 hipError_t set_sample_lds_limit(size_t bytes) {
-  hipError_t e = hipFuncSetAttribute((const void*)sample_kernel<float>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-  if (e != hipSuccess) return e;
-  return hipFuncSetAttribute((const void*)sample_kernel<uint16_t>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  const void* fns[] = {(const void*)fast_kernel<float>,  (const void*)fast_kernel<uint16_t>,
+                       (const void*)chunk_kernel<float>, (const void*)chunk_kernel<uint16_t>,
+                       (const void*)full_kernel<float>,  (const void*)full_kernel<uint16_t>,
+                       (const void*)merge_kernel};
+  hipError_t e = hipSuccess;
+  for (const void* f : fns) {
+    hipError_t e2 = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e2 != hipSuccess) e = e2;
+  }
+  return e;
 }
 
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st) {
   const int grid = a.B * (2 * a.k + 1);
-  if (dtype == 1) hipLaunchKernelGGL(spec_kernel<uint16_t>, dim3(grid), dim3(NT), 0, st, a);
-  else hipLaunchKernelGGL(spec_kernel<float>, dim3(grid), dim3(NT), 0, st, a);
+  if (dtype == 1) hipLaunchKernelGGL(spec_stats_kernel<uint16_t>, dim3(grid), dim3(NT), 0, st, a);
+  else hipLaunchKernelGGL(spec_stats_kernel<float>, dim3(grid), dim3(NT), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (dtype == 1) hipLaunchKernelGGL(spec_verify_kernel<uint16_t>, dim3(a.B), dim3(NT), 0, st, a);
+  else hipLaunchKernelGGL(spec_verify_kernel<float>, dim3(a.B), dim3(NT), 0, st, a);
   return hipGetLastError();
 }
 

@@ -12,7 +12,7 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import ROW_PARAMS_DTYPE, TGS_BF16, TGS_F32, TgsDebug, TgsError
+from ._lib import ROW_PARAMS_DTYPE, TGS_BF16, TGS_F32, TgsDebug, TgsError, TgsHint
 
 
 def _torch():
@@ -38,6 +38,16 @@ def make_params(n, temperature=1.0, top_k=0, top_p=1.0, repetition=1.0, presence
     p["mask_state"] = mask_state
     p["flags"] = flags
     return p
+
+
+def batch_hint(params: np.ndarray, vocab: int) -> int:
+    """max_top_k of tgs_batch_hint computed from host params (see the C helper)."""
+    p = np.ascontiguousarray(params, dtype=ROW_PARAMS_DTYPE)
+    h = TgsHint()
+    rc = _lib.load().tgs_hint_from_params(p.ctypes.data_as(C.c_void_p), p.size, vocab, C.byref(h))
+    if rc != 0:
+        raise TgsError(rc, "tgs_hint_from_params")
+    return int(h.max_top_k)
 
 
 def params_to_device(params: np.ndarray, device):
@@ -96,10 +106,11 @@ class Sampler:
 
     # -------------------------------------------------------------- sample
     def sample(self, logits, params_dev, u, hist=None, hist_len=None, out=None, vocab=None,
-               debug=None, stream=None):
+               debug=None, stream=None, hint=None):
         """logits: [B, >=V] float32 or bfloat16 (row stride = logits.stride(0));
         params_dev: uint8 tensor of B*32 bytes (see params_to_device);
         u: float32 [B]; hist: int32 [B, hist_cap]; hist_len: int32 [B].
+        hint: max_top_k of the batch (see batch_hint) or None (general kernel).
         debug: dict of preallocated tensors (kept_ids, kept_probs, counts,
         mass, cut_ids, post_logits).  Returns the int32 [B] ids tensor."""
         torch = _torch()
@@ -125,10 +136,14 @@ class Sampler:
             kc = debug.get("kept_ids", debug.get("kept_probs"))
             dbg.kept_cap = 0 if kc is None else kc.shape[1]
         st = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
+        hs = None
+        if hint is not None:
+            hs = TgsHint()
+            hs.max_top_k = int(hint)
         rc = self._L.tgs_sample(
             self._h, _ptr(logits), dt, B, V, logits.stride(0), _ptr(hist), _ptr(hist_len), hist_cap,
-            _ptr(params_dev), _ptr(u), _ptr(out), C.byref(dbg) if dbg is not None else None,
-            C.c_void_p(st),
+            _ptr(params_dev), _ptr(u), _ptr(out), C.byref(hs) if hs is not None else None,
+            C.byref(dbg) if dbg is not None else None, C.c_void_p(st),
         )
         self._check(rc, "tgs_sample")
         return out
