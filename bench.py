@@ -190,7 +190,7 @@ def main():
                    "rotating_buffers": ROT, "timing": "graph replay" if graph is not None else "eager"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "alg_bytes_per_launch": alg_bytes, "kernel": "fast_kernel<float> + merge_kernel"},
+                     "alg_bytes_per_launch": alg_bytes, "kernel": "k64_kernel<float>"},
         "cpu_baseline": cpu,
         "id_agreement": agreement,
     }

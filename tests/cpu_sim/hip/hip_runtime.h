@@ -12,6 +12,7 @@
 // Device memory is host memory.
 #pragma once
 
+#include <atomic>
 #include <barrier>
 #include <cmath>
 #include <cstdint>
@@ -148,6 +149,17 @@ inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args
 #define hipLaunchKernelGGL(k, g, b, sh, st, ...) hipcpu::launch(k, dim3(g), dim3(b), (size_t)(sh), __VA_ARGS__)
 
 inline void __syncthreads() { hipcpu::block_ctx()->bar->arrive_and_wait(); }
+inline int __syncthreads_or(int pred) {
+  static std::atomic<int> acc{0};
+  __syncthreads();
+  if (pred) acc.store(1);
+  __syncthreads();
+  const int r = acc.load();
+  __syncthreads();
+  if (threadIdx.x == 0) acc.store(0);
+  __syncthreads();
+  return r;
+}
 inline int __lane_id() { return hipcpu::lane(); }
 
 template <typename T>
@@ -179,6 +191,7 @@ inline long long min(long long a, long long b) { return a < b ? a : b; }
 inline long long max(long long a, long long b) { return a > b ? a : b; }
 
 inline int __popc(unsigned x) { return __builtin_popcount(x); }
+inline int __popcll(unsigned long long x) { return __builtin_popcountll(x); }
 inline int __ffsll(long long x) { return __builtin_ffsll(x); }
 inline int __clzll(long long x) { return x ? __builtin_clzll((unsigned long long)x) : 64; }
 inline unsigned long long __umul64hi(unsigned long long a, unsigned long long b) {
@@ -200,6 +213,18 @@ inline int atomicMin(int* p, int v) {
   }
   return cur;
 }
+
+// Scoped atomics: device memory is host memory, so every scope is the
+// process; s_waitcnt has nothing to wait for.
+#define __HIP_MEMORY_SCOPE_WORKGROUP 3
+#define __HIP_MEMORY_SCOPE_AGENT 4
+template <typename T>
+inline void __hip_atomic_store(T* p, T v, int, int) { __atomic_store_n(p, v, __ATOMIC_SEQ_CST); }
+template <typename T>
+inline T __hip_atomic_load(const T* p, int, int) { return __atomic_load_n(p, __ATOMIC_SEQ_CST); }
+template <typename T, typename U>
+inline T __hip_atomic_fetch_add(T* p, U v, int, int) { return __atomic_fetch_add(p, (T)v, __ATOMIC_SEQ_CST); }
+inline void __builtin_amdgcn_s_waitcnt(int) {}
 
 // ---- runtime API on host memory ----
 inline int& hipcpu_last_error() {

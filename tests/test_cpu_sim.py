@@ -93,3 +93,49 @@ def test_rows_outside_the_hint_get_minus_3(sim, oracle):
         if hint < 50:
             expect[3] = -3
         np.testing.assert_array_equal(r["ids"], expect)
+
+
+def _k64_params(g, params, V):
+    ks = np.array([1, 2, 5, 40, 63, 64])
+    params["top_k"] = g.choice(ks[ks < V], size=params.size)
+    return params
+
+
+@pytest.mark.parametrize("split", [1, 2])
+def test_k64_multi_tile_chunks(sim, oracle, split):
+    """Fused top_k <= 64 kernel with chunks of several 8192-id tiles: later
+    tiles of ascending rows overflow the candidate buffer (exact fallback)."""
+    import tinygpt_amd as tg
+
+    g = np.random.default_rng(40 + split)
+    V = 20000
+    x, params, u, hist, hist_len = _batch(40 + split, 7, V, oracle)
+    params = _k64_params(g, params, V)
+    _check(sim, oracle, x, params, u, hist, hist_len, hint=tg.batch_hint(params, V), split=split, kept_cap=64)
+
+
+def test_k64_split_merge_16(sim, oracle):
+    """Sixteen chunks per row: the last workgroup merges sixteen lists."""
+    import tinygpt_amd as tg
+
+    g = np.random.default_rng(44)
+    V = 20000
+    x, params, u, hist, hist_len = _batch(44, 7, V, oracle)
+    params = _k64_params(g, params, V)
+    _check(sim, oracle, x, params, u, hist, hist_len, hint=tg.batch_hint(params, V), split=16, kept_cap=64)
+
+
+def test_k64_bf16_and_mask(sim, oracle):
+    import tinygpt_amd as tg
+    from tinygpt_amd import workloads as W
+
+    g = np.random.default_rng(45)
+    V = 3000
+    x, params, u, hist, hist_len = _batch(45, 8, V, oracle)
+    params = _k64_params(g, params, V)
+    table = g.integers(0, 1 << 32, size=(3, (V + 31) // 32), dtype=np.uint64).astype(np.uint32)
+    table[1] &= np.uint32(0x00010001)
+    table[2] = 0
+    params["mask_state"] = np.array([0, 1, 2, -1, 0, 1, -1, 2])
+    _check(sim, oracle, W.f32_to_bf16_bits(x), params, u, hist, hist_len, mask=table,
+           hint=tg.batch_hint(params, V), split=3, kept_cap=64)

@@ -27,6 +27,7 @@ struct tgs_ctx {
   unsigned long long* ws = nullptr;
   int* ws_cnt = nullptr;
   int ws_rows = 0;  // chunk lists of KMAX entries the workspace holds
+  unsigned* k64_cnt = nullptr;  // fused kernel arrival counters, one line per row
   uint32_t* mask_table = nullptr;
   int n_states = 0, mask_vocab = 0, mask_words = 0;
   float* spec_stats = nullptr;
@@ -80,6 +81,26 @@ void free_spec(tgs_ctx* h) {
   h->spec_arg = nullptr;
   h->spec_b = 0;
   h->spec_k = -1;
+}
+
+// Chunks per row of the fused top_k <= 64 kernel: every chunk is one tile
+// of at most kK64Tile ids (so S >= V / kK64Tile; with V <= kMaxVocab that is
+// at most kMaxSplit, the most lists the last workgroup of a row merges);
+// beyond that about two workgroups per CU with chunks of at least 2048
+// ids.  TGS_SPLIT raises the split (tuning).
+constexpr int kK64Tile = 16384;
+int choose_split_k64(const tgs_ctx* h, int B, int V) {
+  const int smin = (V + kK64Tile - 1) / kK64Tile;
+  int S;
+  const char* env = std::getenv("TGS_SPLIT");
+  if (env && std::atoi(env) > 0) {
+    S = std::min(std::atoi(env), kMaxSplit);
+  } else {
+    const long long target = 2LL * h->num_cu;
+    S = (int)std::min<long long>(kMaxSplit, std::max<long long>(1, (target + B - 1) / B));
+    while (S > 1 && (V + S - 1) / S < 2048) S--;
+  }
+  return std::max(S, smin);
 }
 
 // Chunks per row: about four workgroups per CU, chunks of at least one
@@ -157,11 +178,15 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
   h->ws_rows = std::max(max_batch, 4 * h->num_cu);
   hipError_t e = hipMalloc(&h->ws, sizeof(unsigned long long) * (size_t)h->ws_rows * tgs::KMAX);
   if (e == hipSuccess) e = hipMalloc(&h->ws_cnt, sizeof(int) * (size_t)h->ws_rows * (tgs::KMAX / 64));
+  const size_t cnt_bytes = sizeof(unsigned) * (size_t)max_batch * tgs::K64_CNT_STRIDE;
+  if (e == hipSuccess) e = hipMalloc(&h->k64_cnt, cnt_bytes);
+  if (e == hipSuccess) e = hipMemset(h->k64_cnt, 0, cnt_bytes);
   if (e == hipSuccess) {
     // raise the dynamic-LDS ceiling to the device limit; a runtime that
     // rejects the attribute keeps its default (calls that need more fail
     // with TGS_ETOOBIG / TGS_EHIP instead)
     if (tgs::set_sample_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_k64_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch) - 4096) != hipSuccess) (void)hipGetLastError();
     e = hipDeviceSynchronize();
   }
   if (e != hipSuccess) {
@@ -177,6 +202,7 @@ void tgs_destroy(tgs_handle h) {
   DeviceGuard g(h->device);
   if (h->ws) (void)hipFree(h->ws);
   if (h->ws_cnt) (void)hipFree(h->ws_cnt);
+  if (h->k64_cnt) (void)hipFree(h->k64_cnt);
   if (h->mask_table) (void)hipFree(h->mask_table);
   free_spec(h);
   delete h;
@@ -255,6 +281,7 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   a.B = B;
   a.V = V;
   a.aligned = ((uintptr_t)d_logits % 16 == 0) && (((uint64_t)row_stride * esz) % 16 == 0);
+  a.whole_vec = a.aligned && ((uint64_t)V * esz) % 16 == 0;
   a.hist = d_hist;
   a.hist_len = d_hist_len;
   a.hist_cap = hist_cap;
@@ -265,32 +292,45 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   a.mask_table = table_ok ? h->mask_table : nullptr;
   a.n_states = table_ok ? h->n_states : 0;
   a.mask_words = h->mask_words;
-  // Kernels: the fast chunk kernel when every row is greedy or has
-  // top_k <= 64 (one-tile chunks); the general chunk kernel otherwise, plus
-  // the full-path kernel when the hint allows rows without a usable top-k.
+  a.ws = h->ws;
+  a.ws_cnt = h->ws_cnt;
+  a.cnt = h->k64_cnt;
+  a.dbg = dz;
+  // Kernels: the fused top_k <= 64 kernel when the hint says every row is
+  // greedy or has top_k <= 64; otherwise the chunk kernel (+ merge kernel
+  // for split rows), plus the full-path kernel when the hint allows rows
+  // without a usable top-k.
   const int mk = hint ? hint->max_top_k : 0x7FFFFFFF;
-  bool fast = mk <= 64 && mk < V;
-  a.full_rows = (mk > tgs::KMAX || mk >= V) ? 1 : 0;
   a.hint_k = mk;
-  int S = 1, L = V;
-  if (fast) {
-    const int tile = 8192;
-    const int smin = (V + tile - 1) / tile;
-    S = std::max(smin, choose_split(h, B, V));
-    if ((long long)S * B * 64 > (long long)h->ws_rows * tgs::KMAX) fast = false;
-  }
-  if (fast) {
-    L = ((V + S - 1) / S + 1023) / 1024 * 1024;
-    a.ws_stride = 64;
-  } else {
-    S = choose_split(h, B, V);
-    L = S > 1 ? ((V + S - 1) / S + 1023) / 1024 * 1024 : V;
-    a.ws_stride = tgs::KMAX;
-  }
-  a.S = (V + L - 1) / L;
-  a.L = L;
   a.TS = hist_cap > 0 ? next_pow2(std::max(64, 2 * hist_cap)) : 0;
   a.ts_shift = a.TS ? 32 - log2i(a.TS) : 0;
+  if (mk <= 64 && mk < V) {
+    a.full_rows = 0;
+    const int S = choose_split_k64(h, B, V);
+    // whole tiles when the split allows them (their loads need no checks)
+    const int L = S == (V + kK64Tile - 1) / kK64Tile ? kK64Tile
+                                                     : std::min(kK64Tile, ((V + S - 1) / S + 63) / 64 * 64);
+    a.S = (V + L - 1) / L;
+    a.L = L;
+    a.BW = tgs::K64_BITMAP_WORDS;
+    a.off_hash = 0;
+    a.off_bitmap = a.TS * 8;
+    a.off_cand = a.off_bitmap + a.BW * 4;
+    a.capt = tgs::K64_CAP;
+    a.ws_stride = 64;
+    const size_t lds = (size_t)a.off_cand + (size_t)tgs::K64_CAND_ENTRIES * 8;
+    if (lds + sizeof(tgs::BlockScratch) + 4096 > h->lds_limit)
+      return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
+    hipError_t e = tgs::launch_k64(a, dt, lds, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
+    return TGS_OK;
+  }
+  a.full_rows = (mk > tgs::KMAX || mk >= V) ? 1 : 0;
+  const int S = choose_split(h, B, V);
+  const int L = S > 1 ? ((V + S - 1) / S + 1023) / 1024 * 1024 : V;
+  a.ws_stride = tgs::KMAX;
+  a.S = (V + L - 1) / L;
+  a.L = L;
   a.BW = hist_cap > 0 ? (L + 31) / 32 : 0;
   a.capt = tgs::CAPB + hist_cap;
   a.off_hash = 0;
@@ -299,10 +339,7 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   const size_t lds = (size_t)a.off_cand + (size_t)a.capt * 8;
   if (lds + sizeof(tgs::BlockScratch) > h->lds_limit)
     return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
-  a.ws = h->ws;
-  a.ws_cnt = h->ws_cnt;
-  a.dbg = dz;
-  hipError_t e = tgs::launch_sample(a, dt, fast, lds, (hipStream_t)stream);
+  hipError_t e = tgs::launch_sample(a, dt, lds, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
   return TGS_OK;
 }

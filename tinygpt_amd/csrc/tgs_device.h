@@ -8,7 +8,9 @@
 //     (atomics, trees, split rows) gives the same result;
 //   * order keys map floats to uint32 monotonically (-0 folded onto +0);
 //     composite keys (key(y) << 32 | ~id) order by (y desc, id asc).
-// Wavefronts are 64 lanes; blocks are NT = 256 threads (4 waves).
+// Wavefronts are 64 lanes.  Most kernels run NT = 256 threads (4 waves); the
+// block primitives take the block size as a template parameter (BS, at most
+// 1024 threads).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -141,8 +143,8 @@ __device__ __forceinline__ float wave_maxf(float x) {
 struct BlockScratch {
   unsigned hc[256];        // radix histogram: counts
   u64 hm[256];             // radix histogram: masses
-  u64 red64[NW];
-  unsigned red32[NW];
+  u64 red64[16];
+  unsigned red32[16];
   int sel, binc_i;
   unsigned need;
   u64 mass_above, found;
@@ -152,7 +154,7 @@ struct BlockScratch {
   int last;
 };
 
-template <typename T>
+template <typename T, int BS = NT>
 __device__ __forceinline__ T block_sum(T x, T* red) {
   x = wave_sum(x);
   const int w = threadIdx.x >> 6;
@@ -161,11 +163,11 @@ __device__ __forceinline__ T block_sum(T x, T* red) {
   __syncthreads();
   T t = 0;
 #pragma unroll
-  for (int i = 0; i < NW; i++) t += red[i];
+  for (int i = 0; i < BS / 64; i++) t += red[i];
   return t;
 }
 
-template <typename T>
+template <typename T, int BS = NT>
 __device__ __forceinline__ T block_max(T x, T* red) {
   x = wave_max(x);
   const int w = threadIdx.x >> 6;
@@ -174,7 +176,7 @@ __device__ __forceinline__ T block_max(T x, T* red) {
   __syncthreads();
   T t = red[0];
 #pragma unroll
-  for (int i = 1; i < NW; i++) t = red[i] > t ? red[i] : t;
+  for (int i = 1; i < BS / 64; i++) t = red[i] > t ? red[i] : t;
   return t;
 }
 
@@ -184,12 +186,12 @@ __device__ __forceinline__ T block_max(T x, T* red) {
 // equals the kth largest key, or a prefix of it with zeroed low bits when
 // the keys of that prefix number exactly what is needed (then
 // #{key >= T} == kth).  kth >= 1 and the multiset holds >= kth keys.
-template <typename K, int NBITS, class Enum>
+template <typename K, int NBITS, int BS = NT, class Enum>
 __device__ __forceinline__ K block_select_kth(Enum en, unsigned kth, BlockScratch& s) {
   K prefix = 0, pmask = 0;
   unsigned need = kth;
   for (int shift = NBITS - 8; shift >= 0; shift -= 8) {
-    for (int i = threadIdx.x; i < 256; i += NT) s.hc[i] = 0;
+    for (int i = threadIdx.x; i < 256; i += BS) s.hc[i] = 0;
     __syncthreads();
     en([&](K x) {
       if ((x & pmask) == prefix) atomicAdd(&s.hc[(unsigned)(x >> shift) & 255u], 1u);
@@ -238,7 +240,7 @@ __device__ __forceinline__ K block_select_kth(Enum en, unsigned kth, BlockScratc
 // `en(f)` calls f(key, mass) for every key this thread owns.  Returns the
 // element's key; *before gets the mass strictly ahead of it, *rank the
 // number of elements strictly ahead of it.
-template <class Enum>
+template <int BS = NT, class Enum>
 __device__ __forceinline__ u64 block_mass_select(Enum en, u64 target, BlockScratch& s, u64* before,
                                  unsigned* rank) {
   u64 prefix = 0, pmask = 0;
@@ -246,7 +248,7 @@ __device__ __forceinline__ u64 block_mass_select(Enum en, u64 target, BlockScrat
   unsigned cnt_above = 0;
   bool single = false;
   for (int shift = 56; shift >= 0; shift -= 8) {
-    for (int i = threadIdx.x; i < 256; i += NT) {
+    for (int i = threadIdx.x; i < 256; i += BS) {
       s.hc[i] = 0;
       s.hm[i] = 0;
     }

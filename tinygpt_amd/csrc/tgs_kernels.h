@@ -8,11 +8,21 @@
 
 namespace tgs {
 
+// Fused top_k <= 64 kernel: block size, candidate buffer entries, bitmap
+// words of a 16384-id tile, and the stride (in unsigned words) between the
+// per-row arrival counters (one 128-byte line each).
+constexpr int K64_NT = 256;
+constexpr int K64_CAP = 1024;
+constexpr int K64_CAND_ENTRIES = 8 * K64_NT + 512 + K64_CAP + 16;  // thread slots, history, compacted
+constexpr int K64_BITMAP_WORDS = 512;
+constexpr int K64_CNT_STRIDE = 32;
+
 struct SampleArgs {
   const void* logits;
   long long row_stride;  // elements
   int B, V;
   int aligned;           // rows start 16-byte aligned: vector loads
+  int whole_vec;         // aligned and V a multiple of the 16-byte vector: a vector lies wholly inside or outside a row
   const int* hist;
   const int* hist_len;
   int hist_cap;
@@ -29,6 +39,7 @@ struct SampleArgs {
   unsigned long long* ws;  // [B*S][ws_stride] chunk candidate lists
   int ws_stride;         // entries per chunk list (64 fast variant, KMAX otherwise)
   int* ws_cnt;           // [B*S]
+  unsigned* cnt;         // fused kernel: [B * K64_CNT_STRIDE] arrival counters (zero between calls)
   int full_rows;         // 1: full_kernel runs after the chunk kernels
   int hint_k;            // the launch hint's max_top_k (INT_MAX without a hint)
   tgs_debug dbg;
@@ -49,11 +60,13 @@ struct SpecArgs {
   unsigned long long* ws_arg;  // [B][2k+1] argmax composite
 };
 
-// Launches the chunk kernel (fast: the one-tile top_k <= 64 kernel), the
-// merge kernel when rows are split (a.S > 1) and the full-path kernel when
-// a.full_rows is set, in that order on stream st.
-hipError_t launch_sample(const SampleArgs& a, int dtype, bool fast, size_t lds, hipStream_t st);
+// Launches the chunk kernel, the merge kernel when rows are split (a.S > 1)
+// and the full-path kernel when a.full_rows is set, in that order on st.
+hipError_t launch_sample(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
 hipError_t set_sample_lds_limit(size_t bytes);
+// The fused kernel for batches of greedy rows and rows with top_k <= 64.
+hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
+hipError_t set_k64_lds_limit(size_t bytes);
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
 
 }  // namespace tgs

@@ -35,234 +35,9 @@
 // the residual or bonus draw.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
+#include "tgs_row.h"
 
 namespace tgs {
-
-// ------------------------------------------------------------------ loads
-
-template <typename Tin>
-struct Elem;
-template <>
-struct Elem<float> {
-  static constexpr int EPV = 4;
-  static constexpr uint32_t NAN_BITS = 0x7FC00000u;
-  __device__ static __forceinline__ float get(const uint4& r, int e) {
-    const uint32_t w = e == 0 ? r.x : e == 1 ? r.y : e == 2 ? r.z : r.w;
-    return tg_u2f(w);
-  }
-  __device__ static __forceinline__ float scalar(const void* p, long long i) {
-    return ((const float*)p)[i];
-  }
-};
-template <>
-struct Elem<uint16_t> {  // bf16 bits
-  static constexpr int EPV = 8;
-  static constexpr uint32_t NAN_BITS = 0x7FC07FC0u;
-  __device__ static __forceinline__ float get(const uint4& r, int e) {
-    const uint32_t w = (e >> 1) == 0 ? r.x : (e >> 1) == 1 ? r.y : (e >> 1) == 2 ? r.z : r.w;
-    return tg_u2f((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
-  }
-  __device__ static __forceinline__ float scalar(const void* p, long long i) {
-    return tg_u2f((uint32_t)((const uint16_t*)p)[i] << 16);
-  }
-};
-
-// Load EPV consecutive logits starting at id v (v a multiple of EPV) from
-// row pointer rowp; ids >= vend read as NaN (never allowed).
-template <typename Tin>
-__device__ __forceinline__ uint4 load_vec(const Tin* rowp, int v, int vend, bool aligned) {
-  constexpr int EPV = Elem<Tin>::EPV;
-  if (aligned && v + EPV <= vend) return *(const uint4*)(rowp + v);
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) w[i] = Elem<Tin>::NAN_BITS;
-  if (sizeof(Tin) == 4) {
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-      if (v + e < vend) w[e] = ((const uint32_t*)rowp)[v + e];
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-      if (v + e < vend) {
-        const uint32_t h = ((const uint16_t*)rowp)[v + e];
-        w[e >> 1] = (e & 1) ? ((w[e >> 1] & 0xFFFFu) | (h << 16)) : ((w[e >> 1] & 0xFFFF0000u) | h);
-      }
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
-// ------------------------------------------------------------------ row state
-
-struct Row {
-  int b, c;
-  int mode;  // 0 greedy, 1 candidate top-k, 2 full
-  float invT;
-  int k;
-  float top_p, rep, pres, freq, u;
-  bool use_pen;
-  int H;
-  const int* hrow;
-  const uint32_t* mrow;  // nullptr: no mask
-  int v0, v1;            // chunk id range [v0, v1)
-};
-
-__device__ __forceinline__ bool row_setup(const SampleArgs& a, int b, int c, Row& r) {
-  const tgs_row_params p = a.params[b];
-  r.b = b;
-  r.c = c;
-  const float T = p.temperature;
-  if (__builtin_isnan(T)) return false;
-  const bool greedy = (p.flags & TGS_FLAG_GREEDY) || T <= 0.0f;
-  r.invT = 1.0f;
-  r.u = 0.0f;
-  if (!greedy) {
-    if (!__builtin_isfinite(T)) return false;
-    r.invT = 1.0f / T;
-    if (!__builtin_isfinite(r.invT)) return false;
-    if (__builtin_isnan(p.top_p) || p.top_p <= 0.0f) return false;
-    r.u = a.u[b];
-    if (__builtin_isnan(r.u) || r.u < 0.0f || r.u >= 1.0f) return false;
-  }
-  if (!(p.repetition > 0.0f) || !__builtin_isfinite(p.repetition)) return false;
-  if (!__builtin_isfinite(p.presence) || !__builtin_isfinite(p.frequency)) return false;
-  r.H = a.hist_len ? a.hist_len[b] : a.hist_cap;
-  if (r.H < 0 || r.H > a.hist_cap) return false;
-  r.hrow = a.hist ? a.hist + (long long)b * a.hist_cap : nullptr;
-  r.mrow = nullptr;
-  if (p.mask_state >= 0) {
-    if (p.mask_state >= a.n_states) return false;
-    r.mrow = a.mask_table + (long long)p.mask_state * a.mask_words;
-  }
-  r.k = p.top_k;
-  r.top_p = p.top_p;
-  r.rep = p.repetition;
-  r.pres = p.presence;
-  r.freq = p.frequency;
-  const bool neutral = (p.repetition == 1.0f && p.presence == 0.0f && p.frequency == 0.0f);
-  r.use_pen = (r.H > 0 && !neutral && r.hrow != nullptr);
-  if (greedy) r.mode = 0;
-  else if (p.top_k >= 1 && p.top_k <= KMAX && p.top_k < a.V) r.mode = 1;
-  else r.mode = 2;
-  r.v0 = 0;
-  r.v1 = a.V;
-  return true;
-}
-
-// A sampling row outside the launch hint: top-k above hint_k, or no usable
-// top-k while the full-path kernel is not launched.  Such rows get id -3.
-__device__ __forceinline__ bool outside_hint(const SampleArgs& a, const Row& r) {
-  return (r.mode == 1 && r.k > a.hint_k) || (r.mode == 2 && !a.full_rows);
-}
-
-// ------------------------------------------------------------------ history
-
-__device__ __forceinline__ unsigned hash_slot(int id, int shift) {
-  return ((unsigned)id * 2654435761u) >> shift;
-}
-
-// Insert the row's history ids that fall in [r.v0, r.v1) into the LDS hash
-// (id -> count) and, when BW > 0, the chunk bitmap.
-__device__ __forceinline__ void hash_build(const SampleArgs& a, const Row& r, int2* hash,
-                                           uint32_t* bitmap, int BW) {
-  for (int i = threadIdx.x; i < a.TS; i += NT) hash[i] = make_int2(-1, 0);
-  for (int i = threadIdx.x; i < BW; i += NT) bitmap[i] = 0u;
-  __syncthreads();
-  const unsigned tmask = (unsigned)a.TS - 1u;
-  for (int j = threadIdx.x; j < r.H; j += NT) {
-    const int id = r.hrow[j];
-    if (id < r.v0 || id >= r.v1 || id >= a.V) continue;
-    unsigned h = hash_slot(id, a.ts_shift);
-    for (;;) {
-      const int old = atomicCAS(&hash[h].x, -1, id);
-      if (old == -1 || old == id) {
-        atomicAdd(&hash[h].y, 1);
-        break;
-      }
-      h = (h + 1) & tmask;
-    }
-    if (BW) atomicOr(&bitmap[(id - r.v0) >> 5], 1u << ((id - r.v0) & 31));
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ int hash_count(const int2* hash, int TS, int shift, int id) {
-  const unsigned tmask = (unsigned)TS - 1u;
-  unsigned h = hash_slot(id, shift);
-  for (;;) {
-    const int2 e = hash[h];
-    if (e.x == id) return e.y;
-    if (e.x == -1) return 0;
-    h = (h + 1) & tmask;
-  }
-}
-
-// Penalised logit of a history id (count c > 0): CTRL repetition, then
-// frequency per occurrence, then presence.
-__device__ __forceinline__ float penalise(float z, int c, const Row& r) {
-  if (r.rep != 1.0f) z = (z > 0.0f) ? z / r.rep : z * r.rep;
-  z = z - r.freq * (float)c;
-  z = z - r.pres;
-  return z;
-}
-
-__device__ __forceinline__ bool mask_allows(const Row& r, int v) {
-  return r.mrow == nullptr || ((r.mrow[v >> 5] >> (v & 31)) & 1u);
-}
-
-// Key of one element (0 when not allowed); *y_out gets the canonical logit.
-__device__ __forceinline__ uint32_t elem_key(float z, bool allowed, float invT, float* y_out) {
-  const float y = z * invT;
-  const bool ok = allowed && (y > -__builtin_inff());
-  *y_out = ok ? y : -__builtin_inff();
-  return ok ? tg_key(y) : 0u;
-}
-
-// ------------------------------------------------------------------ finalize
-
-__device__ __forceinline__ void write_row_diag(const SampleArgs& a, int b, int n1, int n2, u64 S, u64 Sp, int cut) {
-  if (a.dbg.counts) { a.dbg.counts[2 * b] = n1; a.dbg.counts[2 * b + 1] = n2; }
-  if (a.dbg.mass) { a.dbg.mass[2 * b] = S; a.dbg.mass[2 * b + 1] = Sp; }
-  if (a.dbg.cut_ids) a.dbg.cut_ids[b] = cut;
-}
-
-// Called by one whole wave: x is this lane's entry of the kept list sorted
-// by (logit desc, id asc) (lane i = rank i), n in [1, 64] valid entries.
-__device__ __forceinline__ void wave_finalize(const SampleArgs& a, const Row& r, u64 x, int n) {
-  const int lane = lane_id();
-  const int b = r.b;
-  const float y = comp_y(x);
-  const float m = __shfl(y, 0, 64);
-  const u64 q = lane < n ? tg_q40(tg_weight(y, m)) : 0ull;
-  const u64 C = wave_incl_scan(q);
-  const u64 S = __shfl(C, n - 1, 64);
-  int istar = n - 1;
-  if (r.top_p < 1.0f) {
-    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
-    const u64 P = mul_shr24(S, pq);
-    const u64 bal = __ballot(lane < n && C >= P);
-    istar = __ffsll((long long)bal) - 1;
-  }
-  const u64 Sp = __shfl(C, istar, 64);
-  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
-  const u64 t = mul_shr24(Sp, uq);
-  const u64 bal2 = __ballot(lane <= istar && C > t);
-  const int pick = bal2 ? __ffsll((long long)bal2) - 1 : istar;
-  const u64 xp = __shfl(x, pick, 64);
-  const u64 xc = __shfl(x, istar, 64);
-  if (lane == 0) {
-    a.out[b] = comp_id(xp);
-    write_row_diag(a, b, n, istar + 1, S, Sp, comp_id(xc));
-  }
-  if (a.dbg.kept_ids) {
-    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
-    for (int i = lane; i < a.dbg.kept_cap; i += 64) kid[i] = (i < n) ? comp_id(x) : -1;
-  }
-  if (a.dbg.kept_probs) {
-    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
-    const float fs = tg_u64_to_f32(Sp);
-    for (int i = lane; i < a.dbg.kept_cap; i += 64) kp[i] = (i <= istar) ? tg_u64_to_f32(q) / fs : 0.0f;
-  }
-}
 
 // kept candidates in cand[0, n) (unsorted, unique composites, n <= KMAX):
 // sort, masses, top-p, draw.  cand must hold 2*KMAX entries.
@@ -339,21 +114,6 @@ __device__ __forceinline__ void finalize_topk(const SampleArgs& a, const Row& r,
   __syncthreads();
 }
 
-__device__ __forceinline__ void finalize_greedy(const SampleArgs& a, int b, u64 best) {
-  const int id = best ? comp_id(best) : -1;
-  if (threadIdx.x == 0) {
-    a.out[b] = id;
-    write_row_diag(a, b, id >= 0, id >= 0, 0, 0, id);
-  }
-  if (a.dbg.kept_ids) {
-    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kid[i] = (i == 0) ? id : -1;
-  }
-  if (a.dbg.kept_probs) {
-    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) kp[i] = (i == 0 && id >= 0) ? 1.0f : 0.0f;
-  }
-}
 
 // Keep the entries >= T of buf[0, n) in place (order not preserved); returns
 // the new count.  Batches of 4*NT entries: a batch is read completely before
@@ -839,131 +599,6 @@ __global__ __launch_bounds__(NT) void full_kernel(SampleArgs a) {
   full_path<Tin>(a, r, hash, cand, s);
 }
 
-// Fast chunk kernel: every chunk is one tile (L <= 8192) and every row is
-// greedy or samples with top_k <= 64 (the launch hint guarantees it; rows
-// outside it get id -3).
-template <typename Tin>
-__global__ __launch_bounds__(NT) void fast_kernel(SampleArgs a) {
-  using TL = Tile<Tin>;
-  TGS_DYN_SMEM(smem);
-  __shared__ BlockScratch s;
-  int2* hash = (int2*)(smem + a.off_hash);
-  uint32_t* bitmap = (uint32_t*)(smem + a.off_bitmap);
-  u64* cand = (u64*)(smem + a.off_cand);
-  const int b = blockIdx.x / a.S, c = blockIdx.x % a.S;
-  if (b >= a.B) return;
-  Row r;
-  const bool valid = row_setup(a, b, c, r);
-  if (!valid || outside_hint(a, r)) {
-    if (c == 0 && threadIdx.x == 0) {
-      a.out[b] = valid ? -3 : -2;  // -3: row outside the launch hint
-      write_row_diag(a, b, 0, 0, 0, 0, -1);
-    }
-    return;
-  }
-  r.v0 = c * a.L;
-  r.v1 = min(a.V, r.v0 + a.L);
-  const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
-  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)b * a.V : nullptr;
-  uint4 raw[TL::U];
-  uint32_t mw[TL::U];
-  tile_load<Tin>(rowp, r, r.v0, a.aligned, raw, mw);
-  if (r.use_pen) hash_build(a, r, hash, bitmap, a.BW);
-  uint32_t key[TL::EPT];
-  tile_keys<Tin>(r, bitmap, a.BW, r.v0, raw, mw, key, post);
-  if (r.mode == 0) {
-    u64 best = 0;
-#pragma unroll
-    for (int j = 0; j < TL::EPT; j++)
-      if (key[j]) {
-        const u64 cc = comp_key(key[j], tile_id(r.v0, j, TL::EPV));
-        best = cc > best ? cc : best;
-      }
-    if (r.use_pen)
-      history_pass<Tin>(a, r, hash, rowp, [&](int v, uint32_t kk, float y) {
-        if (post) post[v] = y;
-        if (kk) {
-          const u64 cc = comp_key(kk, v);
-          best = cc > best ? cc : best;
-        }
-      });
-    best = block_max(best, s.red64);
-    if (a.S == 1) {
-      finalize_greedy(a, b, best);
-    } else if (threadIdx.x == 0) {
-      a.ws[((long long)b * a.S + c) * a.ws_stride] = best;
-      a.ws_cnt[b * a.S + c] = best ? 1 : 0;
-    }
-    return;
-  }
-  const int k = r.k;
-  if (threadIdx.x == 0) s.nbuf = 0;
-  u64 thr = (u64)first_threshold<TL::EPT>(key, k, s) << 32;
-  uint32_t cm = cand_mask<TL::EPT, TL::EPV>(key, r.v0, thr);
-  if (block_sum((unsigned)__popc(cm), s.red32) > (unsigned)CAPB) {
-    // more ties at the threshold than the buffer holds: exact k-th composite
-    // of the tile (unique composites), leaving exactly k <= 64 candidates
-    const uint32_t cm_old = cm;
-    thr = block_select_kth<u64, 64>(
-        [&](auto f) {
-#pragma unroll
-          for (int j = 0; j < TL::EPT; j++)
-            if ((cm_old >> j) & 1u) f(comp_key(key[j], tile_id(r.v0, j, TL::EPV)));
-        },
-        (unsigned)k, s);
-    cm = cand_mask<TL::EPT, TL::EPV>(key, r.v0, thr);
-  }
-  {
-    const unsigned mine = (unsigned)__popc(cm);
-    const unsigned incl = wave_incl_scan(mine);
-    unsigned base = 0;
-    if (lane_id() == 63 && incl) base = atomicAdd(&s.nbuf, incl);
-    base = __shfl(base, 63, 64) + incl - mine;
-#pragma unroll
-    for (int j = 0; j < TL::EPT; j++)
-      if ((cm >> j) & 1u) {
-        const unsigned p = base + (unsigned)__popc(cm & ((1u << j) - 1u));
-        if (p < (unsigned)a.capt) cand[p] = comp_key(key[j], tile_id(r.v0, j, TL::EPV));
-      }
-  }
-  __syncthreads();
-  if (r.use_pen) {
-    history_pass<Tin>(a, r, hash, rowp, [&](int v, uint32_t kk, float y) {
-      if (post) post[v] = y;
-      if (kk) {
-        const u64 cc = comp_key(kk, v);
-        if (cc >= thr) {
-          const unsigned p = atomicAdd(&s.nbuf, 1u);
-          if (p < (unsigned)a.capt) cand[p] = cc;
-        }
-      }
-    });
-    __syncthreads();
-  }
-  int n = min((int)s.nbuf, a.capt);
-  if (n > 64) {
-    const u64 T = block_select_kth<u64, 64>(
-        [&](auto f) {
-          for (int i = threadIdx.x; i < n; i += NT) f(cand[i]);
-        },
-        (unsigned)k, s);
-    n = compact_ge(cand, n, T, s);  // exactly k <= 64
-  }
-  if (threadIdx.x < 64) {
-    const int lane = lane_id();
-    u64 x = lane < n ? cand[lane] : 0ull;
-    x = wave_sort_desc(x);
-    const int nk = n < k ? n : k;
-    if (a.S == 1) {
-      if (nk > 0) wave_finalize(a, r, x, nk);
-    } else {
-      if (lane < nk) a.ws[((long long)b * a.S + c) * a.ws_stride + lane] = x;
-      if (lane == 0) a.ws_cnt[b * a.S + c] = nk;
-    }
-  }
-  if (a.S == 1 && n == 0) finalize_topk(a, r, cand, 0, s);
-}
-
 // One workgroup per row: merge the S chunk results of greedy and candidate
 // rows and finish them.
 __global__ __launch_bounds__(NT) void merge_kernel(SampleArgs a) {
@@ -1420,15 +1055,10 @@ __global__ __launch_bounds__(NT) void spec_verify_kernel(SpecArgs a) {
 
 // ------------------------------------------------------------------ launchers
 
-hipError_t launch_sample(const SampleArgs& a, int dtype, bool fast, size_t lds, hipStream_t st) {
+hipError_t launch_sample(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
   const dim3 g(a.B * a.S), blk(NT);
-  if (dtype == 1) {
-    if (fast) hipLaunchKernelGGL(fast_kernel<uint16_t>, g, blk, lds, st, a);
-    else hipLaunchKernelGGL(chunk_kernel<uint16_t>, g, blk, lds, st, a);
-  } else {
-    if (fast) hipLaunchKernelGGL(fast_kernel<float>, g, blk, lds, st, a);
-    else hipLaunchKernelGGL(chunk_kernel<float>, g, blk, lds, st, a);
-  }
+  if (dtype == 1) hipLaunchKernelGGL(chunk_kernel<uint16_t>, g, blk, lds, st, a);
+  else hipLaunchKernelGGL(chunk_kernel<float>, g, blk, lds, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (a.S > 1) {
@@ -1445,8 +1075,7 @@ hipError_t launch_sample(const SampleArgs& a, int dtype, bool fast, size_t lds, 
 }
 
 hipError_t set_sample_lds_limit(size_t bytes) {
-  const void* fns[] = {(const void*)fast_kernel<float>,  (const void*)fast_kernel<uint16_t>,
-                       (const void*)chunk_kernel<float>, (const void*)chunk_kernel<uint16_t>,
+  const void* fns[] = {(const void*)chunk_kernel<float>, (const void*)chunk_kernel<uint16_t>,
                        (const void*)full_kernel<float>,  (const void*)full_kernel<uint16_t>,
                        (const void*)merge_kernel};
   hipError_t e = hipSuccess;
