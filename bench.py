@@ -1,16 +1,21 @@
 #!/usr/bin/env python3
 """Benchmark of the decode-time sampler on one MI355X.
 
-A step is one tgs_sample call over one B=64, V=128256 fp32 batch (BASELINE
-config 2: penalties from a 512-id history, temperature, top-k 50, top-p 0.9,
-one host uniform per row).  Inputs are resident in HBM before timing; 16
+A step is one tgs_sample call over one B=64, V=128256 fp32 batch (the
+headline configuration: penalties from a 512-id history, temperature,
+top-k 50, top-p 0.9, one host uniform per row).  Inputs are resident in HBM before timing; 16
 distinct logits buffers (525 MB) rotate so the 256 MB Infinity Cache cannot
 serve repeats.  Launches are captured in a HIP graph (16 launches, one per
 buffer) and replayed; the timed region is bracketed by synchronisations and
 HIP events on the launch stream.
 
-Prints one JSON line (see the contract in the repository docs) with the
-roofline of the sampling kernel and the CPU oracle timed on this host.
+Prints one JSON line with the roofline of the sampling kernel and the CPU
+oracle timed on this host.
+
+`--calibrate-copy MIB` instead runs a plain device-to-device copy of MIB MiB
+a few times: profiling it with the FETCH_SIZE / WRITE_SIZE counters gives the
+scale between those counters and bytes actually moved, which converts the
+sampling kernel's counter readings into HBM bytes per launch.
 """
 from __future__ import annotations
 
@@ -35,6 +40,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run only a plain copy of MIB MiB (counter calibration)")
     return ap.parse_args()
 
 
@@ -80,13 +87,36 @@ def cpu_baseline(sets, seconds):
     ), ids
 
 
+def calibrate_copy(torch, mib, reps=8):
+    """Plain copy of a known size, for scaling HBM byte counters."""
+    n = mib << 20
+    src = torch.empty(n // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / reps
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "reps": reps,
+                      "ms_per_copy": round(ms, 4), "GBps": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the sampler is "
-              "row-parallel and shards by batch with no exchange, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build runs on a "
+              "single GPU; the sampler is row-parallel and would shard by batch rows with "
+              "no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
     import torch
+
+    if args.calibrate_copy:
+        calibrate_copy(torch, args.calibrate_copy)
+        return
 
     import tinygpt_amd as tg
     from tinygpt_amd import workloads as W
@@ -166,7 +196,7 @@ def main():
     achieved = alg_bytes / (ms_per_step * 1e-3) / 1e9
     rows_per_s = B / (ms_per_step * 1e-3)
     traffic = None
-    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_c2.json")
+    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "k64_kernel_c2_traffic.json")
     if os.path.exists(tfile):
         try:
             traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")

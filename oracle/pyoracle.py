@@ -68,6 +68,15 @@ def build() -> str:
     return LIB_PATH
 
 
+def build_ref(ref_root: str = "/root/reference") -> str | None:
+    """Compile the reference's own C++ sampler into oracle/_ref/ (the
+    checker's checker) when the reference checkout is present; else None."""
+    if not os.path.isdir(os.path.join(ref_root, "wasm", "src")):
+        return None
+    subprocess.run(["make", "-s", "-C", HERE, "ref", f"REF={ref_root}"], check=True)
+    return os.path.join(HERE, "_ref", "libtg_ref.so")
+
+
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
