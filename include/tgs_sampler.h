@@ -25,6 +25,9 @@
  *     id == -1  no token is allowed (all masked / -inf / NaN)   [TGS_EALLMASKED]
  *     id == -2  invalid row parameters (see tgs_row_params)
  *     id == -3  row outside the tgs_batch_hint given to the call
+ *     id == -4  a device-side wait between the workgroups of a row ran out
+ *               (cannot happen while the GPU runs every workgroup; the
+ *               handle should then be destroyed)
  *
  * Reference interfaces replaced (paths under the reference repository):
  *   tgs_sample       <- Server.sampleToken(from:temperature:constraint:)

@@ -183,6 +183,58 @@ inline unsigned long long __ballot(int pred) {
   return m;
 }
 
+// ---- lane moves (gfx950 semantics, checked on the GPU for the controls used)
+// DPP move: quad_perm (0x00-0xFF), row_shl:s (0x101-0x10F), row_shr:s
+// (0x111-0x11F), row_ror:s (0x121-0x12F), row_mirror (0x140); rows are 16
+// lanes; a source outside the row leaves `old` (bound_ctrl off, full masks).
+inline uint32_t __builtin_amdgcn_update_dpp(uint32_t old, uint32_t src, int ctrl, int, int, bool) {
+  const int l = hipcpu::lane(), row = l & ~15, r = l & 15;
+  int s = -1;
+  if (ctrl <= 0xFF) s = (l & ~3) | ((ctrl >> (2 * (l & 3))) & 3);
+  else if (ctrl >= 0x101 && ctrl <= 0x10F) s = r + (ctrl - 0x100) < 16 ? l + (ctrl - 0x100) : -1;
+  else if (ctrl >= 0x111 && ctrl <= 0x11F) s = r - (ctrl - 0x110) >= 0 ? l - (ctrl - 0x110) : -1;
+  else if (ctrl >= 0x121 && ctrl <= 0x12F) s = row | ((r + (ctrl - 0x120)) & 15);
+  else if (ctrl == 0x140) s = row | (15 - r);
+  else std::abort();
+  const uint32_t v = hipcpu::exchange(src, s < 0 ? l : s);
+  return s < 0 ? old : v;
+}
+struct hipcpu_u2 {
+  uint32_t v[2];
+  uint32_t operator[](int i) const { return v[i]; }
+};
+// v_permlane16_swap: odd rows of the first operand swap with even rows of
+// the second; v_permlane32_swap: the upper half of the first with the lower
+// half of the second.  Returns {first, second} after the swap.
+inline hipcpu_u2 __builtin_amdgcn_permlane16_swap(uint32_t a, uint32_t b, bool, bool) {
+  const int l = hipcpu::lane();
+  const uint32_t a_up = hipcpu::exchange(a, l < 48 ? l + 16 : l);  // a of lane + 16
+  const uint32_t b_dn = hipcpu::exchange(b, l >= 16 ? l - 16 : l);  // b of lane - 16
+  const bool odd = (l >> 4) & 1;
+  return {{odd ? b_dn : a, odd ? b : a_up}};
+}
+inline hipcpu_u2 __builtin_amdgcn_permlane32_swap(uint32_t a, uint32_t b, bool, bool) {
+  const int l = hipcpu::lane();
+  const uint32_t a_up = hipcpu::exchange(a, l < 32 ? l + 32 : l);
+  const uint32_t b_dn = hipcpu::exchange(b, l >= 32 ? l - 32 : l);
+  const bool hi = l >= 32;
+  return {{hi ? b_dn : a, hi ? b : a_up}};
+}
+inline uint32_t __builtin_amdgcn_mbcnt_lo(uint32_t mask, uint32_t acc) {
+  const int l = hipcpu::lane();
+  return acc + (uint32_t)__builtin_popcount(l >= 32 ? mask : (mask & ((1u << l) - 1u)));
+}
+inline uint32_t __builtin_amdgcn_mbcnt_hi(uint32_t mask, uint32_t acc) {
+  const int l = hipcpu::lane();
+  return acc + (uint32_t)(l < 32 ? 0 : __builtin_popcount(mask & ((1u << (l - 32)) - 1u)));
+}
+template <typename T>
+inline T __builtin_amdgcn_readlane(T x, int l) { return hipcpu::exchange(x, l); }
+// A wave-wide barrier stands in for the code-motion barrier; the fences order
+// nothing further on the host.
+inline void __builtin_amdgcn_wave_barrier() { hipcpu::wave().bar->arrive_and_wait(); }
+#define __builtin_amdgcn_fence(...) ((void)0)
+
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
 inline unsigned min(unsigned a, unsigned b) { return a < b ? a : b; }
@@ -225,6 +277,7 @@ inline T __hip_atomic_load(const T* p, int, int) { return __atomic_load_n(p, __A
 template <typename T, typename U>
 inline T __hip_atomic_fetch_add(T* p, U v, int, int) { return __atomic_fetch_add(p, (T)v, __ATOMIC_SEQ_CST); }
 inline void __builtin_amdgcn_s_waitcnt(int) {}
+inline void __builtin_amdgcn_s_sleep(int) { std::this_thread::yield(); }
 
 // ---- runtime API on host memory ----
 inline int& hipcpu_last_error() {

@@ -28,6 +28,7 @@ struct tgs_ctx {
   int* ws_cnt = nullptr;
   int ws_rows = 0;  // chunk lists of KMAX entries the workspace holds
   unsigned* k64_cnt = nullptr;  // fused kernel arrival counters, one line per row
+  unsigned long long* k64_lists = nullptr;  // fused kernel chunk lists, [max_batch * kMaxSplit][64]
   uint32_t* mask_table = nullptr;
   int n_states = 0, mask_vocab = 0, mask_words = 0;
   float* spec_stats = nullptr;
@@ -88,7 +89,7 @@ void free_spec(tgs_ctx* h) {
 // at most kMaxSplit, the most lists the last workgroup of a row merges);
 // beyond that about two workgroups per CU with chunks of at least 2048
 // ids.  TGS_SPLIT raises the split (tuning).
-constexpr int kK64Tile = 16384;
+constexpr int kK64Tile = tgs::K64_TILE;
 int choose_split_k64(const tgs_ctx* h, int B, int V) {
   const int smin = (V + kK64Tile - 1) / kK64Tile;
   int S;
@@ -181,6 +182,9 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
   const size_t cnt_bytes = sizeof(unsigned) * (size_t)max_batch * tgs::K64_CNT_STRIDE;
   if (e == hipSuccess) e = hipMalloc(&h->k64_cnt, cnt_bytes);
   if (e == hipSuccess) e = hipMemset(h->k64_cnt, 0, cnt_bytes);
+  const size_t list_bytes = sizeof(unsigned long long) * (size_t)max_batch * kMaxSplit * 64;
+  if (e == hipSuccess) e = hipMalloc(&h->k64_lists, list_bytes);
+  if (e == hipSuccess) e = hipMemset(h->k64_lists, 0xFF, list_bytes);  // every entry "not written"
   if (e == hipSuccess) {
     // raise the dynamic-LDS ceiling to the device limit; a runtime that
     // rejects the attribute keeps its default (calls that need more fail
@@ -203,6 +207,7 @@ void tgs_destroy(tgs_handle h) {
   if (h->ws) (void)hipFree(h->ws);
   if (h->ws_cnt) (void)hipFree(h->ws_cnt);
   if (h->k64_cnt) (void)hipFree(h->k64_cnt);
+  if (h->k64_lists) (void)hipFree(h->k64_lists);
   if (h->mask_table) (void)hipFree(h->mask_table);
   free_spec(h);
   delete h;
@@ -295,6 +300,7 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   a.ws = h->ws;
   a.ws_cnt = h->ws_cnt;
   a.cnt = h->k64_cnt;
+  a.lists = h->k64_lists;
   a.dbg = dz;
   // Kernels: the fused top_k <= 64 kernel when the hint says every row is
   // greedy or has top_k <= 64; otherwise the chunk kernel (+ merge kernel
@@ -304,7 +310,7 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   a.hint_k = mk;
   a.TS = hist_cap > 0 ? next_pow2(std::max(64, 2 * hist_cap)) : 0;
   a.ts_shift = a.TS ? 32 - log2i(a.TS) : 0;
-  if (mk <= 64 && mk < V) {
+  if (mk <= 64 && mk < V && hist_cap <= tgs::K64_MAX_HIST) {
     a.full_rows = 0;
     const int S = choose_split_k64(h, B, V);
     // whole tiles when the split allows them (their loads need no checks)
@@ -313,9 +319,9 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
     a.S = (V + L - 1) / L;
     a.L = L;
     a.BW = tgs::K64_BITMAP_WORDS;
-    a.off_hash = 0;
-    a.off_bitmap = a.TS * 8;
-    a.off_cand = a.off_bitmap + a.BW * 4;
+    a.off_hash = 0;                             // 16-bit history count per id of a tile
+    a.off_bitmap = tgs::K64_TILE / 2 * 4;       // history bitmap of a tile
+    a.off_cand = a.off_bitmap + a.BW * 4;       // candidate staging (16-byte aligned)
     a.capt = tgs::K64_CAP;
     a.ws_stride = 64;
     const size_t lds = (size_t)a.off_cand + (size_t)tgs::K64_CAND_ENTRIES * 8;

@@ -377,6 +377,89 @@ __device__ __forceinline__ T tmax(T a, T b) { return a > b ? a : b; }
 template <typename T>
 __device__ __forceinline__ T tmin(T a, T b) { return a < b ? a : b; }
 
+// ------------------------------------------------------------------ lane permutes
+// The value of lane (lane ^ S), S a power of two below 64, by VALU lane
+// moves only (no trip through the LDS crossbar):
+//   S = 1, 2   DPP quad_perm [1,0,3,2] / [2,3,0,1]
+//   S = 4      DPP row_shl:4 and row_shr:4, picked by lane bit 2
+//   S = 8      DPP row_ror:8 (rotation by half a 16-lane row)
+//   S = 16/32  v_permlane16_swap / v_permlane32_swap of x with itself: the
+//              two results hold the rows (halves) moved each way, picked by
+//              the lane bit.
+template <int S>
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t x) {
+  static_assert(S == 1 || S == 2 || S == 4 || S == 8 || S == 16 || S == 32, "lane xor");
+  if constexpr (S == 1) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (S == 2) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (S == 4) {
+    const uint32_t up = __builtin_amdgcn_update_dpp(0u, x, 0x104, 0xF, 0xF, false);  // lane + 4
+    const uint32_t dn = __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xF, 0xF, false);  // lane - 4
+    return (lane_id() & 4) ? dn : up;
+  } else if constexpr (S == 8) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x128, 0xF, 0xF, false);
+  } else if constexpr (S == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane_id() & 16) ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane_id() & 32) ? r[0] : r[1];
+  }
+}
+
+// lane 63 - lane: DPP row_mirror (xor 15 inside a row), then xor 16 and 32
+__device__ __forceinline__ uint32_t rev_lanes32(uint32_t x) {
+  return xor_lane32<32>(xor_lane32<16>(__builtin_amdgcn_update_dpp(0u, x, 0x140, 0xF, 0xF, false)));
+}
+
+template <int S, typename T>
+__device__ __forceinline__ T xor_lane(T x) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
+  if constexpr (sizeof(T) == 8) {
+    const u64 v = (u64)x;
+    return (T)(((u64)xor_lane32<S>((uint32_t)(v >> 32)) << 32) | xor_lane32<S>((uint32_t)v));
+  } else {
+    return (T)xor_lane32<S>((uint32_t)x);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T rev_lanes(T x) {
+  if constexpr (sizeof(T) == 8) {
+    const u64 v = (u64)x;
+    return (T)(((u64)rev_lanes32((uint32_t)(v >> 32)) << 32) | rev_lanes32((uint32_t)v));
+  } else {
+    return (T)rev_lanes32((uint32_t)x);
+  }
+}
+
+// xor_lane for a stride known after unrolling
+template <typename T>
+__device__ __forceinline__ T xor_lane_s(T x, int s) {
+  switch (s) {
+    case 1: return xor_lane<1>(x);
+    case 2: return xor_lane<2>(x);
+    case 4: return xor_lane<4>(x);
+    case 8: return xor_lane<8>(x);
+    case 16: return xor_lane<16>(x);
+    default: return xor_lane<32>(x);
+  }
+}
+
+// Number of set bits of a wave mask below this lane.
+__device__ __forceinline__ unsigned lanes_below(u64 mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Orders a wave's LDS accesses before and after it (LDS operations of one
+// wave execute in issue order, so this only restrains the compiler).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Bitonic sort of 64 values across the lanes of a wave (descending).
 template <typename T>
 __device__ __forceinline__ T wave_sort_desc(T x) {
@@ -385,7 +468,7 @@ __device__ __forceinline__ T wave_sort_desc(T x) {
   for (int size = 2; size <= 64; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const T y = __shfl_xor(x, stride, 64);
+      const T y = xor_lane_s(x, stride);
       const bool lower = (lane & stride) == 0;
       const bool desc = (lane & size) == 0;
       x = (lower == desc) ? tmax(x, y) : tmin(x, y);
@@ -399,10 +482,10 @@ __device__ __forceinline__ T wave_sort_desc(T x) {
 template <typename T>
 __device__ __forceinline__ T wave_merge_top64(T a, T b) {
   const int lane = lane_id();
-  T c = tmax(a, __shfl(b, 63 - lane, 64));
+  T c = tmax(a, rev_lanes(b));
 #pragma unroll
   for (int stride = 32; stride > 0; stride >>= 1) {
-    const T y = __shfl_xor(c, stride, 64);
+    const T y = xor_lane_s(c, stride);
     c = ((lane & stride) == 0) ? tmax(c, y) : tmin(c, y);
   }
   return c;

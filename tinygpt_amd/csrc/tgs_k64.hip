@@ -3,37 +3,47 @@
 //
 // Workgroup (b, c) of K64_NT = 256 threads (4 waves) owns chunk c of row b:
 // S chunks per row, each one tile of at most 16384 ids (64 per thread:
-// sixteen 16-byte vectors of fp32 or eight of bf16).  At entry it requests
-// everything it reads first in one go -- two history ids per thread, the
-// tile, the row's parameters, uniform and history length -- so that one
-// memory latency covers them all.  Then:
-//   * the history ids that fall in the chunk go to an LDS table
-//     (id -> count) and to a 64-bit mask per thread of its history
-//     elements, and the logit of every table slot is fetched again (an L2
-//     hit);
-//   * one pass scales the tile by 1/T (masked ids: -inf) and takes thread
-//     maxima, leaving the history ids out (-inf); their penalised values
-//     are computed per table slot afterwards;
-//   * every wave sorts its thread maxima (bitonic, in registers); their
-//     k-th and ceil(k/4)-th entries give a threshold with at least k
-//     elements above it (first_threshold);
-//   * every thread writes its elements at or above the threshold to its own
-//     eight LDS slots (history candidates go to a compact region), then the
-//     slots are compacted (a wave prefix sum, one LDS atomic per wave); when
-//     ties or a skewed tile overflow them, a radix selection finds the
-//     exact k-th composite first;
-//   * ranks by counting (every candidate counts the entries above it,
-//     several threads per candidate, 16-byte broadcast LDS reads) give the
-//     chunk's top k, sorted.
-// With S == 1 the workgroup finishes its row.  Otherwise wave 0 publishes
-// the chunk's sorted list with agent-coherent stores (sc1: written through
-// to memory past the per-XCD L2s, which are not coherent with each other),
-// waits for them to complete and counts the chunk in the row's arrival
-// counter with a relaxed device atomic.  The workgroup that arrives last
-// reads the S lists back with agent-coherent loads, merges them the same
-// way and finishes the row (masses, top-p, draw); it then clears the
-// counter.  No agent-scope release/acquire fence is issued: on this part
-// such a fence writes back or invalidates the whole L2 of the XCD.
+// sixteen 16-byte vectors of fp32 or eight of bf16).
+//
+// Loads.  At entry a thread requests everything it reads: four history ids,
+// the tile and (with a mask table) the mask word of each of its vectors; the
+// row's parameters come through the scalar cache.  In the vector variant
+// every load is issued unconditionally (addresses clamped into the chunk,
+// values past its end replaced afterwards), so the same number of loads is
+// in flight on every path and each use waits for exactly the loads it needs:
+// the history counts are built while the tile streams in, and the values of
+// a vector are computed as soon as it arrives.
+//
+// History.  The row's history ids that fall in the chunk are counted in LDS
+// (a 16-bit count per id of the tile, two per word) and marked in a bitmap
+// of the tile by owner thread.  The value pass leaves marked elements out
+// (-inf); the thread whose insertion of an id came first (its producer)
+// loads that id's logit once, penalises it and adds it to its wave's
+// candidates, so history ids cost one lane each, not a pass over the tile.
+//
+// Candidates.  Every wave sorts its threads' maxima (bitonic, in registers);
+// the k-th and ceil(k/4)-th entries of all waves give a threshold T with at
+// least k elements of the tile at or above it.  Each wave stages the vectors
+// whose maximum reaches T (placed by ballot prefix counts), tests their
+// elements one per lane, sorts its candidates in registers (64 at a time),
+// and wave 0 merges the four waves' top 64.  A wave with more candidates
+// than its staging holds (ties, skewed tiles) sends the workgroup down an
+// exact path: radix selection of the k-th composite, then ranking of the k
+// candidates at or above it.
+//
+// Rows split over S > 1 chunks.  Each workgroup counts itself in the row's
+// arrival counter at entry (a relaxed device atomic issued with the loads).
+// The workgroup that arrives last merges the row: every other workgroup of
+// the row has started by then and will store its chunk's sorted list with
+// agent-coherent stores (written through past the per-XCD L2s, which are not
+// coherent with each other) without waiting for anything, so the merging
+// workgroup polls those lists with agent-coherent loads until no entry holds
+// the empty marker, merges them with its own, finishes the row (masses,
+// top-p, draw) and resets the lists to the marker and the counter to zero
+// for the next call.  The wait is bounded: one that runs out (it cannot
+// while every workgroup runs) writes id -4 for the row.  No fence is issued:
+// on this part an agent-scope release or acquire fence writes back or
+// invalidates the whole L2 of the XCD.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 #include "tgs_row.h"
@@ -43,7 +53,10 @@ namespace k64 {
 
 constexpr int BS = K64_NT;
 constexpr int NWB = BS / 64;
-constexpr int KM = 64;  // largest top_k served
+constexpr int KM = 64;                   // largest top_k served
+constexpr int NHID = K64_MAX_HIST / BS;  // history ids per thread
+constexpr u64 EMPTY = ~0ull;             // list entry not written yet: above every composite
+constexpr int SPIN_LIMIT = 1 << 18;      // polls of one list before the wait gives up
 
 // A tile gives every thread 64 elements: 16384 ids.
 template <typename Tin>
@@ -52,9 +65,11 @@ struct TileK {
   static constexpr int EPT = 64;
   static constexpr int U = EPT / EPV;  // 16-byte vectors per thread
   static constexpr int SIZE = BS * EPT;
+  static_assert(SIZE == K64_TILE, "tile size");
 };
 constexpr int BITMAP_WORDS = K64_BITMAP_WORDS;  // one bit per id of a tile
-static_assert(BITMAP_WORDS * 32 == BS * 64, "bitmap covers a tile");
+constexpr int CNT_WORDS = K64_TILE / 2;         // 16-bit history counts, two per word
+static_assert(BITMAP_WORDS * 32 == K64_TILE, "bitmap covers a tile");
 
 // id of element j of this thread in the tile starting at t0
 template <int EPV>
@@ -62,65 +77,71 @@ __device__ __forceinline__ int id_of(int t0, int j) {
   return t0 + ((j / EPV) * BS + (int)threadIdx.x) * EPV + (j % EPV);
 }
 
-// The tile's 16-byte vectors; ids at or past v1 read as NaN (never
-// allowed).  A chunk that fills the tile is read without checks; with
-// whole_vec a vector is wholly before or after v1 (chunk ends are multiples
-// of 64 ids, and so is the row end's vector boundary).
-template <typename Tin, int U = TileK<Tin>::U>
-__device__ __forceinline__ void load_data(const Tin* rowp, int t0, int v1, bool aligned, bool whole_vec,
-                                          uint4 (&raw)[U]) {
-  constexpr int EPV = TileK<Tin>::EPV;
-  if (whole_vec && t0 + TileK<Tin>::SIZE <= v1) {
-#pragma unroll
-    for (int u = 0; u < U; u++) raw[u] = *(const uint4*)(rowp + t0 + (u * BS + (int)threadIdx.x) * EPV);
-  } else if (whole_vec) {
-    const uint4 nan4 = make_uint4(Elem<Tin>::NAN_BITS, Elem<Tin>::NAN_BITS, Elem<Tin>::NAN_BITS, Elem<Tin>::NAN_BITS);
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
-      raw[u] = v < v1 ? *(const uint4*)(rowp + v) : nan4;
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < U; u++) raw[u] = load_vec<Tin>(rowp, t0 + (u * BS + (int)threadIdx.x) * EPV, v1, aligned);
-  }
-}
-
-template <typename Tin, int U = TileK<Tin>::U>
-__device__ __forceinline__ void load_mask(const Row& r, int t0, uint32_t (&mw)[U]) {
+// The tile's 16-byte vectors.  VEC: the chunk holds whole vectors (rows
+// aligned, chunk ends multiples of the vector); a vector past the chunk end
+// is read at the chunk's last vector and replaced by NaN in the value pass.
+// Otherwise ids at or past v1 read as NaN here (checked loads).
+template <typename Tin, bool VEC, int U = TileK<Tin>::U>
+__device__ __forceinline__ void load_tile(const Tin* rowp, int t0, int v1, bool aligned, uint4 (&raw)[U]) {
   constexpr int EPV = TileK<Tin>::EPV;
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
-    mw[u] = r.mrow[(v < r.v1 ? v : r.v1 - 1) >> 5];
+    if constexpr (VEC) raw[u] = *(const uint4*)(rowp + (v < v1 ? v : v1 - EPV));
+    else raw[u] = load_vec<Tin>(rowp, v, v1, aligned);
   }
 }
 
-// y = logit / T over a tile with no mask and no history ids.  NaN and -inf
-// (ids at or past the chunk end were loaded as NaN) never pass a threshold
-// test or raise a maximum, so they are left as they are.  Returns the
-// thread maximum.
+// Mask word of each vector (unconditional; rows without a mask read a valid
+// table row and ignore it).
 template <typename Tin, int U = TileK<Tin>::U>
-__device__ __forceinline__ float values_plain(const Row& r, const uint4 (&raw)[U], float (&y)[TileK<Tin>::EPT]) {
+__device__ __forceinline__ void load_mask(const uint32_t* mrow, int t0, int v1, uint32_t (&mw)[U]) {
+  constexpr int EPV = TileK<Tin>::EPV;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
+    mw[u] = mrow[(v < v1 ? v : v1 - 1) >> 5];
+  }
+}
+
+// Logit of element e of a vector; NaN for a vector past the chunk end.
+template <typename Tin>
+__device__ __forceinline__ float elem_z(const uint4& raw, int e, bool past) {
+  const float z = Elem<Tin>::get(raw, e);
+  return past ? __builtin_nanf("") : z;
+}
+
+// y = logit / T over a tile with no mask and no history ids.  NaN and -inf
+// (ids past the chunk end read as NaN) never pass a threshold test or raise
+// a maximum.  vm[u]: the maximum of vector u.  Returns the thread maximum.
+// tail: vectors past the chunk end were read at a clamped address.
+template <typename Tin, int U = TileK<Tin>::U>
+__device__ __forceinline__ float values_plain(const Row& r, int t0, bool tail, const uint4 (&raw)[U],
+                                              float (&y)[TileK<Tin>::EPT], float (&vm)[U]) {
   constexpr int EPV = TileK<Tin>::EPV;
   float mx = -__builtin_inff();
 #pragma unroll
-  for (int u = 0; u < U; u++)
+  for (int u = 0; u < U; u++) {
+    const bool past = tail && t0 + (u * BS + (int)threadIdx.x) * EPV >= r.v1;
+    float m = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < EPV; e++) {
-      y[u * EPV + e] = Elem<Tin>::get(raw[u], e) * r.invT;
-      mx = fmaxf(mx, y[u * EPV + e]);
+      y[u * EPV + e] = elem_z<Tin>(raw[u], e, past) * r.invT;
+      m = fmaxf(m, y[u * EPV + e]);
     }
+    vm[u] = m;
+    mx = fmaxf(mx, m);
+  }
   return mx;
 }
 
-// The same with the grammar mask (masked ids: -inf) and/or the history ids
-// of the tile left out (-inf; they are penalised separately).  hb: this
-// thread's history elements, bit j for element j (from the LDS table
-// build); masked ids are gathered into the same kind of mask first.
-template <typename Tin, int U = TileK<Tin>::U>
-__device__ __forceinline__ float values_general(const Row& r, u64 hb, int t0, const uint4 (&raw)[U],
-                                                const uint32_t (&mw)[U], float (&y)[TileK<Tin>::EPT]) {
+// The same with the grammar mask and the history ids of the tile left out
+// (-inf; their penalised values join the candidates separately).  hb: this
+// thread's history elements, bit j for element j.
+template <typename Tin, bool MASK, int U = TileK<Tin>::U>
+__device__ __forceinline__ float values_general(const Row& r, u64 hb, int t0, bool tail, const uint4 (&raw)[U],
+                                                const uint32_t (&mw)[U], float (&y)[TileK<Tin>::EPT],
+                                                float (&vm)[U]) {
   constexpr int EPV = TileK<Tin>::EPV;
   constexpr uint32_t GM = (1u << EPV) - 1u;
   const float ninf = -__builtin_inff();
@@ -129,16 +150,22 @@ __device__ __forceinline__ float values_general(const Row& r, u64 hb, int t0, co
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
+    const bool past = tail && v >= r.v1;
     uint32_t d = ((u * EPV < 32 ? hlo : hhi) >> ((u * EPV) & 31)) & GM;
-    if (r.mrow) d |= ~(mw[u] >> (v & 31)) & GM;
-#pragma unroll
-    for (int e = 0; e < EPV; e++) y[u * EPV + e] = Elem<Tin>::get(raw[u], e) * r.invT;
-    if (d) {
-#pragma unroll
-      for (int e = 0; e < EPV; e++) y[u * EPV + e] = (d & (1u << e)) ? ninf : y[u * EPV + e];
+    if constexpr (MASK) {
+      if (r.mrow) d |= ~(mw[u] >> (v & 31)) & GM;
     }
 #pragma unroll
-    for (int e = 0; e < EPV; e++) mx = fmaxf(mx, y[u * EPV + e]);
+    for (int e = 0; e < EPV; e++) y[u * EPV + e] = elem_z<Tin>(raw[u], e, past) * r.invT;
+    if (d) {
+#pragma unroll
+      for (int e = 0; e < EPV; e++) y[u * EPV + e] = ((d >> e) & 1u) ? ninf : y[u * EPV + e];
+    }
+    float m = ninf;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) m = fmaxf(m, y[u * EPV + e]);
+    vm[u] = m;
+    mx = fmaxf(mx, m);
   }
   return mx;
 }
@@ -151,8 +178,8 @@ __device__ __forceinline__ float values_general(const Row& r, u64 hb, int t0, co
 __device__ __forceinline__ uint32_t first_threshold(float mx, int k, uint32_t* thr_w) {
   const uint32_t key = mx > -__builtin_inff() ? tg_key(mx) : 0u;
   const uint32_t srt = wave_sort_desc(key);  // lane i: the (i+1)-th largest
-  const uint32_t tk = __shfl(srt, k - 1, 64);
-  const uint32_t tj = __shfl(srt, (k + NWB - 1) / NWB - 1, 64);
+  const uint32_t tk = __builtin_amdgcn_readlane(srt, k - 1);
+  const uint32_t tj = __builtin_amdgcn_readlane(srt, (k + NWB - 1) / NWB - 1);
   const int w = threadIdx.x >> 6;
   if (lane_id() == 0) {
     thr_w[w] = tk;
@@ -176,40 +203,27 @@ __device__ __forceinline__ float thr_value(u64 thr) {
   return tk <= kmin ? -3.40282347e38f : tg_unkey(tk);
 }
 
-// Candidate buffer: ES slots per thread for its tile elements, slot-major
-// (slot q of thread t at q * BS + t), a compact region of HCAP entries for
-// history table slots, and the compacted candidates (CCAP + 16 pad).  Tile candidates (y >= tf; tf is the value of a
-// threshold whose low, id part is 1, so this is the composite test for any
-// id) are written as (y bits << 32 | id) pairs and turned into composite
-// keys by their thread afterwards; unused slots hold 0.  Returns this
-// thread's number of tile candidates (more than ES: overflow).
-constexpr int ES = 8;
-constexpr int HCAP = 512;
-constexpr int CCAP = K64_CAP;  // compacted candidates (rank selection input), + 16 pad entries
-static_assert(ES * BS + HCAP + CCAP + 16 == K64_CAND_ENTRIES, "candidate buffer");
+// Candidate buffer (LDS).  Common path, per wave: up to VCAP candidate
+// vectors (a vector whose maximum reaches the threshold value tf; tf is the
+// value of a threshold whose low, id part is 1, so y >= tf is the composite
+// test for any id) as EPV floats each plus the id of their first element,
+// and a list of up to LCAP candidate composites.  The exact path (a wave
+// with more candidate vectors or candidates than that) reuses the same
+// memory for up to CCAP compacted candidates (+ 16 pad entries for the rank
+// counting).
+constexpr int VCAP = 64;
+constexpr int LCAP = 256;
+constexpr int CCAP = K64_CAP;
+static_assert(CCAP + 16 <= K64_CAND_ENTRIES, "candidate buffer");
 
-template <int EPT, int EPV>
-__device__ __forceinline__ int emit_lane_slots(u64* cand, const float (&y)[EPT], float tf, int t0) {
-  const int idb = t0 + (int)threadIdx.x * EPV;
-  u64* my = cand + threadIdx.x;
-  int pos = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; j++)
-    if (y[j] >= tf) {
-      if (pos < ES) my[pos * BS] = ((u64)tg_f2u(y[j]) << 32) | (uint32_t)(idb + (j / EPV) * BS * EPV + (j % EPV));
-      pos++;
-    }
-#pragma unroll
-  for (int q = 0; q < ES; q++) {
-    if (q >= pos) {
-      my[q * BS] = 0ull;
-    } else {
-      const u64 e = my[q * BS];
-      my[q * BS] = comp_key(tg_key(tg_u2f((uint32_t)(e >> 32))), (int)(uint32_t)e);
-    }
-  }
-  return pos;
-}
+template <typename Tin>
+struct Stage {
+  static constexpr int EPV = Elem<Tin>::EPV;
+  static constexpr int VALS = NWB * VCAP * EPV;  // floats
+  static constexpr int IDS = NWB * VCAP;         // ints
+  static constexpr int BYTES = VALS * 4 + IDS * 4 + NWB * LCAP * 8;
+  static_assert(BYTES <= K64_CAND_ENTRIES * 8, "stage fits the candidate buffer");
+};
 
 // cmp[0, n) holds unique composites (published by a barrier; room for 16
 // pad entries).  Writes the min(n, k) largest to top[rank] (rank 0 = the
@@ -249,21 +263,23 @@ __device__ __forceinline__ void rank_into(u64* cmp, u64* top, int n, int k) {
 }
 
 // Calls f(x) for every candidate composite x of this thread, re-reading the
-// tile (the overflow path: a rolled loop keeps registers free).
-template <typename Tin, class F>
-__device__ __forceinline__ void each_cand(const Row& r, bool has_hist, const uint32_t* bitmap, const Tin* rowp,
-                                          int t0, float tf, const u64* hcomp, int TS, u64 thr, F f) {
+// tile (the exact path: a rolled loop keeps registers free).
+template <typename Tin, bool MASK, class F>
+__device__ __forceinline__ void each_cand(const Row& r, bool has_hist, const uint32_t* bitmap, const uint32_t* hcnt,
+                                          const Tin* rowp, int t0, float tf, F f) {
   constexpr int EPV = TileK<Tin>::EPV;
 #pragma unroll 1
   for (int j = 0; j < TileK<Tin>::EPT; j++) {
     const int id = id_of<EPV>(t0, j);
     if (id >= r.v1) continue;
-    if (has_hist && ((bitmap[2 * threadIdx.x + (j >> 5)] >> (j & 31)) & 1u)) continue;
-    const float yy = Elem<Tin>::scalar(rowp, id) * r.invT;
-    if (yy >= tf && mask_allows(r, id)) f(comp_key(tg_key(yy), id));
+    const float z = Elem<Tin>::scalar(rowp, id);
+    float yy = z * r.invT;
+    if (has_hist && ((bitmap[2 * threadIdx.x + (j >> 5)] >> (j & 31)) & 1u)) {
+      const int loc = id - t0;
+      yy = penalise(z, (int)((hcnt[loc >> 1] >> ((loc & 1) * 16)) & 0xFFFFu), r) * r.invT;
+    }
+    if (yy >= tf && (!MASK || mask_allows(r, id))) f(comp_key(tg_key(yy), id));
   }
-  for (int i = threadIdx.x; i < TS; i += BS)
-    if (hcomp[i] >= thr) f(hcomp[i]);
 }
 
 // Tree merge of the waves' sorted top-64 lists (lane i = rank i) held in
@@ -310,17 +326,17 @@ __device__ __forceinline__ void wave_finish_row(const SampleArgs& a, const Row& 
   }
 }
 
-template <typename Tin>
+template <typename Tin, bool VEC, bool MASK>
 __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
   using TL = TileK<Tin>;
   TGS_DYN_SMEM(smem);
   __shared__ uint32_t thr_w[2 * NWB];
   __shared__ u64 tops[NWB][64];
-  __shared__ unsigned nbuf, nhist, nhc;
-  __shared__ int ovf;
-  __shared__ int last_s;
+  __shared__ u64 own[64];
+  __shared__ unsigned nbuf, nhist;
+  __shared__ int ovf, elect, tmo;
   __shared__ BlockScratch bs;
-  int2* hash = (int2*)(smem + a.off_hash);
+  uint32_t* hcnt = (uint32_t*)(smem + a.off_hash);
   uint32_t* bitmap = (uint32_t*)(smem + a.off_bitmap);
   u64* cand = (u64*)(smem + a.off_cand);
   const int w = threadIdx.x >> 6, lane = lane_id();
@@ -329,17 +345,30 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
   if (b >= a.B) return;
   const int v0 = c * a.L, v1 = min(a.V, v0 + a.L);
   const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
+  const bool full = v0 + TL::SIZE <= v1;
+  unsigned* cnt = a.cnt + (long long)b * K64_CNT_STRIDE;
 
-  // one round trip for the history ids, the tile and the row's parameters
-  // (history ids first: a wave's loads return in order)
-  const int* hrow = a.hist ? a.hist + (long long)b * a.hist_cap : nullptr;
-  const int hid0 = (hrow && (int)threadIdx.x < a.hist_cap) ? hrow[threadIdx.x] : -1;
-  const int hid1 = (hrow && (int)threadIdx.x + BS < a.hist_cap) ? hrow[threadIdx.x + BS] : -1;
-  uint4 raw[TL::U];
-  load_data<Tin>(rowp, v0, v1, a.aligned, a.whole_vec, raw);
+  // everything read first, in one round trip, in the order it is needed (a
+  // wave's loads return in order): the row's parameters, its history length
+  // and ids, the arrival count, the tile
   const tgs_row_params p = a.params[b];
   const float ub = a.u[b];
-  const int hl = a.hist_len ? a.hist_len[b] : a.hist_cap;
+  const int hlr = *(a.hist_len ? a.hist_len + b : (const int*)a.params);
+  const bool hv = a.hist && a.hist_cap > 0;
+  const int* hp = hv ? a.hist + (long long)b * a.hist_cap : (const int*)a.params;
+  const int hlast = hv ? a.hist_cap - 1 : 0;
+  int hid[NHID];
+#pragma unroll
+  for (int q = 0; q < NHID; q++) {
+    const int j = (int)threadIdx.x + q * BS;
+    hid[q] = hp[j < hlast ? j : hlast];
+  }
+  unsigned arrived = 0;
+  if (a.S > 1 && threadIdx.x == 0)
+    arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint4 raw[TL::U];
+  load_tile<Tin, VEC>(rowp, v0, v1, a.aligned, raw);
+  const int hl = a.hist_len ? hlr : a.hist_cap;
 
   Row r;
   const bool valid = row_setup_from(a, b, c, p, ub, hl, r);
@@ -348,6 +377,9 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
       a.out[b] = valid ? -3 : -2;  // -3: row outside the launch hint
       write_row_diag(a, b, 0, 0, 0, 0, -1);
     }
+    // the row's last arrival clears the counter (no lists were written)
+    if (a.S > 1 && threadIdx.x == 0 && arrived == (unsigned)(a.S - 1))
+      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   const int k = r.mode == 0 ? 1 : r.k;
@@ -355,30 +387,38 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
   r.v1 = v1;
   float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)b * a.V : nullptr;
   uint32_t mw[TL::U];
-  if (r.mrow) load_mask<Tin>(r, v0, mw);
+  if constexpr (MASK) load_mask<Tin>(r.mrow ? r.mrow : a.mask_table, v0, v1, mw);
 
   if (threadIdx.x == 0) {
     nbuf = 0;
     nhist = 0;
-    nhc = 0;
     ovf = 0;
+    tmo = 0;
   }
-  // history: id -> count table, and per thread a 64-bit mask of its
-  // elements that are history ids (two words per thread; bitmap[2t + h])
+  // history: count of every id of the tile, and per thread a 64-bit mask of
+  // its elements that are history ids (two words per thread; bitmap[2t + h]);
+  // the first insertion of each id makes its thread the id's producer
+  bool prod[NHID];
+#pragma unroll
+  for (int q = 0; q < NHID; q++) prod[q] = false;
   if (r.use_pen) {
-    for (int i = threadIdx.x; i < a.TS; i += BS) hash[i] = make_int2(-1, 0);
+#pragma unroll
+    for (int i = 0; i < CNT_WORDS / 4 / BS; i++) ((uint4*)hcnt)[threadIdx.x + i * BS] = make_uint4(0u, 0u, 0u, 0u);
     for (int i = threadIdx.x; i < BITMAP_WORDS; i += BS) bitmap[i] = 0u;
     __syncthreads();
     unsigned mine = 0;
-    for (int j = threadIdx.x; j < r.H; j += BS) {
-      const int id = j == (int)threadIdx.x ? hid0 : j == (int)threadIdx.x + BS ? hid1 : r.hrow[j];
-      if (id < v0 || id >= v1) continue;
-      hash_insert(hash, a.TS, a.ts_shift, id);
-      const int loc = id - v0;                              // < TileK::SIZE
-      const int u = loc / (BS * TL::EPV), rr = loc % (BS * TL::EPV);
-      const int t = rr / TL::EPV, el = u * TL::EPV + rr % TL::EPV;  // owner thread, its element
-      atomicOr(&bitmap[2 * t + (el >> 5)], 1u << (el & 31));
-      mine++;
+#pragma unroll
+    for (int q = 0; q < NHID; q++) {
+      const int id = hid[q];
+      if ((int)threadIdx.x + q * BS < r.H && id >= v0 && id < v1) {
+        const int loc = id - v0;                              // < TileK::SIZE
+        const unsigned old = atomicAdd(&hcnt[loc >> 1], 1u << ((loc & 1) * 16));
+        prod[q] = ((old >> ((loc & 1) * 16)) & 0xFFFFu) == 0u;  // first occurrence: this id's producer
+        const int u = loc / (BS * TL::EPV), rr = loc % (BS * TL::EPV);
+        const int t = rr / TL::EPV, el = u * TL::EPV + rr % TL::EPV;  // owner thread, its element
+        atomicOr(&bitmap[2 * t + (el >> 5)], 1u << (el & 31));
+        mine++;
+      }
     }
     if (mine) atomicAdd(&nhist, mine);
   }
@@ -386,23 +426,26 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
   const bool has_hist = r.use_pen && nhist > 0;
   u64 hb = 0;
   if (has_hist) hb = ((u64)bitmap[2 * threadIdx.x + 1] << 32) | bitmap[2 * threadIdx.x];
-
-  // history slots: their logits are fetched now (an L2 hit: the tile was
-  // just read) and penalised after the threshold
-  const int TS = has_hist ? a.TS : 0;
-  constexpr int PRE = 4;
-  float zs[PRE];
+  // producers' logits (and mask words): one load per history id of this
+  // thread, issued behind the tile and first needed after the threshold;
+  // the loads are unconditional (others read id v0) to keep the count fixed
+  float zq[NHID];
+  uint32_t mq[NHID];
 #pragma unroll
-  for (int q = 0; q < PRE; q++) {
-    const int i = (int)threadIdx.x + q * BS;
-    zs[q] = 0.0f;
-    if (i < TS && hash[i].x >= 0) zs[q] = Elem<Tin>::scalar(rowp, hash[i].x);
+  for (int q = 0; q < NHID; q++) {
+    const int id = prod[q] ? hid[q] : v0;
+    zq[q] = Elem<Tin>::scalar(rowp, id);
+    if constexpr (MASK) mq[q] = (r.mrow ? r.mrow : a.mask_table)[id >> 5];
   }
 
-  // the chunk is one tile (L <= TileK::SIZE)
+  // values, per-vector maxima, thread maximum
   float y[TL::EPT];
-  const float mx = (!r.mrow && !has_hist) ? values_plain<Tin>(r, raw, y)
-                                          : values_general<Tin>(r, hb, v0, raw, mw, y);
+  float vm[TL::U];
+  const bool tail = VEC && !full;
+  bool gen = has_hist;
+  if constexpr (MASK) gen = gen || r.mrow != nullptr;
+  const float mx = gen ? values_general<Tin, MASK>(r, hb, v0, tail, raw, mw, y, vm)
+                       : values_plain<Tin>(r, v0, tail, raw, y, vm);
   if (post) {
 #pragma unroll
     for (int j = 0; j < TL::EPT; j++) {
@@ -410,78 +453,98 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
       if (id < v1) post[id] = y[j] > -__builtin_inff() ? y[j] : -__builtin_inff();
     }
   }
-  // candidates are >= thr; thr >= 1 keeps empty history slots (composite 0)
-  // out, every allowed composite is far above it
+  // candidates are >= thr; every allowed composite is far above the id part
   const u64 thr = ((u64)first_threshold(mx, k, thr_w) << 32) | 1ull;
   const float tf = thr_value(thr);
-  // history slots: penalised value, mask, composite (0 if not allowed or
-  // empty), written over the slot (each slot is read and written by one
-  // thread; the table is not probed again)
-  u64* hcomp = (u64*)hash;
+
+  // Every element >= tf, wave by wave.  A vector whose maximum reaches tf
+  // is staged whole (lanes placed by a ballot prefix count); the staged
+  // elements are then tested one per lane and listed with the wave's history
+  // candidates; the list is sorted in registers and the four waves' top 64
+  // are merged.
+  using ST = Stage<Tin>;
+  float* svals = (float*)cand + w * VCAP * TL::EPV;
+  int* sids = (int*)((float*)cand + ST::VALS) + w * VCAP;
+  u64* wl = (u64*)((int*)((float*)cand + ST::VALS) + ST::IDS) + w * LCAP;
+  unsigned nv = 0;  // candidate vectors of the wave
 #pragma unroll
-  for (int q = 0; q < PRE; q++) {
-    const int i = (int)threadIdx.x + q * BS;
-    if (i < TS) {
-      const int2 e = hash[i];
-      u64 x = 0ull;
-      if (e.x >= 0) {
-        const float yy = penalise(zs[q], e.y, r) * r.invT;
-        const bool ok = yy > -__builtin_inff() && mask_allows(r, e.x);
-        if (ok) x = comp_key(tg_key(yy), e.x);
-        if (post) post[e.x] = ok ? yy : -__builtin_inff();
+  for (int u = 0; u < TL::U; u++) {
+    const bool pv = vm[u] >= tf;
+    const u64 bal = __ballot(pv);
+    if (bal) {
+      const unsigned sl = nv + lanes_below(bal);
+      if (pv && sl < (unsigned)VCAP) {
+        uint4* dst = (uint4*)(svals + sl * TL::EPV);
+#pragma unroll
+        for (int q = 0; q < TL::EPV / 4; q++)
+          dst[q] = make_uint4(tg_f2u(y[u * TL::EPV + 4 * q]), tg_f2u(y[u * TL::EPV + 4 * q + 1]),
+                              tg_f2u(y[u * TL::EPV + 4 * q + 2]), tg_f2u(y[u * TL::EPV + 4 * q + 3]));
+        sids[sl] = id_of<TL::EPV>(v0, u * TL::EPV);
       }
-      hcomp[i] = x;
+      nv += (unsigned)__popcll(bal);
     }
   }
-  for (int i = (int)threadIdx.x + PRE * BS; i < TS; i += BS) {
-    const int2 e = hash[i];
-    u64 x = 0ull;
-    if (e.x >= 0) {
-      const float yy = penalise(Elem<Tin>::scalar(rowp, e.x), e.y, r) * r.invT;
-      const bool ok = yy > -__builtin_inff() && mask_allows(r, e.x);
-      if (ok) x = comp_key(tg_key(yy), e.x);
-      if (post) post[e.x] = ok ? yy : -__builtin_inff();
-    }
-    hcomp[i] = x;
+  wave_lds_sync();
+  const unsigned nel = (nv < (unsigned)VCAP ? nv : (unsigned)VCAP) * TL::EPV;
+  unsigned nl = 0;  // list entries of the wave
+  for (unsigned e0 = 0; e0 < nel; e0 += 64) {
+    const unsigned e = e0 + (unsigned)lane;
+    const float yy = e < nel ? svals[e] : -__builtin_inff();
+    const bool pc = yy >= tf;
+    const u64 bal = __ballot(pc);
+    const unsigned sl = nl + lanes_below(bal);
+    if (pc && sl < (unsigned)LCAP) wl[sl] = comp_key(tg_key(yy), sids[e / TL::EPV] + (int)(e % TL::EPV));
+    nl += (unsigned)__popcll(bal);
   }
-  // tile candidates into this thread's slots, history candidates into the
-  // compact region
-  u64* hreg = cand + ES * BS;
-  u64* cmp = hreg + HCAP;
-  const int mine_c = emit_lane_slots<TL::EPT, TL::EPV>(cand, y, tf, v0);
-  for (int i = threadIdx.x; i < TS; i += BS)
-    if (hcomp[i] >= thr) {
-      const unsigned pp = atomicAdd(&nhc, 1u);
-      if (pp < (unsigned)HCAP) hreg[pp] = hcomp[i];
-    }
-  if (mine_c > ES) ovf = 1;
-  __syncthreads();
-  if (!ovf && nhc <= (unsigned)HCAP) {
-    // compact: a wave prefix sum of the per-thread counts, one LDS atomic
-    // per wave, then the history entries
-    const unsigned incl = wave_incl_scan((unsigned)mine_c);
-    unsigned wb = 0;
-    if (lane == 63 && incl) wb = atomicAdd(&nbuf, incl);
-    unsigned pos = __shfl(wb, 63, 64) + incl - (unsigned)mine_c;
+  // history candidates: the penalised logit of each history id of the
+  // chunk, computed by its producer (counts are final since the barrier)
 #pragma unroll
-    for (int q = 0; q < ES; q++)
-      if (q < mine_c && pos + q < (unsigned)CCAP) cmp[pos + q] = cand[q * BS + threadIdx.x];
-    __syncthreads();
-    const unsigned ne = nbuf, nh = nhc;
-    for (unsigned i = threadIdx.x; i < nh; i += BS)
-      if (ne + i < (unsigned)CCAP) cmp[ne + i] = hreg[i];
-    if (ne + nh > (unsigned)CCAP) ovf = 1;
-    __syncthreads();
-    if (threadIdx.x == 0) nbuf = ne + nh;
+  for (int q = 0; q < NHID; q++) {
+    u64 x = 0ull;
+    if (prod[q]) {
+      const int id = hid[q], loc = id - v0;
+      const int hc = (int)((hcnt[loc >> 1] >> ((loc & 1) * 16)) & 0xFFFFu);
+      const float yy = penalise(zq[q], hc, r) * r.invT;
+      bool ok = yy > -__builtin_inff();
+      if constexpr (MASK) ok = ok && (!r.mrow || ((mq[q] >> (id & 31)) & 1u));
+      if (post) post[id] = ok ? yy : -__builtin_inff();
+      if (ok) x = comp_key(tg_key(yy), id);
+    }
+    const bool pc = x >= thr;
+    const u64 bal = __ballot(pc);
+    const unsigned sl = nl + lanes_below(bal);
+    if (pc && sl < (unsigned)LCAP) wl[sl] = x;
+    nl += (unsigned)__popcll(bal);
   }
+  wave_lds_sync();
+  const bool wovf = nv > (unsigned)VCAP || nl > (unsigned)LCAP;
+  // the wave's top 64: its list sorted 64 at a time, merged
+  u64 xs = 0ull;
+  if (!wovf) {
+#pragma unroll 1
+    for (unsigned c0 = 0; c0 < nl; c0 += 64) {
+      u64 x = c0 + (unsigned)lane < nl ? wl[c0 + lane] : 0ull;
+      x = wave_sort_desc(x);
+      xs = c0 == 0 ? x : wave_merge_top64(xs, x);
+    }
+  }
+  if (wovf && lane == 0) ovf = 1;
+  if (threadIdx.x == 0) elect = a.S > 1 && arrived == (unsigned)(a.S - 1);
+  tops[w][lane] = xs;
   __syncthreads();
-  if (ovf || nhc > (unsigned)HCAP) {
-    // more candidates than the slots hold (ties, or a skewed tile): the
-    // exact k-th composite among them, then exactly the k candidates >= it
-    auto en = [&](auto f) { each_cand<Tin>(r, has_hist, bitmap, rowp, v0, tf, hcomp, TS, thr, f); };
+  u64 acc = 0ull;  // wave 0: the chunk's top 64 candidates, sorted
+  if (!ovf) {
+    if (w == 0) {
+      acc = xs;
+#pragma unroll
+      for (int i = 1; i < NWB; i++) acc = wave_merge_top64(acc, tops[i][lane]);
+    }
+  } else {
+    // the exact k-th composite among all candidates, then exactly the k
+    // candidates >= it, ranked
+    u64* cmp = cand;
+    auto en = [&](auto f) { each_cand<Tin, MASK>(r, has_hist, bitmap, hcnt, rowp, v0, tf, f); };
     const u64 T = block_select_kth<u64, 64, BS>(en, (unsigned)k, bs);
-    __syncthreads();
-    if (threadIdx.x == 0) nbuf = 0;
     __syncthreads();
     int c2 = 0;
     en([&](u64 x) { c2 += x >= T ? 1 : 0; });
@@ -490,61 +553,95 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
       if (x >= T) cmp[p2++] = x;
     });
     __syncthreads();
+    const int nc = (int)nbuf;
+    rank_into(cmp, tops[0], nc, k);
+    const int n = nc < k ? nc : k;
+    acc = lane < n ? tops[0][lane] : 0ull;
   }
-  // the chunk's top k, sorted, by ranks
-  const int nc = (int)nbuf;
-  rank_into(cmp, tops[0], nc, k);
-  const int n = nc < k ? nc : k;
-  const u64 acc = lane < n ? tops[0][lane] : 0ull;
 
   if (a.S == 1) {
-    if (w == 0) wave_finish_row(a, r, lane < n ? acc : 0ull, n);
+    if (w == 0) {
+      const int n = __popcll(__ballot(acc != 0ull));
+      const int nk = n < k ? n : k;
+      wave_finish_row(a, r, lane < nk ? acc : 0ull, nk);
+    }
     return;
   }
-  // publish the chunk's list; the last workgroup of the row merges
-  if (w == 0) {
-    const u64 x = lane < n ? acc : 0ull;
-    __hip_atomic_store(a.ws + ((long long)b * a.S + c) * KM + lane, x, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // the list is written through before it is counted
-    unsigned prev = 0;
-    if (lane == 0)
-      prev = __hip_atomic_fetch_add(a.cnt + (long long)b * K64_CNT_STRIDE, 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0, 64);
-    if (lane == 0) last_s = prev == (unsigned)(a.S - 1);
+  u64* lists = a.lists + (long long)b * a.S * KM;
+  if (!elect) {
+    // publish the chunk's list for the row's merging workgroup
+    if (w == 0) __hip_atomic_store(lists + (long long)c * KM + lane, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
   }
-  __syncthreads();
-  if (!last_s) return;
 
-  // last arrival: merge the S sorted, zero-padded lists
-  const u64* lists = a.ws + (long long)b * a.S * KM;
+  // the row's last arrival: merge the S sorted, zero-padded lists
+  if (w == 0) own[lane] = acc;
+  __syncthreads();
   u64 racc = 0ull;
+  bool first = true;
   for (int cc = w; cc < a.S; cc += NWB) {
-    const u64 x = __hip_atomic_load(lists + (long long)cc * KM + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    racc = cc == w ? x : wave_merge_top64(racc, x);
+    u64 x;
+    if (cc == c) {
+      x = own[lane];
+    } else {
+      const u64* lp = lists + (long long)cc * KM + lane;
+      x = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int spins = 0;
+      while (__ballot(x == EMPTY) != 0ull) {
+        if (++spins > SPIN_LIMIT) {
+          if (lane == 0) tmo = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        x = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    racc = first ? x : wave_merge_top64(racc, x);
+    first = false;
   }
   racc = merge_waves(racc, tops);
   if (w == 0) {
-    const int nr = __popcll(__ballot(racc != 0ull));
-    const int nk = nr < k ? nr : k;
-    wave_finish_row(a, r, lane < nk ? racc : 0ull, nk);
-    if (lane == 0)
-      __hip_atomic_store(a.cnt + (long long)b * K64_CNT_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tmo) {
+      if (lane == 0) {
+        a.out[b] = -4;
+        write_row_diag(a, b, 0, 0, 0, 0, -1);
+      }
+    } else {
+      const int nr = __popcll(__ballot(racc != 0ull));
+      const int nk = nr < k ? nr : k;
+      wave_finish_row(a, r, lane < nk ? racc : 0ull, nk);
+    }
   }
+  // ready for the next call: lists empty, counter zero
+  for (int cc = w; cc < a.S; cc += NWB)
+    if (cc != c) __hip_atomic_store(lists + (long long)cc * KM + lane, EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename Tin>
+hipError_t launch_t(const SampleArgs& a, size_t lds, hipStream_t st) {
+  const dim3 g(a.B * a.S), blk(K64_NT);
+  const bool vec = a.whole_vec != 0, mask = a.mask_table != nullptr && a.n_states > 0;
+  if (vec && mask) hipLaunchKernelGGL((k64_kernel<Tin, true, true>), g, blk, lds, st, a);
+  else if (vec) hipLaunchKernelGGL((k64_kernel<Tin, true, false>), g, blk, lds, st, a);
+  else if (mask) hipLaunchKernelGGL((k64_kernel<Tin, false, true>), g, blk, lds, st, a);
+  else hipLaunchKernelGGL((k64_kernel<Tin, false, false>), g, blk, lds, st, a);
+  return hipGetLastError();
 }
 
 }  // namespace k64
 
 hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
-  const dim3 g(a.B * a.S), blk(K64_NT);
-  if (dtype == 1) hipLaunchKernelGGL(k64::k64_kernel<uint16_t>, g, blk, lds, st, a);
-  else hipLaunchKernelGGL(k64::k64_kernel<float>, g, blk, lds, st, a);
-  return hipGetLastError();
+  return dtype == 1 ? k64::launch_t<uint16_t>(a, lds, st) : k64::launch_t<float>(a, lds, st);
 }
 
 hipError_t set_k64_lds_limit(size_t bytes) {
-  const void* fns[] = {(const void*)k64::k64_kernel<float>, (const void*)k64::k64_kernel<uint16_t>};
+  const void* fns[] = {
+      (const void*)k64::k64_kernel<float, true, true>,     (const void*)k64::k64_kernel<float, true, false>,
+      (const void*)k64::k64_kernel<float, false, true>,    (const void*)k64::k64_kernel<float, false, false>,
+      (const void*)k64::k64_kernel<uint16_t, true, true>,  (const void*)k64::k64_kernel<uint16_t, true, false>,
+      (const void*)k64::k64_kernel<uint16_t, false, true>, (const void*)k64::k64_kernel<uint16_t, false, false>,
+  };
   hipError_t e = hipSuccess;
   for (const void* f : fns) {
     hipError_t e2 = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);

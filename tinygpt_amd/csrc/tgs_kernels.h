@@ -8,13 +8,16 @@
 
 namespace tgs {
 
-// Fused top_k <= 64 kernel: block size, candidate buffer entries, bitmap
-// words of a 16384-id tile, and the stride (in unsigned words) between the
-// per-row arrival counters (one 128-byte line each).
+// Fused top_k <= 64 kernel: block size, tile (ids per chunk at most),
+// longest history it takes, exact-path candidate capacity, candidate buffer
+// entries (u64), bitmap words of a tile, and the stride (in unsigned words)
+// between the per-row arrival counters (one 128-byte line each).
 constexpr int K64_NT = 256;
+constexpr int K64_TILE = 16384;
+constexpr int K64_MAX_HIST = 1024;
 constexpr int K64_CAP = 1024;
-constexpr int K64_CAND_ENTRIES = 8 * K64_NT + 512 + K64_CAP + 16;  // thread slots, history, compacted
-constexpr int K64_BITMAP_WORDS = 512;
+constexpr int K64_CAND_ENTRIES = 2176;  // per-wave candidate staging (bf16 size); the exact path reuses it
+constexpr int K64_BITMAP_WORDS = K64_TILE / 32;
 constexpr int K64_CNT_STRIDE = 32;
 
 struct SampleArgs {
@@ -40,6 +43,7 @@ struct SampleArgs {
   int ws_stride;         // entries per chunk list (64 fast variant, KMAX otherwise)
   int* ws_cnt;           // [B*S]
   unsigned* cnt;         // fused kernel: [B * K64_CNT_STRIDE] arrival counters (zero between calls)
+  unsigned long long* lists;  // fused kernel: [B * S][64] chunk lists (all ~0 between calls)
   int full_rows;         // 1: full_kernel runs after the chunk kernels
   int hint_k;            // the launch hint's max_top_k (INT_MAX without a hint)
   tgs_debug dbg;
