@@ -1,16 +1,26 @@
 #!/usr/bin/env python3
 """Benchmark of the decode-time sampler on one MI355X.
 
-A step is one tgs_sample call over one B=64, V=128256 fp32 batch (the
-headline configuration: penalties from a 512-id history, temperature,
-top-k 50, top-p 0.9, one host uniform per row).  Inputs are resident in HBM before timing; 16
-distinct logits buffers (525 MB) rotate so the 256 MB Infinity Cache cannot
-serve repeats.  Launches are captured in a HIP graph (16 launches, one per
-buffer) and replayed; the timed region is bracketed by synchronisations and
-HIP events on the launch stream.
+A step is one sampler call over one batch of seeded synthetic input.  The
+default workload is the headline configuration C2 (B=64, V=128256 fp32:
+penalties from a 512-id history, temperature, top-k 50, top-p 0.9, one host
+uniform per row); `--workload` selects one of the other configurations of the
+same generator set (tinygpt_amd/workloads.py):
 
-Prints one JSON line with the roofline of the sampling kernel and the CPU
-oracle timed on this host.
+  c1  B=1, V=256 byte-level sampling (latency-bound)
+  c2  B=64, V=128256 fp32, full chain (headline)
+  c3  B=128, V=32000 fp32, grammar mask table of 4096 states, greedy + top-p
+  c4  B=1024, V=151936 bf16, per-row top-k/top-p/T/repetition
+  c5  B=32 sequences, k=8 draft tokens, V=128256 speculative verification
+
+Inputs are resident in HBM before timing; distinct input sets rotate so the
+256 MB Infinity Cache cannot serve repeats (at least 512 MB in rotation
+where a set is large).  The calls are captured in a HIP graph (one call per
+set) and replayed; the timed region is bracketed by synchronisations and HIP
+events on the launch stream.
+
+Prints one JSON line with the roofline of the call and the CPU oracle timed
+on this host over a bounded sample.
 
 `--calibrate-copy MIB` instead runs a plain device-to-device copy of MIB MiB
 a few times: profiling it with the FETCH_SIZE / WRITE_SIZE counters gives the
@@ -27,9 +37,9 @@ import time
 
 import numpy as np
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "sampled rows/sec @B=64,V=128256 full chain; HBM GB/s as % of peak"
 HBM_PEAK_GBS = 8000.0
-ROT = 16
 
 
 def parse():
@@ -37,6 +47,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
@@ -45,46 +56,183 @@ def parse():
     return ap.parse_args()
 
 
-def make_sets(n, B, V, H):
-    from tinygpt_amd import workloads as W
-
-    sets = []
-    for i in range(n):
-        sets.append(W.config2(B=B, V=V, H=H, seed_offset=i * 1000))
-    return sets
-
-
-def cpu_baseline(sets, seconds):
-    """Oracle (C restatement of the reference sampler) on this host: rows/s
-    with all host threads (up to 16) and with one thread."""
-    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle"))
+def oracle_mod():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
 
     pyoracle.build()
-    nthr = max(1, min(16, os.cpu_count() or 1))
+    return pyoracle
 
-    def run(nthreads, budget):
-        rows = 0
-        t0 = time.perf_counter()
-        i = 0
-        ids = {}
-        while time.perf_counter() - t0 < budget or rows == 0:
-            s = sets[i % len(sets)]
-            r = pyoracle.sample_batch(s["logits"], s["params"], s["u"], hist=s["hist"],
-                                      hist_len=s["hist_len"], nthreads=nthreads)
-            ids[i % len(sets)] = r["ids"]
-            rows += s["logits"].shape[0]
-            i += 1
-        return rows / (time.perf_counter() - t0), rows, ids
 
-    rate_n, rows_n, ids = run(nthr, seconds * 0.6)
-    rate_1, rows_1, _ = run(1, seconds * 0.4)
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def timed_loop(fn, n_sets, seconds):
+    """Calls fn(i) over the sets for about `seconds`; returns (units/s, units, outputs by set)."""
+    units = 0
+    outs = {}
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds or units == 0:
+        o, n = fn(i % n_sets)
+        outs[i % n_sets] = o
+        units += n
+        i += 1
+    return units / (time.perf_counter() - t0), units, outs
+
+
+# ---------------------------------------------------------------- workloads
+class Sampling:
+    """c1-c4: one tgs_sample call per step over one batch."""
+
+    def __init__(self, name, torch, tg, W):
+        self.name = name
+        self.torch = torch
+        dev = "cuda:0"
+        if name == "c1":
+            self.rot, self.B, self.V, self.H = 16, 1, 256, 64
+            c1 = W.config1_step_inputs(steps=self.rot, V=self.V, H=self.H)
+            self.sets = [dict(logits=c1["logits"][i:i + 1].copy(), params=c1["params"], u=c1["u"][i:i + 1].copy(),
+                              hist=c1["hist0"][None, :].copy(), hist_len=np.array([self.H], np.int32),
+                              mask_table=None) for i in range(self.rot)]
+            self.config = {"workload": "c1_byte_level", "B": 1, "V": 256, "history": 64, "top_k": 40, "top_p": 0.95,
+                           "temperature": 0.8, "repetition": 1.1}
+            self.dtype = "f32"
+        elif name == "c2":
+            self.rot, self.B, self.V, self.H = 16, 64, 128256, 512
+            self.sets = [W.config2(B=self.B, V=self.V, H=self.H, seed_offset=i * 1000) for i in range(self.rot)]
+            self.config = {"workload": "c2_llama3_bpe", "B": 64, "V": 128256, "history": 512, "top_k": 50,
+                           "top_p": 0.9, "temperature": 0.7, "presence": 0.5, "frequency": 0.3}
+            self.dtype = "f32"
+        elif name == "c3":
+            self.rot, self.B, self.V, self.H = 16, 128, 32000, 0
+            base = W.config3(B=self.B, V=self.V)
+            self.sets = [base]
+            g = np.random.default_rng(W.SEED_BASE + 3 + 7777)
+            for i in range(1, self.rot):
+                s = dict(base)
+                s["logits"] = W.normal_f32(g, (self.B, self.V), 2.5)
+                p = base["params"].copy()
+                p["mask_state"] = g.integers(0, base["mask_table"].shape[0], size=self.B).astype(np.int32)
+                s["params"] = p
+                s["u"] = W.uniforms(g, self.B)
+                self.sets.append(s)
+            self.config = {"workload": "c3_grammar", "B": 128, "V": 32000, "mask_states": 4096,
+                           "greedy_rows": 64, "top_p": 0.95, "temperature": 1.0}
+            self.dtype = "f32"
+        else:  # c4
+            self.rot, self.B, self.V, self.H = 2, 1024, 151936, 256
+            self.sets = [W.config4(B=self.B, V=self.V, H=self.H, seed_offset=i * 1000) for i in range(self.rot)]
+            self.config = {"workload": "c4_large_batch_bf16", "B": 1024, "V": 151936, "history": 256,
+                           "top_k": "U{1..1024}", "top_p": "U[0.5,1]", "temperature": "U[0.3,1.5]",
+                           "repetition": "U[1.05,1.3]"}
+            self.dtype = "bf16 (upcast to f32)"
+        mt = self.sets[0].get("mask_table")
+        self.sampler = tg.Sampler(device=0, max_batch=self.B, max_vocab=self.V, max_hist=max(self.H, 1))
+        if mt is not None:
+            self.sampler.set_mask_table(mt, self.V)
+        else:
+            self.sampler.set_mask_table(np.zeros((0, 1), np.uint32), 1)
+        self.d = []
+        for s in self.sets:
+            lg = s["logits"]
+            t = torch.from_numpy(lg).to(dev)
+            if lg.dtype == np.uint16:
+                t = t.view(torch.bfloat16)
+            self.d.append(dict(
+                logits=t,
+                params=tg.params_to_device(s["params"], dev),
+                u=torch.from_numpy(s["u"]).to(dev),
+                hist=None if s.get("hist") is None else torch.from_numpy(s["hist"]).to(dev),
+                hist_len=None if s.get("hist_len") is None else torch.from_numpy(s["hist_len"]).to(dev),
+                out=torch.empty(self.B, dtype=torch.int32, device=dev),
+            ))
+        self.hints = [tg.batch_hint(s["params"], self.V) for s in self.sets]
+        self.alg_bytes = W.algorithmic_bytes_per_row(
+            "c3" if name == "c3" else name, self.V, self.H, dtype_bytes=2 if name == "c4" else 4) * self.B
+        self.units_per_step = self.B
+        self.unit = "rows/s"
+        self.metric = METRIC if name == "c2" else f"sampled rows/sec, workload {self.config['workload']}"
+
+    def launch(self, i, stream):
+        x = self.d[i % self.rot]
+        self.sampler.sample(x["logits"], x["params"], x["u"], hist=x["hist"], hist_len=x["hist_len"],
+                            out=x["out"], stream=stream, hint=self.hints[i % self.rot])
+
+    def gpu_outputs(self):
+        return {i: self.d[i]["out"].cpu().numpy() for i in range(self.rot)}
+
+    def cpu_call(self, pyoracle, nthreads):
+        def fn(i):
+            s = self.sets[i]
+            r = pyoracle.sample_batch(s["logits"], s["params"], s["u"], hist=s.get("hist"),
+                                      hist_len=s.get("hist_len"), mask_table=s.get("mask_table"),
+                                      nthreads=nthreads)
+            return r["ids"], s["logits"].shape[0]
+        return fn
+
+
+class SpecVerify:
+    """c5: one tgs_spec_verify call per step over B=32 sequences of k=8 drafts."""
+
+    def __init__(self, name, torch, tg, W):
+        dev = "cuda:0"
+        self.name = name
+        self.rot, self.B, self.k, self.V = 2, 32, 8, 128256
+        self.sets = [W.config5(B=self.B, k=self.k, V=self.V, seed_offset=i * 1000) for i in range(self.rot)]
+        self.sampler = tg.Sampler(device=0, max_batch=self.B, max_vocab=self.V, max_hist=1)
+        self.sampler.reserve_spec(self.B, self.k)
+        self.d = []
+        for s in self.sets:
+            self.d.append(dict(
+                target=torch.from_numpy(s["target"]).to(dev), draft=torch.from_numpy(s["draft"]).to(dev),
+                dtok=torch.from_numpy(s["dtok"]).to(dev), T=torch.from_numpy(s["T"]).to(dev),
+                u_acc=torch.from_numpy(s["u_acc"]).to(dev), u_res=torch.from_numpy(s["u_res"]).to(dev),
+                n_acc=torch.empty(self.B, dtype=torch.int32, device=dev),
+                out=torch.empty(self.B, self.k + 1, dtype=torch.int32, device=dev),
+            ))
+        self.alg_bytes = W.algorithmic_bytes_per_row("c5", self.V, k=self.k) * self.B
+        self.units_per_step = self.B
+        self.unit = "rows/s"
+        self.metric = "verified sequences/sec, workload c5_spec_verify"
+        self.config = {"workload": "c5_spec_verify", "B": 32, "draft_k": 8, "V": 128256, "temperature": 1.0}
+        self.dtype = "f32"
+
+    def launch(self, i, stream):
+        x = self.d[i % self.rot]
+        self.sampler.spec_verify(x["target"], x["draft"], x["dtok"], x["T"], x["u_acc"], x["u_res"],
+                                 n_acc=x["n_acc"], out=x["out"], stream=stream)
+
+    def gpu_outputs(self):
+        return {i: np.concatenate([self.d[i]["n_acc"].cpu().numpy()[:, None], self.d[i]["out"].cpu().numpy()], 1)
+                for i in range(self.rot)}
+
+    def tokens_per_step(self):
+        return float(np.mean([(self.d[i]["n_acc"].cpu().numpy() + 1).sum() for i in range(self.rot)]))
+
+    def cpu_call(self, pyoracle, nthreads):
+        def fn(i):
+            s = self.sets[i]
+            r = pyoracle.spec_verify_batch(s["target"], s["draft"], s["dtok"], s["T"], s["u_acc"], s["u_res"],
+                                           nthreads=nthreads)
+            return np.concatenate([r["n_acc"][:, None], r["out"]], 1), self.B
+        return fn
+
+
+def cpu_baseline(wl, seconds):
+    """The oracle (C restatement of the reference sampler) on this host:
+    units/s with all host threads (up to 16) and with one thread."""
+    pyoracle = oracle_mod()
+    nthr = cpu_threads()
+    rate_n, units_n, outs = timed_loop(wl.cpu_call(pyoracle, nthr), wl.rot, seconds * 0.6)
+    rate_1, units_1, _ = timed_loop(wl.cpu_call(pyoracle, 1), wl.rot, seconds * 0.4)
     return dict(
-        value=round(rate_n, 2), unit="rows/s", cores=nthr, kind="port",
-        sample=f"{rows_n} C2 rows (B=64 batches cycling over {len(sets)} seeded sets) on {nthr} threads; "
-               f"1 thread: {round(rate_1, 2)} rows/s over {rows_1} rows",
+        value=round(rate_n, 2), unit=wl.unit, cores=nthr, kind="port",
+        sample=f"{units_n} rows of {wl.config['workload']} (batches of {wl.B} cycling over {wl.rot} seeded sets) "
+               f"on {nthr} threads; 1 thread: {round(rate_1, 2)} {wl.unit} over {units_1} rows",
         single_thread_value=round(rate_1, 2),
-    ), ids
+    ), outs
 
 
 def calibrate_copy(torch, mib, reps=8):
@@ -105,6 +253,12 @@ def calibrate_copy(torch, mib, reps=8):
                       "ms_per_copy": round(ms, 4), "GBps": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
+TRAFFIC_FILES = {"c2": "k64_kernel_c2_traffic.json", "c3": "c3_grammar_traffic.json",
+                 "c4": "c4_large_batch_traffic.json", "c5": "c5_spec_verify_traffic.json"}
+KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c3": "chunk_kernel + full_kernel (one call)",
+           "c4": "chunk_kernel + merge_kernel (one call)", "c5": "spec_stats_kernel + spec_verify_kernel (one call)"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -121,35 +275,14 @@ def main():
     import tinygpt_amd as tg
     from tinygpt_amd import workloads as W
 
-    dev = "cuda:0"
-    B, V, H = 64, 128256, 512
-    sets = make_sets(ROT, B, V, H)
-    sampler = tg.Sampler(device=0, max_batch=B, max_vocab=V, max_hist=H)
-    sampler.set_mask_table(np.zeros((0, 1), np.uint32), 1)
-    d = []
-    for s in sets:
-        d.append(dict(
-            logits=torch.from_numpy(s["logits"]).to(dev),
-            params=tg.params_to_device(s["params"], dev),
-            u=torch.from_numpy(s["u"]).to(dev),
-            hist=torch.from_numpy(s["hist"]).to(dev),
-            hist_len=torch.from_numpy(s["hist_len"]).to(dev),
-            out=torch.empty(B, dtype=torch.int32, device=dev),
-        ))
+    wl = SpecVerify(args.workload, torch, tg, W) if args.workload == "c5" else Sampling(args.workload, torch, tg, W)
     torch.cuda.synchronize()
-
-    stream = torch.cuda.Stream(device=dev)  # default priority
-
-    hints = [tg.batch_hint(s["params"], V) for s in sets]
-
-    def launch(i):
-        x = d[i % ROT]
-        sampler.sample(x["logits"], x["params"], x["u"], hist=x["hist"], hist_len=x["hist_len"],
-                       out=x["out"], stream=stream.cuda_stream, hint=hints[i % ROT])
+    stream = torch.cuda.Stream(device="cuda:0")  # default priority
+    ROT = wl.rot
 
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
-            launch(i)
+            wl.launch(i, stream.cuda_stream)
     torch.cuda.synchronize()
 
     graph = None
@@ -157,7 +290,7 @@ def main():
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream, capture_error_mode="thread_local"):
             for i in range(ROT):
-                launch(i)
+                wl.launch(i, stream.cuda_stream)
         torch.cuda.synchronize()
         for _ in range(3):
             graph.replay()
@@ -175,37 +308,38 @@ def main():
                 graph.replay()
         else:
             for i in range(steps):
-                launch(i)
+                wl.launch(i, stream.cuda_stream)
         ev1.record(stream)
     torch.cuda.synchronize()
     ms_total = ev0.elapsed_time(ev1)
     ms_per_step = ms_total / steps
 
     # parity of the timed outputs against the oracle (same inputs)
-    gpu_ids = {i: d[i]["out"].cpu().numpy() for i in range(ROT)}
+    gpu_out = wl.gpu_outputs()
     cpu = None
     agreement = None
     if not args.no_cpu:
-        cpu, cpu_ids = cpu_baseline(sets, args.cpu_seconds)
-        match = [np.array_equal(gpu_ids[i], cpu_ids[i]) for i in cpu_ids]
-        agreement = float(np.mean([np.mean(gpu_ids[i] == cpu_ids[i]) for i in cpu_ids]))
-        if not all(match):
-            print("WARNING: GPU ids differ from the oracle", file=sys.stderr)
+        cpu, cpu_out = cpu_baseline(wl, args.cpu_seconds)
+        agreement = float(np.mean([np.mean(gpu_out[i] == cpu_out[i]) for i in cpu_out]))
+        if not all(np.array_equal(gpu_out[i], cpu_out[i]) for i in cpu_out):
+            print("WARNING: GPU outputs differ from the oracle", file=sys.stderr)
 
-    alg_bytes = W.algorithmic_bytes_per_row("c2", V, H) * B  # 4V + 4H per row
-    achieved = alg_bytes / (ms_per_step * 1e-3) / 1e9
-    rows_per_s = B / (ms_per_step * 1e-3)
+    achieved = wl.alg_bytes / (ms_per_step * 1e-3) / 1e9
+    units_per_s = wl.units_per_step / (ms_per_step * 1e-3)
     traffic = None
-    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "k64_kernel_c2_traffic.json")
-    if os.path.exists(tfile):
+    tf = TRAFFIC_FILES.get(args.workload)
+    if tf and os.path.exists(os.path.join(ROOT, "profiles", tf)):
         try:
-            traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+            traffic = json.load(open(os.path.join(ROOT, "profiles", tf))).get("hbm_bytes_per_launch")
         except Exception:
             traffic = None
+    cfg = dict(wl.config)
+    cfg["rotating_sets"] = ROT
+    cfg["timing"] = "graph replay" if graph is not None else "eager"
     line = {
-        "metric": METRIC,
-        "value": round(rows_per_s, 1),
-        "unit": "rows/s",
+        "metric": wl.metric,
+        "value": round(units_per_s, 1),
+        "unit": wl.unit,
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
@@ -213,17 +347,17 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": wl.dtype,
         "data": "synthetic",
-        "config": {"workload": "c2_llama3_bpe", "B": B, "V": V, "history": H, "top_k": 50,
-                   "top_p": 0.9, "temperature": 0.7, "presence": 0.5, "frequency": 0.3,
-                   "rotating_buffers": ROT, "timing": "graph replay" if graph is not None else "eager"},
+        "config": cfg,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "alg_bytes_per_launch": alg_bytes, "kernel": "k64_kernel<float>"},
+                     "alg_bytes_per_launch": wl.alg_bytes, "kernel": KERNELS[args.workload]},
         "cpu_baseline": cpu,
         "id_agreement": agreement,
     }
+    if isinstance(wl, SpecVerify):
+        line["tokens_per_s"] = round(wl.tokens_per_step() / (ms_per_step * 1e-3), 1)
     print(json.dumps(line), flush=True)
 
 
