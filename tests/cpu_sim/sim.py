@@ -59,3 +59,26 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
                  cut_ids=rd("out_cut.bin", np.int32),
                  post_logits=rd("out_post.bin", np.float32).reshape(B, V) if post else None)
         return r
+
+
+def run_spec(target, draft, dtok, T, u_acc, u_res, timeout=600):
+    """tgs_spec_verify through the simulation: (n_acc [B], out [B, k+1])."""
+    target = np.ascontiguousarray(target)
+    B, k1, V = target.shape
+    k = k1 - 1
+    dtype = 1 if target.dtype == np.uint16 else 0
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        target.tofile(os.path.join(d, "target.bin"))
+        np.ascontiguousarray(draft).tofile(os.path.join(d, "draft.bin"))
+        np.ascontiguousarray(dtok, np.int32).tofile(os.path.join(d, "dtok.bin"))
+        np.ascontiguousarray(T, np.float32).tofile(os.path.join(d, "T.bin"))
+        np.ascontiguousarray(u_acc, np.float32).tofile(os.path.join(d, "u_acc.bin"))
+        np.ascontiguousarray(u_res, np.float32).tofile(os.path.join(d, "u_res.bin"))
+        with open(os.path.join(d, "meta.txt"), "w") as f:
+            f.write(f"{B} {k} {V} {dtype}\n")
+        r = subprocess.run([BIN, "spec", d], capture_output=True, text=True, timeout=timeout)
+        if r.returncode != 0:
+            raise RuntimeError(f"simulation failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")
+        n_acc = np.fromfile(os.path.join(d, "out_nacc.bin"), np.int32)
+        out = np.fromfile(os.path.join(d, "out_spec.bin"), np.int32).reshape(B, k + 1)
+        return n_acc, out

@@ -139,3 +139,60 @@ def test_k64_bf16_and_mask(sim, oracle):
     params["mask_state"] = np.array([0, 1, 2, -1, 0, 1, -1, 2])
     _check(sim, oracle, W.f32_to_bf16_bits(x), params, u, hist, hist_len, mask=table,
            hint=tg.batch_hint(params, V), split=3, kept_cap=64)
+
+
+def _spec_case(seed, B, k, V, T, bf16=False):
+    from tinygpt_amd import workloads as W
+
+    c = W.config5(B=B, k=k, V=V, seed_offset=seed, T=1.0)
+    c["T"][:] = T
+    c["dtok"][::3, 0] = np.argmin(c["target"][::3, 0], axis=-1)  # early rejections
+    if B > 2:
+        c["T"][2] = 0.0  # a greedy sequence among stochastic ones
+    if bf16:
+        c["target"] = W.f32_to_bf16_bits(c["target"])
+        c["draft"] = W.f32_to_bf16_bits(c["draft"])
+    return c
+
+
+def _spec_check(sim, oracle, c):
+    n_s, out_s = sim.run_spec(c["target"], c["draft"], c["dtok"], c["T"], c["u_acc"], c["u_res"])
+    o = oracle.spec_verify_batch(c["target"], c["draft"], c["dtok"], c["T"], c["u_acc"], c["u_res"])
+    np.testing.assert_array_equal(n_s, o["n_acc"])
+    np.testing.assert_array_equal(out_s, o["out"])
+    return o
+
+
+@pytest.mark.parametrize("T", [1.0, 0.5])
+def test_spec_blocks_decide_mass_draw(sim, oracle, T):
+    # V = 2500: three blocks of 1024 ids, the last one partial, rows not
+    # 16-byte aligned (scalar edge loads)
+    o = _spec_check(sim, oracle, _spec_case(11, 6, 3, 2500, T))
+    assert (o["n_acc"] >= 0).all()
+
+
+def test_spec_bf16_aligned(sim, oracle):
+    _spec_check(sim, oracle, _spec_case(12, 4, 2, 2048, 1.0, bf16=True))
+
+
+def test_spec_zero_residual_falls_back_to_target(sim, oracle):
+    # draft == target and the first draft token has probability 0 in both:
+    # rejected (ratio 0), residual 0 everywhere -> draw from the target row
+    from tinygpt_amd import workloads as W
+
+    c = W.config5(B=3, k=2, V=1500, seed_offset=13)
+    c["draft"] = c["target"][:, :2].copy()
+    c["target"][np.arange(3), 0, c["dtok"][:, 0]] = -np.inf
+    c["draft"][np.arange(3), 0, c["dtok"][:, 0]] = -np.inf
+    o = _spec_check(sim, oracle, c)
+    assert (o["n_acc"] == 0).all() and (o["info"]["resampled"] == 2).all()
+
+
+def test_spec_invalid_rows(sim, oracle):
+    from tinygpt_amd import workloads as W
+
+    c = W.config5(B=4, k=2, V=64, seed_offset=4)
+    c["dtok"][0, 1] = 64
+    c["T"][1] = np.nan
+    c["u_acc"][2, 0] = 1.0
+    _spec_check(sim, oracle, c)

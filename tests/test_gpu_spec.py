@@ -65,3 +65,27 @@ def test_spec_invalid(sampler, oracle):
     c["T"][1] = np.nan
     c["u_acc"][2, 0] = 1.0
     _check(sampler, oracle, "spec invalid", c)
+
+
+def test_spec_zero_residual_falls_back_to_target(sampler, oracle):
+    # draft == target and the first draft token has probability 0 in both:
+    # rejected (ratio 0), residual 0 everywhere -> draw from the target row
+    from tinygpt_amd import workloads as W
+
+    c = W.config5(B=5, k=3, V=4100, seed_offset=13)
+    c["draft"] = c["target"][:, :3].copy()
+    c["target"][np.arange(5), 0, c["dtok"][:, 0]] = -np.inf
+    c["draft"][np.arange(5), 0, c["dtok"][:, 0]] = -np.inf
+    o = _check(sampler, oracle, "spec zero residual", c)
+    assert (o["n_acc"] == 0).all() and (o["info"]["resampled"] == 2).all()
+
+
+def test_spec_k64_all_accepted(sampler, oracle):
+    # the longest draft (k = 64) with every token accepted (u_acc = 0): the
+    # bonus draw from target row k, and all 65 outputs written
+    from tinygpt_amd import workloads as W
+
+    c = W.config5(B=2, k=64, V=2048, seed_offset=14)
+    c["u_acc"][:] = 0.0
+    o = _check(sampler, oracle, "spec k64", c)
+    assert (o["n_acc"] == 64).all()

@@ -31,9 +31,11 @@ struct tgs_ctx {
   unsigned long long* k64_lists = nullptr;  // fused kernel chunk lists, [max_batch * kMaxSplit][64]
   uint32_t* mask_table = nullptr;
   int n_states = 0, mask_vocab = 0, mask_words = 0;
-  float* spec_stats = nullptr;
-  unsigned long long* spec_arg = nullptr;
-  int spec_b = 0, spec_k = -1;
+  float* spec_blk_m = nullptr;             // speculative workspace (tgs_reserve_spec)
+  unsigned long long* spec_blk_q = nullptr;
+  unsigned long long* spec_blk_w = nullptr;
+  void* spec_state = nullptr;
+  int spec_b = 0, spec_k = -1, spec_nbs = 0;
   std::string err;
 };
 
@@ -76,12 +78,17 @@ int log2i(int x) {
 }
 
 void free_spec(tgs_ctx* h) {
-  if (h->spec_stats) (void)hipFree(h->spec_stats);
-  if (h->spec_arg) (void)hipFree(h->spec_arg);
-  h->spec_stats = nullptr;
-  h->spec_arg = nullptr;
+  if (h->spec_blk_m) (void)hipFree(h->spec_blk_m);
+  if (h->spec_blk_q) (void)hipFree(h->spec_blk_q);
+  if (h->spec_blk_w) (void)hipFree(h->spec_blk_w);
+  if (h->spec_state) (void)hipFree(h->spec_state);
+  h->spec_blk_m = nullptr;
+  h->spec_blk_q = nullptr;
+  h->spec_blk_w = nullptr;
+  h->spec_state = nullptr;
   h->spec_b = 0;
   h->spec_k = -1;
+  h->spec_nbs = 0;
 }
 
 // Chunks per row of the fused top_k <= 64 kernel: every chunk is one tile
@@ -359,9 +366,13 @@ int tgs_reserve_spec(tgs_handle h, int max_batch, int max_k) {
   const int nb = std::max(max_batch, h->spec_b);
   const int nk = std::max(max_k, h->spec_k);
   free_spec(h);
+  // per row: block maxima and masses for every block of the handle's vocab
   const size_t rows = (size_t)nb * (2 * nk + 1);
-  hipError_t e = hipMalloc(&h->spec_stats, sizeof(float) * 2 * rows);
-  if (e == hipSuccess) e = hipMalloc(&h->spec_arg, sizeof(unsigned long long) * rows);
+  const int nbs = (h->max_vocab + tgs::SPEC_BLOCK - 1) / tgs::SPEC_BLOCK;
+  hipError_t e = hipMalloc(&h->spec_blk_m, sizeof(float) * rows * nbs);
+  if (e == hipSuccess) e = hipMalloc(&h->spec_blk_q, sizeof(unsigned long long) * rows * nbs);
+  if (e == hipSuccess) e = hipMalloc(&h->spec_blk_w, sizeof(unsigned long long) * (size_t)nb * nbs);
+  if (e == hipSuccess) e = hipMalloc(&h->spec_state, (size_t)32 * nb);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     free_spec(h);
@@ -369,6 +380,7 @@ int tgs_reserve_spec(tgs_handle h, int max_batch, int max_k) {
   }
   h->spec_b = nb;
   h->spec_k = nk;
+  h->spec_nbs = nbs;
   return TGS_OK;
 }
 
@@ -404,8 +416,12 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
   a.u_res = d_u_res;
   a.n_acc = d_n_acc;
   a.out = d_out;
-  a.ws_stats = h->spec_stats;
-  a.ws_arg = h->spec_arg;
+  a.nb = (V + tgs::SPEC_BLOCK - 1) / tgs::SPEC_BLOCK;
+  a.nbs = h->spec_nbs;
+  a.blk_m = h->spec_blk_m;
+  a.blk_q = h->spec_blk_q;
+  a.blk_w = h->spec_blk_w;
+  a.seq_state = h->spec_state;
   hipError_t e = tgs::launch_spec(a, dt, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(h, e, "spec kernel launch");
   return TGS_OK;

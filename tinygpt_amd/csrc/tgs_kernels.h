@@ -60,9 +60,15 @@ struct SpecArgs {
   const float* u_res;
   int* n_acc;
   int* out;
-  float* ws_stats;             // [B][2k+1][2] (m, S)
-  unsigned long long* ws_arg;  // [B][2k+1] argmax composite
+  int nb;                      // blocks of SPEC_BLOCK ids per row
+  int nbs;                     // block stride of the per-row workspace arrays (>= nb)
+  float* blk_m;                // [B][2k+1][nbs] block maxima
+  unsigned long long* blk_q;   // [B][2k+1][nbs] exact block masses (greedy: block argmax composite)
+  unsigned long long* blk_w;   // [B][nbs] draw mass per block of the row drawn from
+  void* seq_state;             // [B] 32-byte per-sequence decision
 };
+
+constexpr int SPEC_MAX_K = 64;  // most draft tokens per sequence
 
 // Launches the chunk kernel, the merge kernel when rows are split (a.S > 1)
 // and the full-path kernel when a.full_rows is set, in that order on st.

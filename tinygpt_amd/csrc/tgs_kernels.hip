@@ -28,11 +28,7 @@
 // Every device function is inlined into its kernel: no kernel makes calls,
 // so none needs a call stack or passes pointers to private memory.
 //
-// spec_stats_kernel / spec_verify_kernel: speculative verification.  One
-// workgroup per (sequence, row) computes the row maximum and canonical
-// softmax denominator (block maxima, exact 2^-40 block sums, pairwise fp32
-// tree); one workgroup per sequence then runs the accept/reject scan and
-// the residual or bonus draw.
+// Speculative verification lives in tgs_spec.hip.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 #include "tgs_row.h"
@@ -692,367 +688,6 @@ __global__ __launch_bounds__(NT) void merge_kernel(SampleArgs a) {
   finalize_topk(a, r, cand, n, s);
 }
 
-// ------------------------------------------------------------------ spec verify
-
-template <typename Tin>
-struct SpecTile {
-  static constexpr int EPV = Elem<Tin>::EPV;
-  static constexpr int NV = SPEC_BLOCK / (64 * EPV);  // vectors per lane per block
-  static constexpr int EPL = NV * EPV;                // elements per lane per block
-};
-
-// id of (vector i, element e) for this lane within block blk
-template <typename Tin>
-__device__ __forceinline__ int spec_id(int blk, int i, int e) {
-  constexpr int EPV = Elem<Tin>::EPV;
-  return blk * SPEC_BLOCK + i * 64 * EPV + lane_id() * EPV + e;
-}
-
-template <typename Tin>
-__device__ __forceinline__ void spec_load_block(const Tin* rowp, int blk, int V, bool aligned,
-                                                float invT, float (&y)[SpecTile<Tin>::EPL]) {
-  using ST = SpecTile<Tin>;
-  uint4 raw[ST::NV];
-#pragma unroll
-  for (int i = 0; i < ST::NV; i++) raw[i] = load_vec<Tin>(rowp, spec_id<Tin>(blk, i, 0), V, aligned);
-#pragma unroll
-  for (int i = 0; i < ST::NV; i++)
-#pragma unroll
-    for (int e = 0; e < ST::EPV; e++) {
-      const float t = Elem<Tin>::get(raw[i], e) * invT;
-      y[i * ST::EPV + e] = (t > -__builtin_inff()) ? t : -__builtin_inff();
-    }
-}
-
-struct SpecScratch {
-  float mb[256];
-  u64 qb[256];
-  u64 wsum[256];
-};
-
-template <typename Tin>
-__device__ __forceinline__ const Tin* spec_row_ptr(const SpecArgs& a, int b, int r) {
-  const int k = a.k;
-  if (r <= k) return (const Tin*)a.target + ((long long)b * (k + 1) + r) * a.V;
-  return (const Tin*)a.draft + ((long long)b * k + (r - k - 1)) * a.V;
-}
-
-// Row statistics: m, S (canonical) and the argmax composite (greedy rows).
-template <typename Tin>
-__global__ __launch_bounds__(NT) void spec_stats_kernel(SpecArgs a) {
-  using ST = SpecTile<Tin>;
-  __shared__ BlockScratch s;
-  __shared__ SpecScratch ss;
-  const int R = 2 * a.k + 1;
-  const int b = blockIdx.x / R, r = blockIdx.x % R;
-  if (b >= a.B) return;
-  const float T = a.T[b];
-  if (__builtin_isnan(T)) return;  // reported by the verify kernel
-  const bool greedy = !(T > 0.0f);
-  if (greedy && r > a.k) return;  // draft rows unused by greedy verification
-  const float Tc = T > 1e-5f ? T : 1e-5f;
-  const float invT = greedy ? 1.0f : 1.0f / Tc;
-  const Tin* rowp = spec_row_ptr<Tin>(a, b, r);
-  const int nb = (a.V + SPEC_BLOCK - 1) / SPEC_BLOCK;
-  const int w = threadIdx.x >> 6;
-  u64 arg = 0;
-  for (int blk = w; blk < nb; blk += NW) {
-    float y[ST::EPL];
-    spec_load_block<Tin>(rowp, blk, a.V, a.aligned, invT, y);
-    if (greedy) {
-#pragma unroll
-      for (int j = 0; j < ST::EPL; j++)
-        if (y[j] > -__builtin_inff()) {
-          const u64 c = comp_key(tg_key(y[j]), spec_id<Tin>(blk, j / ST::EPV, j % ST::EPV));
-          arg = c > arg ? c : arg;
-        }
-      continue;
-    }
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int j = 0; j < ST::EPL; j++) mx = fmaxf(mx, y[j]);
-    mx = wave_maxf(mx);
-    u64 q = 0;
-    if (mx > -__builtin_inff()) {
-#pragma unroll
-      for (int j = 0; j < ST::EPL; j++)
-        if (y[j] > -__builtin_inff()) q += tg_q40(tg_weight(y[j], mx));
-    }
-    q = wave_sum(q);
-    if (lane_id() == 0) {
-      ss.mb[blk] = mx;
-      ss.qb[blk] = q;
-    }
-  }
-  float* stat = a.ws_stats + ((long long)b * R + r) * 2;
-  if (greedy) {
-    arg = block_max(arg, s.red64);
-    if (threadIdx.x == 0) a.ws_arg[(long long)b * R + r] = arg;
-    return;
-  }
-  __syncthreads();
-  // m and the pairwise tree over 256 (zero padded) block terms, in wave 0
-  if (threadIdx.x < 64) {
-    float m = -__builtin_inff();
-    for (int i = 0; i < nb; i++) m = fmaxf(m, ss.mb[i]);
-    float S = 0.0f;
-    if (m > -__builtin_inff()) {
-      float t[4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int i = 4 * lane_id() + j;
-        float v = 0.0f;
-        if (i < nb && ss.mb[i] > -__builtin_inff())
-          v = (tg_u64_to_f32(ss.qb[i]) * 0x1p-40f) * tg_weight(ss.mb[i], m);
-        t[j] = v;
-      }
-      float x = (t[0] + t[1]) + (t[2] + t[3]);
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) x = x + __shfl_xor(x, d, 64);
-      S = x;
-    }
-    if (threadIdx.x == 0) {
-      stat[0] = m;
-      stat[1] = S;
-    }
-  }
-}
-
-// id-order draw over per-element masses wfn(v) (identical in both passes):
-// returns the first id whose inclusive prefix exceeds floor(total * uq / 2^24)
-// (-1 if the total is 0); *total_out gets the total.
-template <typename Tin, class W>
-__device__ __forceinline__ int spec_draw_id_order(int V, uint32_t uq, W wfn, SpecScratch& ss,
-                                                  BlockScratch& s, u64* total_out) {
-  using ST = SpecTile<Tin>;
-  const int nb = (V + SPEC_BLOCK - 1) / SPEC_BLOCK;
-  const int w = threadIdx.x >> 6;
-  for (int blk = w; blk < nb; blk += NW) {
-    u64 q = 0;
-#pragma unroll
-    for (int i = 0; i < ST::NV; i++)
-#pragma unroll
-      for (int e = 0; e < ST::EPV; e++) q += wfn(spec_id<Tin>(blk, i, e));
-    q = wave_sum(q);
-    if (lane_id() == 0) ss.wsum[blk] = q;
-  }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int lane = lane_id();
-    u64 vals[4];
-    u64 ls = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int i = 4 * lane + j;
-      vals[j] = i < nb ? ss.wsum[i] : 0ull;
-      ls += vals[j];
-    }
-    const u64 incl = wave_incl_scan(ls);
-    const u64 total = __shfl(incl, 63, 64);
-    const u64 t = mul_shr24(total, uq);
-    u64 cum = incl - ls;
-    int found = -1;
-    u64 before = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      if (found < 0 && cum + vals[j] > t) {
-        found = 4 * lane + j;
-        before = cum;
-      }
-      cum += vals[j];
-    }
-    const u64 bal = __ballot(found >= 0);
-    const int first = bal ? __ffsll((long long)bal) - 1 : -1;
-    if (lane == 0) {
-      s.sel = -1;
-      s.found = total;
-      s.red64[0] = t;
-    }
-    if (first >= 0 && lane == first) {
-      s.sel = found;
-      s.mass_above = before;
-    }
-  }
-  __syncthreads();
-  const int blk = s.sel;
-  *total_out = s.found;
-  if (blk < 0) return -1;
-  const u64 t = s.red64[0];
-  const u64 before = s.mass_above;
-  if (threadIdx.x < 64) {
-    u64 run = before;
-    int pick = -1;
-    for (int i = 0; i < ST::NV && pick < 0; i++) {
-      u64 ws[ST::EPV];
-      u64 ls = 0;
-#pragma unroll
-      for (int e = 0; e < ST::EPV; e++) {
-        ws[e] = wfn(spec_id<Tin>(blk, i, e));
-        ls += ws[e];
-      }
-      const u64 incl = wave_incl_scan(ls);
-      u64 cum = run + incl - ls;
-      int mine = -1;
-#pragma unroll
-      for (int e = 0; e < ST::EPV; e++) {
-        if (mine < 0 && cum + ws[e] > t) mine = spec_id<Tin>(blk, i, e);
-        cum += ws[e];
-      }
-      const u64 bal = __ballot(mine >= 0);
-      if (bal) {
-        const int first = __ffsll((long long)bal) - 1;
-        pick = __shfl(mine, first, 64);
-      }
-      run += __shfl(incl, 63, 64);
-    }
-    if (lane_id() == 0) s.imin0 = pick;
-  }
-  __syncthreads();
-  return s.imin0;
-}
-
-template <typename Tin>
-__global__ __launch_bounds__(NT) void spec_verify_kernel(SpecArgs a) {
-  __shared__ BlockScratch s;
-  __shared__ SpecScratch ss;
-  const int R = 2 * a.k + 1;
-  const int b = blockIdx.x;
-  if (b >= a.B) return;
-  const float T = a.T[b];
-  const bool greedy = !(T > 0.0f);
-  const float Tc = T > 1e-5f ? T : 1e-5f;
-  const float invT = greedy ? 1.0f : 1.0f / Tc;
-  const int k = a.k;
-  int* out = a.out + (long long)b * (k + 1);
-  const float* stats = a.ws_stats + (long long)b * R * 2;
-  const u64* args = a.ws_arg + (long long)b * R;
-  // validation (same rules as the CPU restatement)
-  bool bad = __builtin_isnan(T) || (!greedy && !(invT > 0.0f && __builtin_isfinite(invT)));
-  for (int j = 0; j < k; j++) {
-    const int d = a.dtok[(long long)b * k + j];
-    if (d < 0 || d >= a.V) bad = true;
-    if (!greedy) {
-      const float ua = a.u_acc[(long long)b * k + j];
-      if (__builtin_isnan(ua) || ua < 0.0f || ua >= 1.0f) bad = true;
-    }
-  }
-  const float ur = a.u_res[b];
-  if (!greedy && (__builtin_isnan(ur) || ur < 0.0f || ur >= 1.0f)) bad = true;
-  if (bad) {
-    for (int j = threadIdx.x; j <= k; j += NT) out[j] = j == 0 ? -2 : -1;
-    if (threadIdx.x == 0) a.n_acc[b] = -1;
-    return;
-  }
-  if (greedy) {
-    if (threadIdx.x == 0) {
-      int j;
-      for (j = 0; j <= k; j++) out[j] = -1;
-      for (j = 0; j < k; j++) {
-        const u64 c = args[j];
-        const int am = c ? comp_id(c) : -1;
-        out[j] = am;
-        if (am != a.dtok[(long long)b * k + j]) break;
-      }
-      if (j == k) out[k] = args[k] ? comp_id(args[k]) : -1;
-      a.n_acc[b] = j;
-    }
-    return;
-  }
-  // stochastic accept/reject scan (thread 0), then the draw (whole block)
-  if (threadIdx.x == 0) {
-    int j;
-    int status = 0;  // 0 all accepted, 1 rejected at j, -1 empty row
-    for (j = 0; j <= k; j++) out[j] = -1;
-    for (j = 0; j < k; j++) {
-      const float mt = stats[2 * j], St = stats[2 * j + 1];
-      const float md = stats[2 * (k + 1 + j)], Sd = stats[2 * (k + 1 + j) + 1];
-      if (!(St > 0.0f) || !(Sd > 0.0f)) {
-        status = -1;
-        break;
-      }
-      const int d = a.dtok[(long long)b * k + j];
-      const Tin* tr = spec_row_ptr<Tin>(a, b, j);
-      const Tin* dr = spec_row_ptr<Tin>(a, b, k + 1 + j);
-      float yt = Elem<Tin>::scalar(tr, d) * invT;
-      float yd = Elem<Tin>::scalar(dr, d) * invT;
-      if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
-      if (!(yd > -__builtin_inff())) yd = -__builtin_inff();
-      const float pt = tg_weight(yt, mt) / St;
-      const float pd = tg_weight(yd, md) / Sd;
-      const float ratio = pt / fmaxf(pd, 1e-10f);
-      if (a.u_acc[(long long)b * k + j] < ratio) {
-        out[j] = d;
-        continue;
-      }
-      status = 1;
-      break;
-    }
-    if (status == 0) {
-      const float St = stats[2 * k + 1];
-      if (!(St > 0.0f)) status = -1;
-    }
-    s.sel = status;
-    s.binc_i = j;
-  }
-  __syncthreads();
-  const int status = s.sel, j = s.binc_i;
-  __syncthreads();
-  if (status < 0) {
-    if (threadIdx.x == 0) {
-      for (int i = 0; i <= k; i++) out[i] = -1;
-      a.n_acc[b] = -1;
-    }
-    return;
-  }
-  const uint32_t uq = (uint32_t)(ur * 16777216.0f);
-  const int V = a.V;
-  int pick;
-  if (status == 1) {
-    const float mt = stats[2 * j], St = stats[2 * j + 1];
-    const float md = stats[2 * (k + 1 + j)], Sd = stats[2 * (k + 1 + j) + 1];
-    const Tin* tr = spec_row_ptr<Tin>(a, b, j);
-    const Tin* dr = spec_row_ptr<Tin>(a, b, k + 1 + j);
-    auto resid = [&](int v) -> u64 {
-      if (v >= V) return 0ull;
-      float yt = Elem<Tin>::scalar(tr, v) * invT;
-      float yd = Elem<Tin>::scalar(dr, v) * invT;
-      if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
-      if (!(yd > -__builtin_inff())) yd = -__builtin_inff();
-      const float pa = tg_weight(yt, mt) / St;
-      const float pb = tg_weight(yd, md) / Sd;
-      return tg_q40(fmaxf(pa - pb, 0.0f));
-    };
-    u64 Rm;
-    pick = spec_draw_id_order<Tin>(V, uq, resid, ss, s, &Rm);
-    if (Rm < 110ull) {  // residual mass <= 1e-10: draw from the target row
-      auto wt = [&](int v) -> u64 {
-        if (v >= V) return 0ull;
-        float yt = Elem<Tin>::scalar(tr, v) * invT;
-        if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
-        return tg_q40(tg_weight(yt, mt));
-      };
-      __syncthreads();
-      u64 Sq;
-      pick = spec_draw_id_order<Tin>(V, uq, wt, ss, s, &Sq);
-    }
-  } else {
-    const float mt = stats[2 * k];
-    const Tin* tr = spec_row_ptr<Tin>(a, b, k);
-    auto wt = [&](int v) -> u64 {
-      if (v >= V) return 0ull;
-      float yt = Elem<Tin>::scalar(tr, v) * invT;
-      if (!(yt > -__builtin_inff())) yt = -__builtin_inff();
-      return tg_q40(tg_weight(yt, mt));
-    };
-    u64 Sq;
-    pick = spec_draw_id_order<Tin>(V, uq, wt, ss, s, &Sq);
-  }
-  if (threadIdx.x == 0) {
-    out[j] = pick;
-    a.n_acc[b] = j;
-  }
-}
-
 // ------------------------------------------------------------------ launchers
 
 hipError_t launch_sample(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
@@ -1084,17 +719,6 @@ hipError_t set_sample_lds_limit(size_t bytes) {
     if (e2 != hipSuccess) e = e2;
   }
   return e;
-}
-
-hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st) {
-  const int grid = a.B * (2 * a.k + 1);
-  if (dtype == 1) hipLaunchKernelGGL(spec_stats_kernel<uint16_t>, dim3(grid), dim3(NT), 0, st, a);
-  else hipLaunchKernelGGL(spec_stats_kernel<float>, dim3(grid), dim3(NT), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (dtype == 1) hipLaunchKernelGGL(spec_verify_kernel<uint16_t>, dim3(a.B), dim3(NT), 0, st, a);
-  else hipLaunchKernelGGL(spec_verify_kernel<float>, dim3(a.B), dim3(NT), 0, st, a);
-  return hipGetLastError();
 }
 
 }  // namespace tgs
