@@ -230,6 +230,9 @@ inline uint32_t __builtin_amdgcn_mbcnt_hi(uint32_t mask, uint32_t acc) {
 }
 template <typename T>
 inline T __builtin_amdgcn_readlane(T x, int l) { return hipcpu::exchange(x, l); }
+// The kernels call it with every lane of the wave active: lane 0 is the first.
+template <typename T>
+inline T __builtin_amdgcn_readfirstlane(T x) { return hipcpu::exchange(x, 0); }
 // A wave-wide barrier stands in for the code-motion barrier; the fences order
 // nothing further on the host.
 inline void __builtin_amdgcn_wave_barrier() { hipcpu::wave().bar->arrive_and_wait(); }

@@ -1,0 +1,93 @@
+// numerics.cpp -- checks, on the CPU, that the device arithmetic shortcuts of
+// tgs_device.h equal the canonical operations they replace, over the input
+// ranges the kernels feed them.  The header is compiled unchanged (host
+// shim).  TEST INFRASTRUCTURE ONLY.
+//   numerics div N seed   tg_div_rcp(a, b, 1/b) == a / b, a in [0, 1], b in [1, 2^18]
+//   numerics exp N seed   tg_expf_nonpos(x) == tg_expf(x), x <= 0, -inf, NaN
+//   numerics q40 N seed   (u64)tg_q40d(e) == tg_q40(e), e in [0, 1]
+// Prints the number of mismatches (and the first few).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <string>
+
+#include "tgs_device.h"
+
+using namespace tgs;
+
+static float bits(uint32_t u) {
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+static uint32_t ubits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  return u;
+}
+
+int main(int argc, char** argv) {
+  if (argc < 4) return 2;
+  const std::string mode = argv[1];
+  const long long N = std::atoll(argv[2]);
+  std::mt19937_64 g(std::strtoull(argv[3], nullptr, 10));
+  long long bad = 0;
+  auto report = [&](const char* what, float x, float y, double r0, double r1) {
+    if (++bad <= 5) std::printf("mismatch %s %a %a: %a vs %a\n", what, x, y, r0, r1);
+  };
+  if (mode == "div") {
+    // weights a: every exponent from 2^-48 to 1 (and 0, 1); denominators b in [1, 2^18]
+    for (long long i = 0; i < N; i++) {
+      const uint64_t r = g();
+      float a, b;
+      const int ea = (int)(r % 49), eb = (int)((r >> 8) % 19);
+      const uint32_t ma = (uint32_t)(r >> 16) & 0x7FFFFFu, mb = (uint32_t)(r >> 40) & 0x7FFFFFu;
+      a = bits(((uint32_t)(127 - ea) << 23) | ma);
+      if (a > 1.0f) a = 1.0f;
+      b = bits(((uint32_t)(127 + eb) << 23) | mb);
+      switch (i & 15) {
+        case 0: a = 0.0f; break;
+        case 1: a = 1.0f; break;
+        case 2: b = bits(((uint32_t)(127 + eb) << 23) | 0x7FFFFFu); break;
+        case 3: a = bits(((uint32_t)(127 - ea) << 23) | 0x7FFFFFu); if (a > 1.0f) a = 1.0f; break;
+        case 4: b = bits((uint32_t)(127 + eb) << 23); break;
+        case 5: a = tg_expf(-(float)(r % 32000) * 0.001f); break;
+        default: break;
+      }
+      const float rb = 1.0f / b;
+      const float q1 = tg_div_rcp(a, b, rb), q0 = a / b;
+      if (ubits(q1) != ubits(q0)) report("div", a, b, q1, q0);
+    }
+  } else if (mode == "exp") {
+    for (long long i = 0; i < N; i++) {
+      const uint64_t r = g();
+      float x;
+      if ((i & 3) == 0) x = -bits((uint32_t)r & 0x7FFFFFFFu);               // any non-positive bit pattern
+      else x = -(float)((double)(r >> 11) * 0x1p-53 * 40.0);                 // uniform in [-40, 0]
+      if (i == 0) x = -__builtin_inff();
+      if (i == 1) x = bits(0x7FC00000u);
+      if (i == 2) x = -0.0f;
+      if (i == 3) x = 0.0f;
+      if (i == 4) x = -32.0f;
+      const float e1 = tg_expf_nonpos(x), e0 = tg_expf(x);
+      if (ubits(e1) != ubits(e0)) report("exp", x, 0, e1, e0);
+    }
+  } else if (mode == "q40") {
+    for (long long i = 0; i < N; i++) {
+      const uint64_t r = g();
+      float e = (i & 1) ? tg_expf(-(float)((double)(r >> 11) * 0x1p-53 * 33.0))
+                        : bits(((uint32_t)(127 - (int)(r % 60)) << 23) | ((uint32_t)(r >> 20) & 0x7FFFFFu));
+      if (e > 1.0f) e = 1.0f;
+      if (i == 0) e = 0.0f;
+      if (i == 1) e = 1.0f;
+      const u64 q1 = (u64)tg_q40d(e), q0 = tg_q40(e);
+      if (q1 != q0) report("q40", e, 0, (double)q1, (double)q0);
+    }
+  } else {
+    return 2;
+  }
+  std::printf("%s %lld checked, %lld mismatches\n", mode.c_str(), N, bad);
+  return bad ? 1 : 0;
+}

@@ -196,3 +196,16 @@ def test_spec_invalid_rows(sim, oracle):
     c["T"][1] = np.nan
     c["u_acc"][2, 0] = 1.0
     _spec_check(sim, oracle, c)
+
+
+@pytest.mark.parametrize("mode,n", [("div", 20_000_000), ("exp", 20_000_000), ("q40", 10_000_000)])
+def test_device_shortcuts_equal_canonical_ops(sim, mode, n):
+    """tg_div_rcp == IEEE a / b (weights over softmax denominators),
+    tg_expf_nonpos == tg_expf on x <= 0 / -inf / NaN, and f64-summed
+    tg_q40d == tg_q40, on the device header compiled for the host."""
+    import subprocess
+
+    r = subprocess.run([os.path.join(HERE, "cpu_sim", "build", "numerics"), mode, str(n), "12345"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert " 0 mismatches" in r.stdout

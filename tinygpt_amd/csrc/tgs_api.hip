@@ -371,7 +371,7 @@ int tgs_reserve_spec(tgs_handle h, int max_batch, int max_k) {
   const int nbs = (h->max_vocab + tgs::SPEC_BLOCK - 1) / tgs::SPEC_BLOCK;
   hipError_t e = hipMalloc(&h->spec_blk_m, sizeof(float) * rows * nbs);
   if (e == hipSuccess) e = hipMalloc(&h->spec_blk_q, sizeof(unsigned long long) * rows * nbs);
-  if (e == hipSuccess) e = hipMalloc(&h->spec_blk_w, sizeof(unsigned long long) * (size_t)nb * nbs);
+  if (e == hipSuccess) e = hipMalloc(&h->spec_blk_w, sizeof(unsigned long long) * (size_t)nb * nbs * tgs::SPEC_GROUPS);
   if (e == hipSuccess) e = hipMalloc(&h->spec_state, (size_t)32 * nb);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
@@ -422,6 +422,7 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
   a.blk_q = h->spec_blk_q;
   a.blk_w = h->spec_blk_w;
   a.seq_state = h->spec_state;
+  a.ncu = h->num_cu;
   hipError_t e = tgs::launch_spec(a, dt, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(h, e, "spec kernel launch");
   return TGS_OK;

@@ -60,6 +60,49 @@ __device__ __forceinline__ float tg_expf(float x) {
   return p * tg_u2f((uint32_t)(ni + 127) << 23);
 }
 
+// tg_expf(x) for x <= 0, -inf or NaN (the range of y - m with m the maximum
+// of the y's): the same value bit for bit.  The overflow test cannot fire,
+// and 2^n (n >= -47 once x >= -32) scales p exactly through ldexp.
+// Branch free: the polynomial runs on max(x, -32) (x itself wherever the
+// result is used) and x < -32, -inf and NaN select 0 at the end.
+__device__ __forceinline__ float tg_expf_nonpos(float x_in) {
+  const float x = fmaxf(x_in, -32.0f);
+  const float log2e = 0x1.715476p+0f;
+  const float ln2_hi = 0x1.62ep-1f;
+  const float ln2_lo = 0x1.0bfbe8p-15f;
+  const float shifter = 12582912.0f;
+  float t = x * log2e;
+  float n = (t + shifter) - shifter;
+  float r = __builtin_fmaf(n, -ln2_hi, x);
+  r = __builtin_fmaf(n, -ln2_lo, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const float e = __builtin_ldexpf(p, (int)n);
+  return (x_in >= -32.0f) ? e : 0.0f;
+}
+
+// floor(e * 2^40) of a weight e in [0, 1] as an integer-valued double: the
+// per-lane sums of a few dozen such terms stay exact (below 2^53) and
+// convert to the same u64 as summing tg_q40 terms.
+__device__ __forceinline__ double tg_q40d(float e) { return (double)__builtin_floorf(e * 0x1p40f); }
+
+// a / b correctly rounded from rb = RN(1 / b): q = RN(a * rb) is within one
+// ulp of a / b, the residual a - b q is exact through a fused multiply-add,
+// and one correction q + (a - b q) rb rounds to RN(a / b) (Markstein's
+// theorem; a, b and a / b normal or a == 0).  Used for weights a in [0, 1]
+// over softmax denominators b >= 1.
+__device__ __forceinline__ float tg_div_rcp(float a, float b, float rb) {
+  const float q = a * rb;
+  const float r = __builtin_fmaf(-q, b, a);
+  return __builtin_fmaf(r, rb, q);
+}
+
 __device__ __forceinline__ float tg_weight(float y, float m) {
   return (y == m) ? 1.0f : tg_expf(y - m);
 }
@@ -103,6 +146,13 @@ __device__ __forceinline__ u64 mul_shr24(u64 a, uint32_t b) {
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Butterfly wave reductions (defined with the lane permutes below).
+template <typename T>
+__device__ __forceinline__ T wave_sum(T x);
+template <typename T>
+__device__ __forceinline__ T wave_max(T x);
+__device__ __forceinline__ float wave_maxf(float x);
+
 template <typename T>
 __device__ __forceinline__ T wave_incl_scan(T x) {
   const int lane = lane_id();
@@ -111,29 +161,6 @@ __device__ __forceinline__ T wave_incl_scan(T x) {
     T y = __shfl_up(x, d, 64);
     if (lane >= d) x += y;
   }
-  return x;
-}
-
-template <typename T>
-__device__ __forceinline__ T wave_sum(T x) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
-  return x;
-}
-
-template <typename T>
-__device__ __forceinline__ T wave_max(T x) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    T y = __shfl_xor(x, d, 64);
-    x = y > x ? y : x;
-  }
-  return x;
-}
-
-__device__ __forceinline__ float wave_maxf(float x) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x = fmaxf(x, __shfl_xor(x, d, 64));
   return x;
 }
 
@@ -445,6 +472,41 @@ __device__ __forceinline__ T xor_lane_s(T x, int s) {
     case 16: return xor_lane<16>(x);
     default: return xor_lane<32>(x);
   }
+}
+
+// Butterfly reductions over the wave with the lane moves above (every lane
+// gets the result).  Exact for maxima and integer sums.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T x) {
+  x += xor_lane<32>(x);
+  x += xor_lane<16>(x);
+  x += xor_lane<8>(x);
+  x += xor_lane<4>(x);
+  x += xor_lane<2>(x);
+  x += xor_lane<1>(x);
+  return x;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max(T x) {
+  T y;
+  y = xor_lane<32>(x); x = y > x ? y : x;
+  y = xor_lane<16>(x); x = y > x ? y : x;
+  y = xor_lane<8>(x); x = y > x ? y : x;
+  y = xor_lane<4>(x); x = y > x ? y : x;
+  y = xor_lane<2>(x); x = y > x ? y : x;
+  y = xor_lane<1>(x); x = y > x ? y : x;
+  return x;
+}
+
+__device__ __forceinline__ float wave_maxf(float x) {
+  x = fmaxf(x, tg_u2f(xor_lane32<32>(tg_f2u(x))));
+  x = fmaxf(x, tg_u2f(xor_lane32<16>(tg_f2u(x))));
+  x = fmaxf(x, tg_u2f(xor_lane32<8>(tg_f2u(x))));
+  x = fmaxf(x, tg_u2f(xor_lane32<4>(tg_f2u(x))));
+  x = fmaxf(x, tg_u2f(xor_lane32<2>(tg_f2u(x))));
+  x = fmaxf(x, tg_u2f(xor_lane32<1>(tg_f2u(x))));
+  return x;
 }
 
 // Number of set bits of a wave mask below this lane.

@@ -64,11 +64,13 @@ struct SpecArgs {
   int nbs;                     // block stride of the per-row workspace arrays (>= nb)
   float* blk_m;                // [B][2k+1][nbs] block maxima
   unsigned long long* blk_q;   // [B][2k+1][nbs] exact block masses (greedy: block argmax composite)
-  unsigned long long* blk_w;   // [B][nbs] draw mass per block of the row drawn from
+  unsigned long long* blk_w;   // [B][nbs][SPEC_GROUPS] draw mass per vector group of each block of the row drawn from
   void* seq_state;             // [B] 32-byte per-sequence decision
+  int ncu;                     // compute units of the device (grid sizing)
 };
 
 constexpr int SPEC_MAX_K = 64;  // most draft tokens per sequence
+constexpr int SPEC_GROUPS = 4;  // 16-byte vector groups per block of 1024 ids (fp32: 4, bf16: 2)
 
 // Launches the chunk kernel, the merge kernel when rows are split (a.S > 1)
 // and the full-path kernel when a.full_rows is set, in that order on st.

@@ -32,6 +32,8 @@
 // another workgroup.  Semantics follow SpeculativeDecode.stepStochastic /
 // .step (native-mac/Sources/TinyGPT/SpeculativeDecode.swift:121-210, :41-98)
 // with the contract's strict u < pT/pD accept rule and id-order draws.
+#include <algorithm>
+
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 #include "tgs_row.h"
@@ -40,6 +42,7 @@ namespace tgs {
 namespace spec {
 
 constexpr int WPB = NT / 64;  // waves per workgroup
+constexpr int K1_WG_PER_CU = 8;  // resident workgroups per CU of the block kernel's grid
 
 template <typename Tin>
 struct Tile {
@@ -91,25 +94,56 @@ __device__ __forceinline__ SeqT seq_temp(float T) {
 
 // ------------------------------------------------------------------ K1
 
-template <typename Tin>
-__global__ __launch_bounds__(NT) void spec_block_kernel(SpecArgs a) {
-  using TL = Tile<Tin>;
-  const int R = 2 * a.k + 1;
-  const long long nwork = (long long)a.B * R * a.nb;
-  const long long f = (long long)blockIdx.x * WPB + (threadIdx.x >> 6);
-  if (f >= nwork) return;
-  const int blk = (int)(f % a.nb);
-  const int br = (int)(f / a.nb);
-  const int b = br / R, r = br % R;
-  const float T = a.T[b];
-  if (__builtin_isnan(T)) return;
+// Block (b, r, blk) of the flat index, with the sequence's temperature;
+// live: computed (NaN T is reported by the decide kernel, greedy sequences
+// skip their draft rows).  A wave walks consecutive blocks and updates the
+// cursor incrementally (wave-uniform scalar arithmetic; the temperature is
+// re-read only when the sequence changes).
+struct BlockRef {
+  int b, r, blk;
+  bool live, greedy;
+  float invT;
+};
+__device__ __forceinline__ void block_ref_temp(const SpecArgs& a, BlockRef& x) {
+  const float T = a.T[x.b];
   const SeqT st = seq_temp(T);
-  if (st.greedy && r > a.k) return;  // draft rows unused by greedy verification
-  const Tin* rowp = row_ptr<Tin>(a, b, r);
-  uint4 raw[TL::NV];
-  load_block<Tin>(rowp, blk, a.V, a.aligned, raw);
-  const long long o = (long long)br * a.nbs + blk;
-  if (st.greedy) {
+  x.greedy = st.greedy;
+  x.invT = st.invT;
+}
+__device__ __forceinline__ bool block_live(const SpecArgs& a, const BlockRef& x) {
+  return !__builtin_isnan(a.T[x.b]) && !(x.greedy && x.r > a.k);
+}
+__device__ __forceinline__ BlockRef block_ref(const SpecArgs& a, int f) {
+  const int R = 2 * a.k + 1;
+  BlockRef x;
+  x.blk = f % a.nb;
+  const int br = f / a.nb;
+  x.b = br / R;
+  x.r = br % R;
+  block_ref_temp(a, x);
+  x.live = block_live(a, x);
+  return x;
+}
+__device__ __forceinline__ BlockRef block_next(const SpecArgs& a, const BlockRef& x) {
+  BlockRef y = x;
+  if (++y.blk == a.nb) {
+    y.blk = 0;
+    if (++y.r == 2 * a.k + 1) {
+      y.r = 0;
+      y.b++;
+      block_ref_temp(a, y);
+    }
+  }
+  y.live = block_live(a, y);
+  return y;
+}
+
+// One block's statistics from its loaded vectors; lane 0 stores them.
+template <typename Tin>
+__device__ __forceinline__ void block_stats(const SpecArgs& a, const BlockRef& x, const uint4 (&raw)[Tile<Tin>::NV]) {
+  using TL = Tile<Tin>;
+  const long long o = ((long long)x.b * (2 * a.k + 1) + x.r) * a.nbs + x.blk;
+  if (x.greedy) {
     u64 arg = 0;
 #pragma unroll
     for (int i = 0; i < TL::NV; i++)
@@ -117,7 +151,7 @@ __global__ __launch_bounds__(NT) void spec_block_kernel(SpecArgs a) {
       for (int e = 0; e < TL::EPV; e++) {
         const float y = scaled(Elem<Tin>::get(raw[i], e), 1.0f);
         if (y > -__builtin_inff()) {
-          const u64 c = comp_key(tg_key(y), blk_id<Tin>(blk, i, e));
+          const u64 c = comp_key(tg_key(y), blk_id<Tin>(x.blk, i, e));
           arg = c > arg ? c : arg;
         }
       }
@@ -125,26 +159,70 @@ __global__ __launch_bounds__(NT) void spec_block_kernel(SpecArgs a) {
     if (lane_id() == 0) a.blk_q[o] = arg;
     return;
   }
+  // y = z / T; NaN and -inf never raise the maximum and weigh 0 (y - m is
+  // NaN or -inf there), so they need no mapping
   float y[TL::EPL];
   float mx = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < TL::NV; i++)
 #pragma unroll
     for (int e = 0; e < TL::EPV; e++) {
-      y[i * TL::EPV + e] = scaled(Elem<Tin>::get(raw[i], e), st.invT);
+      y[i * TL::EPV + e] = Elem<Tin>::get(raw[i], e) * x.invT;
       mx = fmaxf(mx, y[i * TL::EPV + e]);
     }
   mx = wave_maxf(mx);
   u64 q = 0;
-  if (mx > -__builtin_inff()) {
+  if (mx > -__builtin_inff() && mx < __builtin_inff()) {
+    // y - m <= 0 (y == m gives +-0 and weight 1): the non-positive exp, and
+    // exact masses summed per lane in f64
+    double qd = 0.0;
 #pragma unroll
-    for (int j = 0; j < TL::EPL; j++)
-      if (y[j] > -__builtin_inff()) q += tg_q40(tg_weight(y[j], mx));
+    for (int j = 0; j < TL::EPL; j++) qd += tg_q40d(tg_expf_nonpos(y[j] - mx));
+    q = (u64)qd;
+  } else if (mx > -__builtin_inff()) {
+    // a +inf logit in the block (weight(inf, inf) = 1, everything else 0)
+#pragma unroll
+    for (int j = 0; j < TL::EPL; j++) {
+      const float yy = (y[j] > -__builtin_inff()) ? y[j] : -__builtin_inff();
+      if (yy > -__builtin_inff()) q += tg_q40(tg_weight(yy, mx));
+    }
   }
   q = wave_sum(q);
   if (lane_id() == 0) {
     a.blk_m[o] = mx;
     a.blk_q[o] = q;
+  }
+}
+
+// K1: every wave takes a run of consecutive blocks (about eight at C5's
+// size), the loads of its next block issued before the current block is
+// reduced.
+template <typename Tin>
+__global__ __launch_bounds__(NT) void spec_block_kernel(SpecArgs a) {
+  using TL = Tile<Tin>;
+  const int nwork = a.B * (2 * a.k + 1) * a.nb;
+  const int nwaves = (int)gridDim.x * WPB;
+  const int gw = __builtin_amdgcn_readfirstlane((int)blockIdx.x * WPB + (int)(threadIdx.x >> 6));
+  const int per = (nwork + nwaves - 1) / nwaves;
+  const int f0 = gw * per;
+  const int n = min(per, nwork - f0);
+  if (n <= 0) return;
+  BlockRef x = block_ref(a, f0);
+  uint4 cur[TL::NV];
+  if (x.live) load_block<Tin>(row_ptr<Tin>(a, x.b, x.r), x.blk, a.V, a.aligned, cur);
+  for (int i = 0; i < n; i++) {
+    const bool more = i + 1 < n;
+    BlockRef xn = x;
+    uint4 nxt[TL::NV];
+    if (more) {
+      xn = block_next(a, x);
+      if (xn.live) load_block<Tin>(row_ptr<Tin>(a, xn.b, xn.r), xn.blk, a.V, a.aligned, nxt);
+    }
+    if (x.live) block_stats<Tin>(a, x, cur);
+    if (!more) break;
+#pragma unroll
+    for (int v = 0; v < TL::NV; v++) cur[v] = nxt[v];
+    x = xn;
   }
 }
 
@@ -158,6 +236,7 @@ struct alignas(16) SeqState {
   float mt, St, md, Sd;
 };
 static_assert(sizeof(SeqState) == 32, "state layout");
+static_assert(Tile<float>::NV <= SPEC_GROUPS && Tile<uint16_t>::NV <= SPEC_GROUPS, "group sums per block");
 
 // Row statistics (m, S) of row r of sequence b from its block terms, by one
 // wave: m = max m_b; S = pairwise tree over term_b = (f32(Q_b) 2^-40)
@@ -190,8 +269,11 @@ __device__ __forceinline__ void row_stats(const SpecArgs& a, long long br, float
   *S_out = S;
 }
 
+constexpr int DT = 1024;        // decide kernel: threads per workgroup
+constexpr int DW = DT / 64;    // its waves
+
 template <typename Tin>
-__global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
+__global__ __launch_bounds__(DT) void spec_decide_kernel(SpecArgs a) {
   __shared__ float sm[2 * SPEC_MAX_K + 1], sS[2 * SPEC_MAX_K + 1];
   __shared__ u64 sarg[SPEC_MAX_K + 1];
   __shared__ unsigned sbad;
@@ -203,38 +285,35 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
   const SeqT st = seq_temp(T);
   int* out = a.out + (long long)b * (k + 1);
   SeqState* state = (SeqState*)a.seq_state + b;
+  // wave 0, lane j < k: draft token j, its uniform and its two logits (the
+  // id clamped into the row for the load; an invalid id fails validation)
+  int d = 0;
+  float ua = 0.0f, zt = 0.0f, zd = 0.0f;
+  if (w == 0 && lane < k) {
+    d = a.dtok[(long long)b * k + lane];
+    ua = a.u_acc[(long long)b * k + lane];
+    const int dc = d < 0 ? 0 : (d >= a.V ? a.V - 1 : d);
+    zt = Elem<Tin>::scalar(row_ptr<Tin>(a, b, lane), dc);
+    zd = Elem<Tin>::scalar(row_ptr<Tin>(a, b, k + 1 + lane), dc);
+  }
   // validation (the CPU restatement's rules): T, draft ids, uniforms
-  if (threadIdx.x == 0) sbad = 0u;
-  __syncthreads();
-  {
+  if (w == 0) {
     bool bad = __builtin_isnan(T) || (!st.greedy && !(st.invT > 0.0f && __builtin_isfinite(st.invT)));
-    for (int j = threadIdx.x; j < k; j += NT) {
-      const int d = a.dtok[(long long)b * k + j];
+    if (lane < k) {
       if (d < 0 || d >= a.V) bad = true;
-      if (!st.greedy) {
-        const float ua = a.u_acc[(long long)b * k + j];
-        if (__builtin_isnan(ua) || ua < 0.0f || ua >= 1.0f) bad = true;
-      }
+      if (!st.greedy && (__builtin_isnan(ua) || ua < 0.0f || ua >= 1.0f)) bad = true;
     }
-    if (threadIdx.x == 0 && !st.greedy) {
+    if (lane == 0 && !st.greedy) {
       const float ur = a.u_res[b];
       if (__builtin_isnan(ur) || ur < 0.0f || ur >= 1.0f) bad = true;
     }
-    if (bad) atomicOr(&sbad, 1u);
+    const u64 bb = __ballot(bad);
+    if (lane == 0) sbad = bb ? 1u : 0u;
   }
-  __syncthreads();
-  if (sbad) {
-    for (int j = threadIdx.x; j <= k; j += NT) out[j] = j == 0 ? -2 : -1;
-    if (threadIdx.x == 0) {
-      a.n_acc[b] = -1;
-      state->status = 2;
-    }
-    return;
-  }
+  // row statistics (stochastic) or argmax (greedy), one row per wave
   const long long br0 = (long long)b * R;
   if (st.greedy) {
-    // argmax of target rows 0..k: the largest block composite
-    for (int r = w; r <= k; r += WPB) {
+    for (int r = w; r <= k; r += DW) {
       u64 x = 0;
       for (int i = lane; i < a.nb; i += 64) {
         const u64 c = a.blk_q[(br0 + r) * a.nbs + i];
@@ -243,42 +322,43 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
       x = wave_max(x);
       if (lane == 0) sarg[r] = x;
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int j;
-      for (j = 0; j <= k; j++) out[j] = -1;
-      for (j = 0; j < k; j++) {
-        const u64 c = sarg[j];
-        const int am = c ? comp_id(c) : -1;
-        out[j] = am;
-        if (am != a.dtok[(long long)b * k + j]) break;
+  } else if (!__builtin_isnan(T)) {
+    for (int r = w; r < R; r += DW) {
+      float m, S;
+      row_stats(a, br0 + r, &m, &S);
+      if (lane == 0) {
+        sm[r] = m;
+        sS[r] = S;
       }
-      if (j == k) out[k] = sarg[k] ? comp_id(sarg[k]) : -1;
+    }
+  }
+  __syncthreads();
+  if (w != 0) return;
+  if (sbad) {
+    for (int i = lane; i <= k; i += 64) out[i] = i == 0 ? -2 : -1;
+    if (lane == 0) {
+      a.n_acc[b] = -1;
+      state->status = 2;
+    }
+    return;
+  }
+  if (st.greedy) {
+    // accept while the target argmax equals the draft token (lane j: position j)
+    const int am = lane < k ? (sarg[lane] ? comp_id(sarg[lane]) : -1) : -1;
+    const u64 miss = __ballot(lane < k && am != d);
+    const int j = miss ? __ffsll((long long)miss) - 1 : k;  // first mismatch, or k
+    // accepted tokens, then the correction (or the bonus argmax at k)
+    for (int i = lane; i <= k; i += 64) out[i] = i <= j ? (sarg[i] ? comp_id(sarg[i]) : -1) : -1;
+    if (lane == 0) {
       a.n_acc[b] = j;
       state->status = 2;
     }
     return;
   }
-  for (int r = w; r < R; r += WPB) {
-    float m, S;
-    row_stats(a, br0 + r, &m, &S);
-    if (lane == 0) {
-      sm[r] = m;
-      sS[r] = S;
-    }
-  }
-  __syncthreads();
-  if (w != 0) return;
   // every draft position at once (lane j), then the first rejection
   bool acc = true, empty = false;
-  float yt = 0.0f, yd = 0.0f;
-  int d = 0;
   if (lane < k) {
-    d = a.dtok[(long long)b * k + lane];
-    yt = scaled(Elem<Tin>::scalar(row_ptr<Tin>(a, b, lane), d), st.invT);
-    yd = scaled(Elem<Tin>::scalar(row_ptr<Tin>(a, b, k + 1 + lane), d), st.invT);
-  }
-  if (lane < k) {
+    const float yt = scaled(zt, st.invT), yd = scaled(zd, st.invT);
     const float mt = sm[lane], St = sS[lane];
     const float md = sm[k + 1 + lane], Sd = sS[k + 1 + lane];
     if (!(St > 0.0f) || !(Sd > 0.0f)) {
@@ -288,25 +368,26 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
       const float pt = tg_weight(yt, mt) / St;
       const float pd = tg_weight(yd, md) / Sd;
       const float ratio = pt / fmaxf(pd, 1e-10f);
-      acc = a.u_acc[(long long)b * k + lane] < ratio;
+      acc = ua < ratio;
     }
   }
   const u64 stop = __ballot(lane < k && !acc);
   const int j = stop ? __ffsll((long long)stop) - 1 : k;
-  const bool empty_j = __shfl(empty ? 1 : 0, j < k ? j : 0, 64) != 0 && j < k;
-  // i < j <= k <= 64 only for i == lane (this lane's draft token d)
-  for (int i = lane; i <= k; i += 64) out[i] = (i < j) ? d : -1;
+  const bool empty_j = j < k && __shfl(empty ? 1 : 0, j < k ? j : 0, 64) != 0;
+  const bool none = empty_j || (j == k && !(sS[k] > 0.0f));
+  // i < j <= k <= 64 only for i == lane (this lane's draft token d); an empty
+  // row at the stop makes every output -1 (the rows after the stop are never
+  // examined, as in the serial scan)
+  for (int i = lane; i <= k; i += 64) out[i] = (!none && i < j) ? d : -1;
   if (lane == 0) {
     SeqState s;
     s.pad0 = s.pad1 = 0;
     s.j = j;
-    if (empty_j || (j == k && !(sS[k] > 0.0f))) {
+    if (none) {
       s.status = 2;
       a.n_acc[b] = -1;
-    } else if (j < k) {
-      s.status = 1;
     } else {
-      s.status = 0;
+      s.status = j < k ? 1 : 0;
     }
     s.mt = sm[j];
     s.St = sS[j];
@@ -314,29 +395,37 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
     s.Sd = j < k ? sS[k + 1 + j] : 0.0f;
     *state = s;
   }
-  // an empty row at the stop: every output -1 (the rows after the stop are
-  // never examined, as in the serial scan)
-  if (empty_j || (j == k && !(sS[k] > 0.0f)))
-    for (int i = lane; i <= k; i += 64) out[i] = -1;
 }
 
 // ------------------------------------------------------------------ K3 / K4
 
-// Mass of id v of the draw row (0 past V): residual or target weight.
+// Mass of one id of the draw row: the residual q40(max(pT - pD, 0)) or the
+// target weight q40(weight(yt, mt)), both as exact integer-valued doubles.
+// With finite row maxima (the common case) the weights use the non-positive
+// exp and the divisions by the softmax denominators (>= 1) the reciprocal
+// with one correction; both equal the canonical operations bit for bit.
 template <typename Tin>
 struct DrawRow {
   const Tin* tr;
   const Tin* dr;
-  float invT, mt, St, md, Sd;
+  float invT, mt, St, md, Sd, rSt, rSd;
   int V;
-  bool resid;
-  __device__ __forceinline__ u64 mass(float zt, float zd) const {
+  bool resid, fast;
+  __device__ __forceinline__ double mass(float zt, float zd) const {
+    if (fast) {
+      const float wt = tg_expf_nonpos(zt * invT - mt);
+      if (!resid) return tg_q40d(wt);
+      const float wd = tg_expf_nonpos(zd * invT - md);
+      const float pa = tg_div_rcp(wt, St, rSt);
+      const float pb = tg_div_rcp(wd, Sd, rSd);
+      return tg_q40d(fmaxf(pa - pb, 0.0f));
+    }
     const float yt = scaled(zt, invT);
-    if (!resid) return tg_q40(tg_weight(yt, mt));
+    if (!resid) return tg_q40d(tg_weight(yt, mt));
     const float yd = scaled(zd, invT);
     const float pa = tg_weight(yt, mt) / St;
     const float pb = tg_weight(yd, md) / Sd;
-    return tg_q40(fmaxf(pa - pb, 0.0f));
+    return tg_q40d(fmaxf(pa - pb, 0.0f));
   }
 };
 
@@ -350,29 +439,26 @@ __device__ __forceinline__ DrawRow<Tin> draw_row(const SpecArgs& a, int b, const
   d.St = s.St;
   d.md = s.md;
   d.Sd = s.Sd;
+  d.rSt = 1.0f / s.St;
+  d.rSd = resid ? 1.0f / s.Sd : 1.0f;
+  d.fast = s.mt < __builtin_inff() && (!resid || s.md < __builtin_inff());
   d.tr = row_ptr<Tin>(a, b, s.status == 0 ? a.k : s.j);
   d.dr = resid ? row_ptr<Tin>(a, b, a.k + 1 + s.j) : d.tr;
   return d;
 }
 
-// Masses of this lane's elements of block blk; ws[i * EPV + e].
+// Masses of this lane's EPV ids of vector group i of block blk (ids past V
+// were loaded as NaN: mass 0).
 template <typename Tin>
-__device__ __forceinline__ void block_masses(const SpecArgs& a, const DrawRow<Tin>& dw, int blk,
-                                             u64 (&ws)[Tile<Tin>::EPL]) {
-  using TL = Tile<Tin>;
-  uint4 rt[TL::NV], rd[TL::NV];
-  load_block<Tin>(dw.tr, blk, dw.V, a.aligned, rt);
-  if (dw.resid) load_block<Tin>(dw.dr, blk, dw.V, a.aligned, rd);
+__device__ __forceinline__ void group_masses(const DrawRow<Tin>& dw, const uint4& rt, const uint4& rd,
+                                             double (&ws)[Elem<Tin>::EPV]) {
 #pragma unroll
-  for (int i = 0; i < TL::NV; i++)
-#pragma unroll
-    for (int e = 0; e < TL::EPV; e++) {
-      const float zt = Elem<Tin>::get(rt[i], e);
-      const float zd = dw.resid ? Elem<Tin>::get(rd[i], e) : 0.0f;
-      ws[i * TL::EPV + e] = dw.mass(zt, zd);  // ids past V were loaded as NaN: mass 0
-    }
+  for (int e = 0; e < Elem<Tin>::EPV; e++)
+    ws[e] = dw.mass(Elem<Tin>::get(rt, e), dw.resid ? Elem<Tin>::get(rd, e) : 0.0f);
 }
 
+// K3: per (sequence, block) the draw mass of each vector group of the block
+// (group i: ids blk*SPEC_BLOCK + i*64*EPV + [0, 64*EPV)).
 template <typename Tin>
 __global__ __launch_bounds__(NT) void spec_mass_kernel(SpecArgs a) {
   using TL = Tile<Tin>;
@@ -382,13 +468,20 @@ __global__ __launch_bounds__(NT) void spec_mass_kernel(SpecArgs a) {
   const SeqState s = ((const SeqState*)a.seq_state)[b];
   if (s.status > 1) return;
   const DrawRow<Tin> dw = draw_row<Tin>(a, b, s, s.status == 1);
-  u64 ws[TL::EPL];
-  block_masses<Tin>(a, dw, blk, ws);
-  u64 q = 0;
+  uint4 rt[TL::NV], rd[TL::NV];
+  load_block<Tin>(dw.tr, blk, dw.V, a.aligned, rt);
+  if (dw.resid) load_block<Tin>(dw.dr, blk, dw.V, a.aligned, rd);
+  u64* gw = a.blk_w + ((long long)b * a.nbs + blk) * SPEC_GROUPS;
 #pragma unroll
-  for (int j = 0; j < TL::EPL; j++) q += ws[j];
-  q = wave_sum(q);
-  if (lane_id() == 0) a.blk_w[(long long)b * a.nbs + blk] = q;
+  for (int i = 0; i < TL::NV; i++) {
+    double ws[TL::EPV];
+    group_masses<Tin>(dw, rt[i], dw.resid ? rd[i] : rt[i], ws);
+    double ls = 0.0;
+#pragma unroll
+    for (int e = 0; e < TL::EPV; e++) ls += ws[e];
+    const u64 q = wave_sum((u64)ls);
+    if (lane_id() == 0) gw[i] = q;
+  }
 }
 
 struct DrawScratch {
@@ -399,15 +492,16 @@ struct DrawScratch {
 };
 
 // Block of the first id whose inclusive prefix (id order) exceeds
-// floor(total * uq / 2^24), from the block masses bw[0, nb) (wave 0).
-__device__ __forceinline__ void pick_block(const u64* bw, int nb, uint32_t uq, DrawScratch& ds) {
+// floor(total * uq / 2^24), from the block masses bw(i), i < nb (wave 0).
+template <class BW>
+__device__ __forceinline__ void pick_block(BW bw, int nb, uint32_t uq, DrawScratch& ds) {
   const int lane = lane_id();
   u64 vals[4];
   u64 ls = 0;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int i = 4 * lane + j;
-    vals[j] = i < nb ? bw[i] : 0ull;
+    vals[j] = i < nb ? bw(i) : 0ull;
     ls += vals[j];
   }
   const u64 incl = wave_incl_scan(ls);
@@ -437,37 +531,58 @@ __device__ __forceinline__ void pick_block(const u64* bw, int nb, uint32_t uq, D
   }
 }
 
-// Within block blk (wave 0): the first id whose inclusive prefix exceeds t,
-// given the mass `before` of the blocks ahead of it.
+// Within vector group i of block blk (wave 0): the first id whose inclusive
+// prefix exceeds t, given the mass `run` of everything ahead of the group;
+// -1 when the group does not reach t.
+template <typename Tin>
+__device__ __forceinline__ int pick_in_group(const SpecArgs& a, const DrawRow<Tin>& dw, int blk, int i, u64 t,
+                                             u64 run) {
+  constexpr int EPV = Elem<Tin>::EPV;
+  const int v = blk_id<Tin>(blk, i, 0);
+  const uint4 rt = load_vec<Tin>(dw.tr, v, dw.V, a.aligned);
+  const uint4 rd = dw.resid ? load_vec<Tin>(dw.dr, v, dw.V, a.aligned) : rt;
+  double ws[EPV];
+  group_masses<Tin>(dw, rt, rd, ws);
+  u64 ls = 0;
+#pragma unroll
+  for (int e = 0; e < EPV; e++) ls += (u64)ws[e];
+  const u64 incl = wave_incl_scan(ls);
+  u64 cum = run + incl - ls;
+  int mine = -1;
+#pragma unroll
+  for (int e = 0; e < EPV; e++) {
+    if (mine < 0 && cum + (u64)ws[e] > t) mine = v + e;
+    cum += (u64)ws[e];
+  }
+  const u64 bal = __ballot(mine >= 0);
+  return bal ? __shfl(mine, __ffsll((long long)bal) - 1, 64) : -1;
+}
+
+// Within block blk (wave 0), group by group.
 template <typename Tin>
 __device__ __forceinline__ int pick_in_block(const SpecArgs& a, const DrawRow<Tin>& dw, int blk, u64 t, u64 before) {
-  using TL = Tile<Tin>;
-  u64 ws[TL::EPL];
-  block_masses<Tin>(a, dw, blk, ws);
   u64 run = before;
-  int pick = -1;
+  for (int i = 0; i < Tile<Tin>::NV; i++) {
+    const int p = pick_in_group<Tin>(a, dw, blk, i, t, run);
+    if (p >= 0) return p;
+    // mass of the group, for the next one
+    constexpr int EPV = Elem<Tin>::EPV;
+    const int v = blk_id<Tin>(blk, i, 0);
+    const uint4 rt = load_vec<Tin>(dw.tr, v, dw.V, a.aligned);
+    const uint4 rd = dw.resid ? load_vec<Tin>(dw.dr, v, dw.V, a.aligned) : rt;
+    double ws[EPV];
+    group_masses<Tin>(dw, rt, rd, ws);
+    double ls = 0.0;
 #pragma unroll
-  for (int i = 0; i < TL::NV; i++) {
-    u64 ls = 0;
-#pragma unroll
-    for (int e = 0; e < TL::EPV; e++) ls += ws[i * TL::EPV + e];
-    const u64 incl = wave_incl_scan(ls);
-    u64 cum = run + incl - ls;
-    int mine = -1;
-#pragma unroll
-    for (int e = 0; e < TL::EPV; e++) {
-      if (mine < 0 && cum + ws[i * TL::EPV + e] > t) mine = blk_id<Tin>(blk, i, e);
-      cum += ws[i * TL::EPV + e];
-    }
-    const u64 bal = __ballot(mine >= 0);
-    if (pick < 0 && bal) pick = __shfl(mine, __ffsll((long long)bal) - 1, 64);
-    run += __shfl(incl, 63, 64);
+    for (int e = 0; e < EPV; e++) ls += ws[e];
+    run += wave_sum((u64)ls);
   }
-  return pick;
+  return -1;
 }
 
 template <typename Tin>
 __global__ __launch_bounds__(NT) void spec_draw_kernel(SpecArgs a) {
+  using TL = Tile<Tin>;
   __shared__ DrawScratch ds;
   const int b = blockIdx.x;
   if (b >= a.B) return;
@@ -475,31 +590,65 @@ __global__ __launch_bounds__(NT) void spec_draw_kernel(SpecArgs a) {
   if (s.status > 1) return;
   const uint32_t uq = (uint32_t)(a.u_res[b] * 16777216.0f);
   const int w = threadIdx.x >> 6;
-  const u64* bw = a.blk_w + (long long)b * a.nbs;
+  const u64* gw = a.blk_w + (long long)b * a.nbs * SPEC_GROUPS;
   bool resid = s.status == 1;
-  if (w == 0) pick_block(bw, a.nb, uq, ds);
+  if (w == 0)
+    pick_block([&](int i) {
+      u64 x = 0;
+#pragma unroll
+      for (int g = 0; g < TL::NV; g++) x += gw[i * SPEC_GROUPS + g];
+      return x;
+    }, a.nb, uq, ds);
   __syncthreads();
   if (resid && ds.total < 110ull) {
     // residual mass <= 1e-10: draw from the target row at the rejected
-    // position instead (its block masses summed here)
+    // position instead (its block masses summed here, id order within the
+    // chosen block group by group)
     resid = false;
     const DrawRow<Tin> dw = draw_row<Tin>(a, b, s, false);
     for (int blk = w; blk < a.nb; blk += WPB) {
-      u64 ws[Tile<Tin>::EPL];
-      block_masses<Tin>(a, dw, blk, ws);
-      u64 q = 0;
+      uint4 rt[TL::NV];
+      load_block<Tin>(dw.tr, blk, dw.V, a.aligned, rt);
+      double ls = 0.0;
 #pragma unroll
-      for (int j = 0; j < Tile<Tin>::EPL; j++) q += ws[j];
-      q = wave_sum(q);
+      for (int i = 0; i < TL::NV; i++) {
+        double ws[TL::EPV];
+        group_masses<Tin>(dw, rt[i], rt[i], ws);
+#pragma unroll
+        for (int e = 0; e < TL::EPV; e++) ls += ws[e];
+      }
+      const u64 q = wave_sum((u64)ls);
       if (lane_id() == 0) ds.wsum[blk] = q;
     }
     __syncthreads();
-    if (w == 0) pick_block(ds.wsum, a.nb, uq, ds);
+    if (w == 0) pick_block([&](int i) { return ds.wsum[i]; }, a.nb, uq, ds);
     __syncthreads();
+    if (w != 0) return;
+    const int pick = ds.blk >= 0 ? pick_in_block<Tin>(a, dw, ds.blk, ds.t, ds.before) : -1;
+    if (lane_id() == 0) {
+      a.out[(long long)b * (a.k + 1) + s.j] = pick;
+      a.n_acc[b] = s.j;
+    }
+    return;
   }
   if (w != 0) return;
-  const DrawRow<Tin> dw = draw_row<Tin>(a, b, s, resid);
-  const int pick = ds.blk >= 0 ? pick_in_block<Tin>(a, dw, ds.blk, ds.t, ds.before) : -1;
+  int pick = -1;
+  if (ds.blk >= 0) {
+    // the group of the chosen block that holds the draw, from its stored
+    // group masses, then the id within the group
+    const u64* g = gw + (long long)ds.blk * SPEC_GROUPS;
+    u64 run = ds.before;
+    int gi = TL::NV - 1;
+    for (int i = 0; i < TL::NV; i++) {
+      if (run + g[i] > ds.t) {
+        gi = i;
+        break;
+      }
+      run += g[i];
+    }
+    const DrawRow<Tin> dw = draw_row<Tin>(a, b, s, resid);
+    pick = pick_in_group<Tin>(a, dw, ds.blk, gi, ds.t, run);
+  }
   if (lane_id() == 0) {
     a.out[(long long)b * (a.k + 1) + s.j] = pick;
     a.n_acc[b] = s.j;
@@ -509,10 +658,11 @@ __global__ __launch_bounds__(NT) void spec_draw_kernel(SpecArgs a) {
 template <typename Tin>
 hipError_t launch_t(const SpecArgs& a, hipStream_t st) {
   const long long nblk = (long long)a.B * (2 * a.k + 1) * a.nb;
-  hipLaunchKernelGGL(spec_block_kernel<Tin>, dim3((unsigned)((nblk + WPB - 1) / WPB)), dim3(NT), 0, st, a);
+  const long long g1 = std::min<long long>((nblk + WPB - 1) / WPB, (long long)a.ncu * K1_WG_PER_CU);
+  hipLaunchKernelGGL(spec_block_kernel<Tin>, dim3((unsigned)g1), dim3(NT), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(spec_decide_kernel<Tin>, dim3(a.B), dim3(NT), 0, st, a);
+  hipLaunchKernelGGL(spec_decide_kernel<Tin>, dim3(a.B), dim3(DT), 0, st, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const long long nm = (long long)a.B * a.nb;
