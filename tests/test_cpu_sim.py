@@ -209,3 +209,41 @@ def test_device_shortcuts_equal_canonical_ops(sim, mode, n):
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert " 0 mismatches" in r.stdout
+
+
+def _topp_batch(seed, B, V, oracle, bf16=False):
+    x, params, u, hist, hist_len = _batch(seed, B, V, oracle)
+    g = np.random.default_rng(seed)
+    params["top_k"] = g.choice([0, -1, V, V + 7], size=B)  # no top-k: the top-p kernel
+    params["top_p"][::2] = 0.9
+    if bf16:
+        from tinygpt_amd import workloads as W
+
+        x = W.f32_to_bf16_bits(x)
+    return x, params, u, hist, hist_len
+
+
+def test_topp_kernel_rows(sim, oracle):
+    x, params, u, hist, hist_len = _topp_batch(21, 10, 3000, oracle)
+    _check(sim, oracle, x, params, u, hist, hist_len)
+
+
+def test_topp_kernel_mask_bf16(sim, oracle):
+    x, params, u, hist, hist_len = _topp_batch(22, 6, 2100, oracle, bf16=True)
+    g = np.random.default_rng(5)
+    words = (2100 + 31) // 32
+    mask = g.integers(0, 1 << 32, size=(4, words), dtype=np.uint64).astype(np.uint32)
+    mask[1] = 0
+    params["mask_state"] = g.integers(-1, 4, size=6)
+    _check(sim, oracle, x, params, u, hist, hist_len, mask=mask)
+
+
+def test_topp_kernel_bucket_overflow(sim, oracle):
+    # flat rows: every id in the first bucket (more than the ranked capacity)
+    B, V = 3, 5000
+    x = np.full((B, V), 0.75, np.float32)
+    x[1, ::3] = 0.7
+    params = oracle.make_params(B, temperature=1.0, top_k=0, top_p=0.37)
+    params["top_p"][2] = 1.0
+    u = np.array([0.1, 0.5, 0.99], np.float32)
+    _check(sim, oracle, x, params, u, None, None)

@@ -198,6 +198,7 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
     // with TGS_ETOOBIG / TGS_EHIP instead)
     if (tgs::set_sample_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_k64_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch) - 4096) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_topp_lds_limit(h->lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     e = hipDeviceSynchronize();
   }
   if (e != hipSuccess) {
@@ -352,6 +353,8 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   const size_t lds = (size_t)a.off_cand + (size_t)a.capt * 8;
   if (lds + sizeof(tgs::BlockScratch) > h->lds_limit)
     return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
+  if (a.full_rows && tgs::topp_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) > h->lds_limit)
+    return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS (top-p rows)");
   hipError_t e = tgs::launch_sample(a, dt, lds, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
   return TGS_OK;

@@ -20,6 +20,11 @@ constexpr int K64_CAND_ENTRIES = 2176;  // per-wave candidate staging (bf16 size
 constexpr int K64_BITMAP_WORDS = K64_TILE / 32;
 constexpr int K64_CNT_STRIDE = 32;
 
+// Top-p kernel (rows without a top-k): threads per workgroup and the most
+// ids of one histogram bucket ranked in LDS.
+constexpr int TOPP_NT = 1024;
+constexpr int TOPP_CAP = 2048;
+
 struct SampleArgs {
   const void* logits;
   long long row_stride;  // elements
@@ -73,12 +78,18 @@ constexpr int SPEC_MAX_K = 64;  // most draft tokens per sequence
 constexpr int SPEC_GROUPS = 4;  // 16-byte vector groups per block of 1024 ids (fp32: 4, bf16: 2)
 
 // Launches the chunk kernel, the merge kernel when rows are split (a.S > 1)
-// and the full-path kernel when a.full_rows is set, in that order on st.
+// and, when a.full_rows is set, the full-path kernel (rows with
+// KMAX < top_k < V) and the top-p kernel (rows without a top-k), in that
+// order on st.
 hipError_t launch_sample(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
 hipError_t set_sample_lds_limit(size_t bytes);
 // The fused kernel for batches of greedy rows and rows with top_k <= 64.
 hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
 hipError_t set_k64_lds_limit(size_t bytes);
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
+// Rows sampling top-p over the whole vocabulary (top_k disabled).
+size_t topp_lds_bytes(int V, int TS);
+hipError_t launch_topp(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
+hipError_t set_topp_lds_limit(size_t bytes);
 
 }  // namespace tgs

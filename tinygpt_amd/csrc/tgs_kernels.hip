@@ -16,6 +16,8 @@
 //                 chunk lists -- for k <= 64 entirely in wave registers
 //                 (bitonic top-64 merges) -- and finishes the row.
 //
+// Rows sampling top-p without a top-k run in tgs_topp.hip.
+//
 // The kernel boundary is the handoff between chunks: cross-workgroup
 // fences cost a full L2 writeback per workgroup on this part, a second
 // launch costs one dispatch.
@@ -579,8 +581,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(SampleArgs a) {
   else topk_chunk<Tin>(a, r, hash, bitmap, cand, s, raw, mw);
 }
 
-// Rows that need the full path (top_k disabled or above KMAX), one
-// workgroup per row; every other row returns at once.
+// Rows with KMAX < top_k < V, one workgroup per row; every other row
+// returns at once (rows without a top-k go to the top-p kernel).
 template <typename Tin>
 __global__ __launch_bounds__(NT) void full_kernel(SampleArgs a) {
   TGS_DYN_SMEM(smem);
@@ -590,7 +592,7 @@ __global__ __launch_bounds__(NT) void full_kernel(SampleArgs a) {
   const int b = blockIdx.x;
   if (b >= a.B) return;
   Row r;
-  if (!row_setup(a, b, 0, r) || r.mode != 2) return;
+  if (!row_setup(a, b, 0, r) || r.mode != 2 || !(r.k >= 1 && r.k < a.V)) return;
   if (r.use_pen) hash_build(a, r, hash, nullptr, 0);  // whole row, lookups per id
   full_path<Tin>(a, r, hash, cand, s);
 }
@@ -705,6 +707,8 @@ hipError_t launch_sample(const SampleArgs& a, int dtype, size_t lds, hipStream_t
     if (dtype == 1) hipLaunchKernelGGL(full_kernel<uint16_t>, dim3(a.B), blk, lds, st, a);
     else hipLaunchKernelGGL(full_kernel<float>, dim3(a.B), blk, lds, st, a);
     e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = launch_topp(a, dtype, topp_lds_bytes(a.V, a.TS), st);
   }
   return e;
 }

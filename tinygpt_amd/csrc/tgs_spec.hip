@@ -518,16 +518,16 @@ __device__ __forceinline__ void pick_block(BW bw, int nb, uint32_t uq, DrawScrat
     }
     cum += vals[j];
   }
+  // one lane writes the result (the first lane that found the block)
   const u64 bal = __ballot(found >= 0);
-  const int first = bal ? __ffsll((long long)bal) - 1 : -1;
+  const int first = bal ? __ffsll((long long)bal) - 1 : 0;
+  const int fb = __shfl(found, first, 64);
+  const u64 fbefore = __shfl(before, first, 64);
   if (lane == 0) {
-    ds.blk = -1;
+    ds.blk = fb;
+    ds.before = fbefore;
     ds.total = total;
     ds.t = t;
-  }
-  if (first >= 0 && lane == first) {
-    ds.blk = found;
-    ds.before = before;
   }
 }
 
