@@ -446,6 +446,8 @@ __device__ __forceinline__ T xor_lane(T x) {
   if constexpr (sizeof(T) == 8) {
     const u64 v = (u64)x;
     return (T)(((u64)xor_lane32<S>((uint32_t)(v >> 32)) << 32) | xor_lane32<S>((uint32_t)v));
+  } else if constexpr (__is_same(T, float)) {
+    return tg_u2f(xor_lane32<S>(tg_f2u(x)));  // the bits, not the value
   } else {
     return (T)xor_lane32<S>((uint32_t)x);
   }
