@@ -112,6 +112,8 @@ template <typename... Args>
 inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args... args) {
   g_grid_dim = grid;
   g_block_dim = block;
+  if (std::getenv("TGS_SIM_TRACE"))  // launch log (tests check which kernel ran)
+    std::fprintf(stderr, "launch grid=%u block=%u lds=%zu\n", grid.x, block.x, shmem);
   const unsigned nt = block.x;
   for (unsigned bx = 0; bx < grid.x; bx++) {
     BlockCtx ctx;

@@ -45,9 +45,13 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
             env["TGS_SPLIT"] = str(split)
         env.setdefault("ASAN_OPTIONS", "detect_leaks=0:abort_on_error=0")
         env.setdefault("UBSAN_OPTIONS", "halt_on_error=1:print_stacktrace=1")
+        env["TGS_SIM_TRACE"] = "1"
         p = subprocess.run([BIN, "sample", d], capture_output=True, text=True, env=env, timeout=timeout)
-        if p.stderr.strip():
-            print(p.stderr[-12000:])
+        launches = [tuple(int(f.split("=")[1]) for f in l.split()[1:3])
+                    for l in p.stderr.splitlines() if l.startswith("launch grid=")]
+        err = "\n".join(l for l in p.stderr.splitlines() if not l.startswith("launch grid="))
+        if err.strip():
+            print(err[-12000:])
         if p.returncode != 0:
             raise RuntimeError(f"run_case exit {p.returncode}\n{p.stdout[-4000:]}\n{p.stderr[-12000:]}")
         rd = lambda n, dt: np.fromfile(os.path.join(d, n), dt)
@@ -58,6 +62,7 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
                  mass=rd("out_mass.bin", np.uint64).reshape(B, 2),
                  cut_ids=rd("out_cut.bin", np.int32),
                  post_logits=rd("out_post.bin", np.float32).reshape(B, V) if post else None)
+        r["launches"] = launches  # (grid, block) of every kernel launch, in order
         return r
 
 

@@ -225,7 +225,8 @@ def _topp_batch(seed, B, V, oracle, bf16=False):
 
 def test_topp_kernel_rows(sim, oracle):
     x, params, u, hist, hist_len = _topp_batch(21, 10, 3000, oracle)
-    _check(sim, oracle, x, params, u, hist, hist_len)
+    r, _, _ = _check(sim, oracle, x, params, u, hist, hist_len)
+    assert (10, 1024) in r["launches"]  # the top-p kernel ran
 
 
 def test_topp_kernel_mask_bf16(sim, oracle):
@@ -247,3 +248,49 @@ def test_topp_kernel_bucket_overflow(sim, oracle):
     params["top_p"][2] = 1.0
     u = np.array([0.1, 0.5, 0.99], np.float32)
     _check(sim, oracle, x, params, u, None, None)
+
+
+def _topk_batch(seed, B, V, oracle, bf16=False):
+    x, params, u, hist, hist_len = _batch(seed, B, V, oracle)
+    g = np.random.default_rng(seed)
+    params["top_k"] = g.choice([1, 3, 64, 65, 200, 1000, 1024], size=B)
+    if bf16:
+        from tinygpt_amd import workloads as W
+
+        x = W.f32_to_bf16_bits(x)
+    return x, params, u, hist, hist_len
+
+
+def test_topk_kernel_rows(sim, oracle):
+    import tinygpt_amd as tg
+
+    # hint above 64: the register-resident top-k kernel (V * 4 bytes is a whole number of vectors)
+    x, params, u, hist, hist_len = _topk_batch(31, 9, 3000, oracle)
+    r, _, _ = _check(sim, oracle, x, params, u, hist, hist_len, hint=tg.batch_hint(params, 3000))
+    assert r["launches"] == [(9, 1024)]  # one 1024-thread workgroup per row
+
+
+def test_topk_kernel_bf16_mask(sim, oracle):
+    import tinygpt_amd as tg
+
+    x, params, u, hist, hist_len = _topk_batch(32, 6, 2048, oracle, bf16=True)
+    g = np.random.default_rng(6)
+    mask = g.integers(0, 1 << 32, size=(3, 64), dtype=np.uint64).astype(np.uint32)
+    mask[2] = 0
+    params["mask_state"] = g.integers(-1, 3, size=6)
+    r, _, _ = _check(sim, oracle, x, params, u, hist, hist_len, mask=mask, hint=tg.batch_hint(params, 2048))
+    assert r["launches"] == [(6, 1024)]
+
+
+def test_topk_kernel_candidate_overflow(sim, oracle):
+    import tinygpt_amd as tg
+
+    # one value everywhere but a few ids: every id ties at the bound, more
+    # candidates than the list holds
+    B, V = 2, 6000
+    x = np.full((B, V), 0.5, np.float32)
+    x[0, [5, 77, 4000]] = 3.0
+    params = oracle.make_params(B, temperature=0.9, top_k=700, top_p=0.8)
+    u = np.array([0.3, 0.95], np.float32)
+    r, _, _ = _check(sim, oracle, x, params, u, None, None, hint=tg.batch_hint(params, V))
+    assert r["launches"] == [(2, 1024)]

@@ -15,7 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libtgs_sampler.so")
-SOURCES = ["tgs_kernels.hip", "tgs_k64.hip", "tgs_spec.hip", "tgs_topp.hip", "tgs_api.hip"]
+SOURCES = ["tgs_kernels.hip", "tgs_k64.hip", "tgs_spec.hip", "tgs_topp.hip", "tgs_topk.hip", "tgs_api.hip"]
 ARCH = os.environ.get("TGS_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -44,15 +44,35 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    """Compiles every source to an object in parallel, then links the library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    comp = [f for f in HIPCC_FLAGS if f != "-shared"]
+
+    def compile_one(src):
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        cmd = [hipcc(), *comp, "-c", os.path.join(CSRC, src), "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        return src, obj, cmd, r
+
+    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
+        results = list(ex.map(compile_one, SOURCES))
+    msgs = []
+    for src, obj, cmd, r in results:
+        errors = "\n".join(l for l in (r.stderr or "").splitlines() if "packed-fp32-ops" not in l)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({r.returncode}):\n{' '.join(cmd)}\n{errors}")
+        if errors.strip():
+            msgs.append(errors)
     tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *srcs, "-o", tmp]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for _, o, _, _ in results], "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
-    errors = "\n".join(l for l in (r.stderr or "").splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{' '.join(cmd)}\n{errors}")
-    if verbose and errors.strip():
-        print(errors, file=sys.stderr)
+        raise RuntimeError(f"link failed ({r.returncode}):\n{' '.join(cmd)}\n{r.stderr}")
+    if verbose and msgs:
+        print("\n".join(msgs), file=sys.stderr)
     os.replace(tmp, OUT)
     return OUT
 

@@ -199,6 +199,7 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
     if (tgs::set_sample_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_k64_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch) - 4096) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topp_lds_limit(h->lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_topk_lds_limit(h->lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     e = hipDeviceSynchronize();
   }
   if (e != hipSuccess) {
@@ -336,6 +337,17 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
     if (lds + sizeof(tgs::BlockScratch) + 4096 > h->lds_limit)
       return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
     hipError_t e = tgs::launch_k64(a, dt, lds, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
+    return TGS_OK;
+  }
+  if (mk <= tgs::KMAX && mk < V && V <= tgs::topk_max_vocab(dt) && a.whole_vec && hist_cap <= tgs::KMAX &&
+      tgs::topk_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) <= h->lds_limit) {
+    // every row greedy or 1 <= top_k <= KMAX, the row fits in registers: one
+    // workgroup per row
+    a.full_rows = 0;
+    a.S = 1;
+    a.L = V;
+    hipError_t e = tgs::launch_topk(a, dt, tgs::topk_lds_bytes(V, a.TS), (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
     return TGS_OK;
   }

@@ -217,6 +217,7 @@ template <typename K, int NBITS, int BS = NT, class Enum>
 __device__ __forceinline__ K block_select_kth(Enum en, unsigned kth, BlockScratch& s) {
   K prefix = 0, pmask = 0;
   unsigned need = kth;
+#pragma unroll 1  // one pass live at a time: callers hold large register state across
   for (int shift = NBITS - 8; shift >= 0; shift -= 8) {
     for (int i = threadIdx.x; i < 256; i += BS) s.hc[i] = 0;
     __syncthreads();
@@ -274,6 +275,7 @@ __device__ __forceinline__ u64 block_mass_select(Enum en, u64 target, BlockScrat
   u64 mass_above = 0;
   unsigned cnt_above = 0;
   bool single = false;
+#pragma unroll 1
   for (int shift = 56; shift >= 0; shift -= 8) {
     for (int i = threadIdx.x; i < 256; i += BS) {
       s.hc[i] = 0;

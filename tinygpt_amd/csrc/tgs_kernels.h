@@ -25,6 +25,11 @@ constexpr int K64_CNT_STRIDE = 32;
 constexpr int TOPP_NT = 1024;
 constexpr int TOPP_CAP = 2048;
 
+// Top-k kernel (1 <= top_k <= KMAX, the row held in registers): threads per
+// workgroup and candidate capacity.
+constexpr int TOPK_NT = 1024;
+constexpr int TOPK_CAP = 4096;
+
 struct SampleArgs {
   const void* logits;
   long long row_stride;  // elements
@@ -91,5 +96,11 @@ hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
 size_t topp_lds_bytes(int V, int TS);
 hipError_t launch_topp(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
 hipError_t set_topp_lds_limit(size_t bytes);
+// Batches of greedy rows and rows with 1 <= top_k <= KMAX whose rows fit the
+// top-k kernel's registers (V <= topk_max_vocab(dtype)).
+int topk_max_vocab(int dtype);
+size_t topk_lds_bytes(int V, int TS);
+hipError_t launch_topk(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
+hipError_t set_topk_lds_limit(size_t bytes);
 
 }  // namespace tgs

@@ -107,6 +107,23 @@ struct RowView {
     }
   }
 
+  // f(id, y) for every allowed id of the row, read again from L2 / MALL
+  // (a rolled loop: no register-held state besides the caller's)
+  template <class F>
+  __device__ __forceinline__ void each_stream(F f) const {
+    const int nvec = (a.V + EPV - 1) / EPV;
+#pragma unroll 1
+    for (int vi = threadIdx.x; vi < nvec; vi += BT) {
+      const int v = vi * EPV;
+      const uint4 raw = load_vec<Tin>(rowp, v, a.V, a.aligned);
+      float yv[EPV];
+      vec_y(v, raw, yv);
+#pragma unroll
+      for (int e = 0; e < EPV; e++)
+        if (yv[e] > -__builtin_inff()) f(v + e, yv[e]);
+    }
+  }
+
   // f(id, y) for every allowed id of the row
   template <class F>
   __device__ __forceinline__ void each(F f) const {
@@ -312,7 +329,7 @@ __device__ __forceinline__ u64 select_in_bucket(const View& rv, float m, int bkt
     return R[i];
   }
   auto en = [&](auto f) {
-    rv.each([&](int id, float y) {
+    rv.each_stream([&](int id, float y) {
       if (bucket_of(y, m) == bkt) f(comp_key(tg_key(y), id), tg_q40(weight_le(y, m)));
     });
   };
