@@ -189,7 +189,11 @@ inline unsigned long long __ballot(int pred) {
 // DPP move: quad_perm (0x00-0xFF), row_shl:s (0x101-0x10F), row_shr:s
 // (0x111-0x11F), row_ror:s (0x121-0x12F), row_mirror (0x140); rows are 16
 // lanes; a source outside the row leaves `old` (bound_ctrl off, full masks).
-inline uint32_t __builtin_amdgcn_update_dpp(uint32_t old, uint32_t src, int ctrl, int, int, bool) {
+// DPP lane moves as the gfx9 ISA defines them: a lane whose source lies out
+// of its row (or of the wave), or whose row is off in row_mask, keeps `old`
+// (bound_ctrl off).  row_bcast:15 takes lane 15 of the previous row,
+// row_bcast:31 lane 31.
+inline uint32_t __builtin_amdgcn_update_dpp(uint32_t old, uint32_t src, int ctrl, int row_mask, int bank_mask, bool) {
   const int l = hipcpu::lane(), row = l & ~15, r = l & 15;
   int s = -1;
   if (ctrl <= 0xFF) s = (l & ~3) | ((ctrl >> (2 * (l & 3))) & 3);
@@ -197,7 +201,10 @@ inline uint32_t __builtin_amdgcn_update_dpp(uint32_t old, uint32_t src, int ctrl
   else if (ctrl >= 0x111 && ctrl <= 0x11F) s = r - (ctrl - 0x110) >= 0 ? l - (ctrl - 0x110) : -1;
   else if (ctrl >= 0x121 && ctrl <= 0x12F) s = row | ((r + (ctrl - 0x120)) & 15);
   else if (ctrl == 0x140) s = row | (15 - r);
+  else if (ctrl == 0x142) s = row >= 16 ? row - 1 : -1;
+  else if (ctrl == 0x143) s = 31;
   else std::abort();
+  if (!((row_mask >> (l >> 4)) & 1) || !((bank_mask >> (r >> 2)) & 1)) s = -1;
   const uint32_t v = hipcpu::exchange(src, s < 0 ? l : s);
   return s < 0 ? old : v;
 }

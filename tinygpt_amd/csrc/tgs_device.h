@@ -153,14 +153,33 @@ template <typename T>
 __device__ __forceinline__ T wave_max(T x);
 __device__ __forceinline__ float wave_maxf(float x);
 
+// Inclusive wave scan with DPP lane moves (no trip through LDS): Kogge-Stone
+// within rows of 16 lanes (row_shr 1, 2, 4, 8; a lane with no source adds
+// 0), then the row totals: row_bcast:15 adds lane 15 of rows 0 and 2 to
+// rows 1 and 3, row_bcast:31 adds lane 31 to rows 2 and 3.  Exact for
+// integer sums (32- or 64-bit lanes).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_or0(uint32_t x) {
+  return __builtin_amdgcn_update_dpp(0u, x, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS, typename T>
+__device__ __forceinline__ T dpp_or0_t(T x) {
+  if constexpr (sizeof(T) == 8) {
+    const u64 v = (u64)x;
+    return (T)(((u64)dpp_or0<CTRL, ROWS>((uint32_t)(v >> 32)) << 32) | dpp_or0<CTRL, ROWS>((uint32_t)v));
+  } else {
+    return (T)dpp_or0<CTRL, ROWS>((uint32_t)x);
+  }
+}
 template <typename T>
 __device__ __forceinline__ T wave_incl_scan(T x) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    T y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "integer lanes");
+  x += dpp_or0_t<0x111, 0xF>(x);  // row_shr:1
+  x += dpp_or0_t<0x112, 0xF>(x);  // row_shr:2
+  x += dpp_or0_t<0x114, 0xF>(x);  // row_shr:4
+  x += dpp_or0_t<0x118, 0xF>(x);  // row_shr:8
+  x += dpp_or0_t<0x142, 0xA>(x);  // row_bcast:15 into rows 1, 3
+  x += dpp_or0_t<0x143, 0xC>(x);  // row_bcast:31 into rows 2, 3
   return x;
 }
 
