@@ -142,9 +142,30 @@ __device__ __forceinline__ u64 mul_shr24(u64 a, uint32_t b) {
   return (hi << 40) | (lo >> 24);
 }
 
+// A 16-byte load that is not expected to be reused (streamed logits):
+// marked non-temporal so it does not displace cache lines that are.
+__device__ __forceinline__ uint4 tg_load_nt(const void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  const v4u t = __builtin_nontemporal_load((const v4u*)p);
+  return make_uint4(t.x, t.y, t.z, t.w);
+#else
+  return *(const uint4*)p;
+#endif
+}
+
 // ------------------------------------------------------------------ waves
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Lane l's value (l wave-uniform) through the scalar unit, bit for bit.
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, l);
+}
+__device__ __forceinline__ u64 readlane_u64(u64 x, int l) {
+  return ((u64)readlane_u32((uint32_t)(x >> 32), l) << 32) | readlane_u32((uint32_t)x, l);
+}
+__device__ __forceinline__ float readlane_f32(float x, int l) { return tg_u2f(readlane_u32(tg_f2u(x), l)); }
 
 // Butterfly wave reductions (defined with the lane permutes below).
 template <typename T>

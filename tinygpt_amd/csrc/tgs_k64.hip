@@ -57,6 +57,7 @@ constexpr int KM = 64;                   // largest top_k served
 constexpr int NHID = K64_MAX_HIST / BS;  // history ids per thread
 constexpr u64 EMPTY = ~0ull;             // list entry not written yet: above every composite
 constexpr int SPIN_LIMIT = 1 << 18;      // polls of one list before the wait gives up
+constexpr int KM_PRE = 2;                // lists per wave the merging workgroup requests early (S <= 8)
 
 // A tile gives every thread 64 elements: 16384 ids.
 template <typename Tin>
@@ -87,7 +88,7 @@ __device__ __forceinline__ void load_tile(const Tin* rowp, int t0, int v1, bool 
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
-    if constexpr (VEC) raw[u] = *(const uint4*)(rowp + (v < v1 ? v : v1 - EPV));
+    if constexpr (VEC) raw[u] = tg_load_nt(rowp + (v < v1 ? v : v1 - EPV));
     else raw[u] = load_vec<Tin>(rowp, v, v1, aligned);
   }
 }
@@ -454,7 +455,21 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
     }
   }
   // candidates are >= thr; every allowed composite is far above the id part
+  if (threadIdx.x == 0) elect = a.S > 1 && arrived == (unsigned)(a.S - 1);  // published by the next barrier
   const u64 thr = ((u64)first_threshold(mx, k, thr_w) << 32) | 1ull;
+  // the merging workgroup requests the other chunks' lists now, so that
+  // their load overlaps its own candidate work; entries still empty are
+  // polled again at the merge
+  u64 pre[KM_PRE];
+  const bool elected = elect != 0;
+  u64* lists = a.lists + (long long)b * a.S * KM;
+#pragma unroll
+  for (int q = 0; q < KM_PRE; q++) {
+    const int cc = w + q * NWB;
+    pre[q] = (elected && cc < a.S && cc != c)
+                 ? __hip_atomic_load(lists + (long long)cc * KM + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                 : EMPTY;
+  }
   const float tf = thr_value(thr);
 
   // Every element >= tf, wave by wave.  A vector whose maximum reaches tf
@@ -529,7 +544,6 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
     }
   }
   if (wovf && lane == 0) ovf = 1;
-  if (threadIdx.x == 0) elect = a.S > 1 && arrived == (unsigned)(a.S - 1);
   tops[w][lane] = xs;
   __syncthreads();
   u64 acc = 0ull;  // wave 0: the chunk's top 64 candidates, sorted
@@ -567,8 +581,7 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
     }
     return;
   }
-  u64* lists = a.lists + (long long)b * a.S * KM;
-  if (!elect) {
+  if (!elected) {
     // publish the chunk's list for the row's merging workgroup
     if (w == 0) __hip_atomic_store(lists + (long long)c * KM + lane, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
@@ -585,7 +598,8 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
       x = own[lane];
     } else {
       const u64* lp = lists + (long long)cc * KM + lane;
-      x = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int q = (cc - w) / NWB;
+      x = q < KM_PRE ? pre[q] : __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       int spins = 0;
       while (__ballot(x == EMPTY) != 0ull) {
         if (++spins > SPIN_LIMIT) {

@@ -220,10 +220,10 @@ __device__ __forceinline__ void wave_finalize(const SampleArgs& a, const Row& r,
   const int lane = lane_id();
   const int b = r.b;
   const float y = comp_y(x);
-  const float m = __shfl(y, 0, 64);
+  const float m = readlane_f32(y, 0);
   const u64 q = lane < n ? tg_q40(tg_weight(y, m)) : 0ull;
   const u64 C = wave_incl_scan(q);
-  const u64 S = __shfl(C, n - 1, 64);
+  const u64 S = readlane_u64(C, n - 1);
   int istar = n - 1;
   if (r.top_p < 1.0f) {
     const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
@@ -231,13 +231,13 @@ __device__ __forceinline__ void wave_finalize(const SampleArgs& a, const Row& r,
     const u64 bal = __ballot(lane < n && C >= P);
     istar = __ffsll((long long)bal) - 1;
   }
-  const u64 Sp = __shfl(C, istar, 64);
+  const u64 Sp = readlane_u64(C, istar);
   const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
   const u64 t = mul_shr24(Sp, uq);
   const u64 bal2 = __ballot(lane <= istar && C > t);
   const int pick = bal2 ? __ffsll((long long)bal2) - 1 : istar;
-  const u64 xp = __shfl(x, pick, 64);
-  const u64 xc = __shfl(x, istar, 64);
+  const u64 xp = readlane_u64(x, pick);
+  const u64 xc = readlane_u64(x, istar);
   if (lane == 0) {
     a.out[b] = comp_id(xp);
     write_row_diag(a, b, n, istar + 1, S, Sp, comp_id(xc));
