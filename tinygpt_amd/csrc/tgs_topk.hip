@@ -16,10 +16,9 @@
 //           above the bound.  Temperature is applied after the bound: 16
 //           representable values of slack keep every id whose scaled logit
 //           could round to the bound's.
-//   collect every id at or above the bound (registers, counted then
-//           written) as composites (logit desc, id asc) into LDS; entries of
-//           history ids are replaced by every history id with its penalised
-//           logit.
+//   collect every non-history id at or above the bound (registers, counted
+//           then written), plus every history id with its penalised logit,
+//           as composites (logit desc, id asc) into LDS.
 //   select  the exact k-th composite (radix select over the candidates),
 //           the k kept in order by a block bitonic sort (one per thread),
 //           then masses, top-p and the draw.
@@ -45,7 +44,6 @@ struct Scratch {
   u64 red64[WT];
   unsigned red32[WT];
   unsigned nc;    // candidates written
-  uint32_t tkey;  // the bound (order key)
   int imin0, imin1;
 };
 
@@ -287,17 +285,18 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
   const uint32_t kneg = 0x007FFFFFu;  // key of -inf
   const float thz = tkey > kneg + 16u ? tg_unkey(tkey - 16u) : -__builtin_inff();
 
-  // collect: every id at or above the bound (history ids too, dropped
-  // below: their list entries carry the unpenalised logit), counted without
-  // branches, placed by a wave scan, written vector by vector (a vector no
-  // lane needs is skipped)
+  // collect: every non-history id at or above the bound (counted, placed by
+  // a wave scan, written), then every history id with its penalised logit
   const float thf = fmaxf(thz, -3.40282347e38f);  // -inf never qualifies
   unsigned cnt = 0;
 #pragma unroll
   for (int j = 0; j < NVR; j++) {
     const uint32_t mw = MASK && mask ? RG::mword(r, V, j) : 0xFFFFFFFFu;
 #pragma unroll
-    for (int e = 0; e < EPV; e++) cnt += g.template xval<MASK>(j, e, mw) >= thf ? 1u : 0u;
+    for (int e = 0; e < EPV; e++) {
+      const float x = g.template xval<MASK>(j, e, mw);
+      if (x >= thf && !(r.use_pen && hist_bit(hbits, RG::vec_id(j) + e))) cnt++;
+    }
   }
   g.fence();
   if (threadIdx.x == 0) ts.nc = 0;
@@ -307,37 +306,22 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
   if (lane_id() == 63 && wincl) wbase = atomicAdd(&ts.nc, wincl);
   wbase = __shfl(wbase, 63, 64);
   unsigned slot = wbase + wincl - cnt;
-  if (__ballot(cnt != 0)) {
+  if (cnt) {
 #pragma unroll
     for (int j = 0; j < NVR; j++) {
       const uint32_t mw = MASK && mask ? RG::mword(r, V, j) : 0xFFFFFFFFu;
-      float xs[EPV];
-      bool any = false;
 #pragma unroll
       for (int e = 0; e < EPV; e++) {
-        xs[e] = g.template xval<MASK>(j, e, mw);
-        any = any || xs[e] >= thf;
-      }
-      if (__ballot(any) == 0ull) continue;
-#pragma unroll
-      for (int e = 0; e < EPV; e++)
-        if (xs[e] >= thf) {
-          if (slot < (unsigned)CAPK) cand[slot] = comp_of(xs[e], true, r.invT, RG::vec_id(j) + e);
+        const float x = g.template xval<MASK>(j, e, mw);
+        const int id = RG::vec_id(j) + e;
+        if (x >= thf && !(r.use_pen && hist_bit(hbits, id))) {
+          if (slot < (unsigned)CAPK) cand[slot] = comp_of(x, true, r.invT, id);
           slot++;  // a composite 0 (scaled to -inf) drops out below
         }
+      }
     }
   }
   if (r.use_pen) {
-    __syncthreads();
-    // main entries of history ids carry the raw logit: drop them, then add
-    // every history id with its penalised logit (the count of main entries
-    // is read by every thread before any history entry is appended)
-    const int nmain = min((int)ts.nc, CAPK);
-    __syncthreads();
-    for (int i = threadIdx.x; i < nmain; i += BT) {
-      const u64 c = cand[i];
-      if (c && hist_bit(hbits, comp_id(c))) cand[i] = 0ull;
-    }
     for (int i = threadIdx.x; i < a.TS; i += BT) {
       const int2 h = hash[i];
       if (h.x == -1) continue;
@@ -345,8 +329,8 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
       const float z = penalise(Elem<Tin>::scalar(rowp, id), h.y, r);
       const u64 c = comp_of(z, mask_allows(r, id), r.invT, id);
       if (c) {
-        const unsigned s = atomicAdd(&ts.nc, 1u);
-        if (s < (unsigned)CAPK) cand[s] = c;
+        const unsigned sl = atomicAdd(&ts.nc, 1u);
+        if (sl < (unsigned)CAPK) cand[sl] = c;
       }
     }
   }
