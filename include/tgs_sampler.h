@@ -98,11 +98,14 @@ typedef struct {
 
 /* Host-side summary of a batch's row parameters.  It selects kernels
  * specialised for the batch: max_top_k <= 64 -> one-tile chunks merged in
- * wave registers; <= 1024 -> candidate path; otherwise (or no hint) the
- * candidate path plus the full-path kernel for rows without a usable top-k.
- * The hint is a promise: a sampling row whose top_k exceeds max_top_k (a
- * row without a usable top-k counts as V) gets id -3.  Greedy rows are
- * served under any hint. */
+ * wave registers (one launch); <= 1024 -> one workgroup per row holding the
+ * row in registers (16-byte aligned rows of whole vectors: bf16 V <= 163840,
+ * fp32 V <= 81920, history <= 1024 ids), else the candidate path; otherwise
+ * (or no hint) the candidate path, the full-path kernel for rows with
+ * 1024 < top_k < V and the top-p kernel for rows without a top-k.  The hint
+ * is a promise: a sampling row whose top_k exceeds max_top_k (a row without
+ * a usable top-k counts as V) gets id -3.  Greedy rows are served under any
+ * hint. */
 typedef struct {
   int32_t max_top_k; /* max over sampling rows of top_k when 1 <= top_k < V, else V;
                         0 when every row is greedy */
