@@ -282,6 +282,37 @@ def test_topk_kernel_bf16_mask(sim, oracle):
     assert r["launches"] == [(6, 1024)]
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_topk_kernel_tail_buckets(sim, oracle, bf16):
+    """Rows that drive every path of the top-k kernel's bucket tail: ties
+    filling a bucket past one wave (counting ranks) and past the ranking
+    capacity (radix selections within the bucket), kept ids in the mass-0
+    bucket (y - m <= -32) with top-p off (cut = k-th id), a top-p target of
+    0, greedy rows, rows of mostly or only negative logits."""
+    import tinygpt_amd as tg
+
+    B, V = 7, 3000
+    g = np.random.default_rng(41)
+    x = np.empty((B, V), np.float32)
+    x[0] = np.round(g.normal(0.0, 2.0, V) * 4.0) / 4.0  # ~30 distinct values: ties
+    x[1] = 0.25
+    x[1, [7, 900, 2999]] = [2.0, 1.0, 1.5]  # one huge bucket
+    x[2] = g.normal(0.0, 1.0, V)  # T = 0.01: most kept ids carry mass 0
+    x[3] = g.normal(0.0, 3.0, V) - 6.0
+    x[4] = np.round(g.normal(0.0, 1.0, V) * 2.0) / 2.0
+    x[5] = g.normal(0.0, 2.0, V) - 50.0  # all negative: the bound from group minima
+    x[6] = np.round(g.normal(0.0, 2.0, V))
+    params = oracle.make_params(B, temperature=[1.0, 0.7, 0.01, 1.3, 0.5, 0.0, 2.0],
+                                top_k=[1000, 1024, 500, 800, 1024, 5, 64], top_p=[0.9, 0.5, 1.0, 1e-9, 1.0, 1.0, 0.999])
+    u = g.random(B).astype(np.float32)
+    if bf16:
+        from tinygpt_amd import workloads as W
+
+        x = W.f32_to_bf16_bits(x)
+    r, _, _ = _check(sim, oracle, x, params, u, None, None, hint=tg.batch_hint(params, V))
+    assert r["launches"] == [(B, 1024)]
+
+
 def test_topk_kernel_candidate_overflow(sim, oracle):
     import tinygpt_amd as tg
 

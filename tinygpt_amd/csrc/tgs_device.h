@@ -154,6 +154,32 @@ __device__ __forceinline__ uint4 tg_load_nt(const void* p) {
 #endif
 }
 
+// Per-half signed 16-bit maxima of two words (one packed max).
+__device__ __forceinline__ uint32_t pk_max_i16(uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b)));
+#else
+  const short al = (short)(a & 0xFFFFu), bl = (short)(b & 0xFFFFu);
+  const short ah = (short)(a >> 16), bh = (short)(b >> 16);
+  return (uint32_t)(uint16_t)(al > bl ? al : bl) | ((uint32_t)(uint16_t)(ah > bh ? ah : bh) << 16);
+#endif
+}
+
+// Per-half signed 16-bit minima of two words (one packed min).
+__device__ __forceinline__ uint32_t pk_min_i16(uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_min(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b)));
+#else
+  const short al = (short)(a & 0xFFFFu), bl = (short)(b & 0xFFFFu);
+  const short ah = (short)(a >> 16), bh = (short)(b >> 16);
+  return (uint32_t)(uint16_t)(al < bl ? al : bl) | ((uint32_t)(uint16_t)(ah < bh ? ah : bh) << 16);
+#endif
+}
+
 // ------------------------------------------------------------------ waves
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

@@ -7,24 +7,36 @@
 //   load    every thread issues its NVR 16-byte vectors (ids tid*EPV +
 //           j*1024*EPV) and keeps them; the row's history (ids -> counts)
 //           goes into an LDS hash and a bitmap while they are in flight.
-//   bound   each thread keeps the two largest allowed logits among its ids
-//           (NaN and masked ids count as -inf; three min/max per id).  Any k'
-//           of the 2048 values are distinct ids, so the k'-th largest is a
-//           logit with at least k' ids at or above it.  History ids may
+//   bound   four slot values per thread, each the largest logit of a
+//           disjoint group of its ids (packed 16-bit integer maxima and
+//           minima of the raw bf16 words, 32-bit ones of fp32 words; -inf
+//           where that lands on a NaN).  So at least k' distinct ids lie at
+//           or above the k'-th largest slot value.  History ids may
 //           still be penalised downward, so k' = k + (distinct history ids
-//           of the row): at least k ids that are not history ids lie at or
-//           above the bound.  Temperature is applied after the bound: 16
-//           representable values of slack keep every id whose scaled logit
-//           could round to the bound's.
-//   collect every non-history id at or above the bound (registers, counted
-//           then written), plus every history id with its penalised logit,
-//           as composites (logit desc, id asc) into LDS.
-//   select  the exact k-th composite (radix select over the candidates),
-//           the k kept in order by a block bitonic sort (one per thread),
-//           then masses, top-p and the draw.
+//           of the row).  The k'-th slot is found to 16 key bits by one
+//           histogram of the slots' distance below the largest one (a radix
+//           pass only when it lies more than 254 bf16 steps below).
+//           Temperature is applied after the bound: 16 representable values
+//           of slack keep every id whose scaled logit could round to the
+//           bound's.
+//   collect one compare per id (16-bit compares on the raw bf16 halves)
+//           shifted into per-thread bit masks; the set bits become ids in LDS
+//           (block offsets from a wave scan); their logits are read again (a
+//           scattered gather) and turned into composites (logit desc, id
+//           asc), history ids skipped there and added with their penalised
+//           logits instead.
+//   tail    over the candidates (at most 4096, four per thread): the maximum
+//           m, then a count and exact-mass histogram over 1024 buckets of
+//           width 1/32 below m (y - m <= -32, mass 0, in one more bucket).
+//           Bucket order follows the composite order, so prefixes over the
+//           buckets find the bucket of the k-th composite, of the top-p cut
+//           and of the draw; only those buckets are ranked (a wave sort of
+//           at most 64, else counting ranks) to place the element inside.
 //
 // A candidate list beyond its capacity (massive ties at the bound) falls
-// back to a radix selection over all ids of the row, still in registers.
+// back to a radix selection over all ids of the row, read again from
+// L2 / MALL; a bucket beyond the ranking capacity to radix selections
+// restricted to it.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 #include "tgs_row.h"
@@ -32,9 +44,14 @@
 namespace tgs {
 namespace topk {
 
-constexpr int BT = TOPK_NT;   // threads per workgroup
-constexpr int WT = BT / 64;   // waves
-constexpr int CAPK = TOPK_CAP;
+constexpr int BT = TOPK_NT;    // threads per workgroup
+constexpr int WT = BT / 64;    // waves
+constexpr int CAPK = TOPK_CAP; // candidates
+constexpr int CPT = CAPK / BT; // candidates per thread in the tail
+constexpr int NB = 1024;       // mass buckets of width 1/32 below the maximum (+1 for mass 0)
+constexpr int LCAP = KMAX;     // ids of one bucket ranked in LDS
+static_assert(NB == BT, "one bucket per thread in the prefix");
+static_assert(2 * LCAP * 8 >= CAPK * 4, "candidate ids alias the ranking lists");
 
 struct alignas(16) u64x2 {
   u64 x, y;
@@ -42,9 +59,14 @@ struct alignas(16) u64x2 {
 
 struct Scratch {
   u64 red64[WT];
+  u64 red64b[WT];
   unsigned red32[WT];
   unsigned nc;    // candidates written
-  int imin0, imin1;
+  unsigned ng;    // bucket members gathered
+  unsigned need;  // bound: slots still needed below the histogram range
+  int dsel;       // bound: histogram bin of the k'-th slot
+  int sel[3];     // tail: buckets of the k-th, of the cut and of the draw
+  int first;      // tail: first rank meeting a mass target
 };
 
 template <typename T>
@@ -59,18 +81,19 @@ __device__ __forceinline__ T bsum(T x, T* red) {
   return t;
 }
 
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 template <typename Tin, int NVR>
 struct Regs {
   static constexpr int EPV = Elem<Tin>::EPV;
   uint4 raw[NVR];  // the row, packed as loaded
   __device__ __forceinline__ static int vec_id(int j) { return ((int)threadIdx.x + j * BT) * EPV; }
-  // mask word of vector j (vectors past the row end hold NaN already)
-  __device__ __forceinline__ static uint32_t mword(const Row& r, int V, int j) {
-    const int v = vec_id(j);
-    return r.mrow[(v < V ? v : V - 1) >> 5];
-  }
   // every vector, from addresses clamped into the row (the row is 16-byte
-  // aligned and a whole number of vectors); vectors past the end become NaN
+  // aligned and a whole number of vectors); vectors past the end become
+  // all-ones words: NaN in every element, below every logit as a signed
+  // integer and never at or above a bound
   __device__ __forceinline__ void load(const Tin* rowp, int V) {
 #pragma unroll
     for (int j = 0; j < NVR; j++) {
@@ -79,24 +102,27 @@ struct Regs {
     }
 #pragma unroll
     for (int j = 0; j < NVR; j++)
-      if (vec_id(j) >= V) raw[j] = make_uint4(Elem<Tin>::NAN_BITS, Elem<Tin>::NAN_BITS, Elem<Tin>::NAN_BITS, Elem<Tin>::NAN_BITS);
+      if (vec_id(j) >= V) raw[j] = make_uint4(~0u, ~0u, ~0u, ~0u);
   }
-  // logit of element e of vector j mapped for the bound: -inf when NaN,
-  // -inf or masked out (and for ids past the row end)
-  template <bool MASK>
-  __device__ __forceinline__ float xval(int j, int e, uint32_t mw) const {
-    const float x = fmaxf(Elem<Tin>::get(raw[j], e), -__builtin_inff());
-    if constexpr (!MASK) return x;
-    return ((mw >> ((vec_id(j) + e) & 31)) & 1u) ? x : -__builtin_inff();
-  }
-  // Each pass over the row unpacks it again: an empty asm on the packed
-  // registers keeps the compiler from holding every unpacked logit live from
-  // one pass to the next (they do not fit the register budget).
-  __device__ __forceinline__ void fence() {
-#if defined(__HIP_DEVICE_COMPILE__)
+  // a masked-out element becomes the all-ones pattern (as past the row end)
+  __device__ __forceinline__ void apply_mask(const Row& r, int V) {
 #pragma unroll
-    for (int j = 0; j < NVR; j++) asm volatile("" : "+v"(raw[j].x), "+v"(raw[j].y), "+v"(raw[j].z), "+v"(raw[j].w));
-#endif
+    for (int j = 0; j < NVR; j++) {
+      const int v = vec_id(j);
+      const uint32_t bits = (r.mrow[(v < V ? v : V - 1) >> 5] >> (v & 31)) & ((1u << EPV) - 1u);
+      uint32_t wd[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        if constexpr (EPV == 8) {
+          const uint32_t lo = ((bits >> (2 * w)) & 1u) ? 0u : 0x0000FFFFu;
+          const uint32_t hi = ((bits >> (2 * w + 1)) & 1u) ? 0u : 0xFFFF0000u;
+          wd[w] |= lo | hi;
+        } else {
+          wd[w] |= ((bits >> w) & 1u) ? 0u : 0xFFFFFFFFu;
+        }
+      }
+      raw[j] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    }
   }
 };
 
@@ -109,104 +135,130 @@ __device__ __forceinline__ u64 comp_of(float z, bool allowed, float invT, int id
   return (allowed && y > -__builtin_inff()) ? comp_key(tg_key(y), id) : 0ull;
 }
 
-// Block bitonic sort, descending, of BT * RG values, RG per thread: element
-// (w * RG + h) * 64 + lane is x[h] of lane `lane` of wave w.  Partners in the
-// same 64-block move through lane permutes; stride 64 (RG == 2) swaps the
-// thread's two registers; wider strides go through LDS (buf: BT * RG
-// entries).  Every thread calls it.
-template <int RG, typename T>
-__device__ __forceinline__ void block_sort_desc(T (&x)[RG], T* buf) {
-  const int lane = lane_id(), w = threadIdx.x >> 6;
-  constexpr int N = BT * RG;
+__device__ __forceinline__ float nan_to_ninf(float x) { return x == x ? x : -__builtin_inff(); }
+
+// Four slot values of this thread: the largest logit of each of four
+// disjoint groups of its ids, from signed-integer maxima and minima of the
+// raw patterns (a group with a non-negative logit: its largest pattern; an
+// all-negative group: its smallest pattern, the negative logit nearest 0).
+// A NaN pattern there (NaN logits, masked-out ids, vectors past the end hold
+// all-ones) gives -inf: still at most the group's largest logit.
+template <typename Tin, int NVR>
+__device__ __forceinline__ void slot_values(const Regs<Tin, NVR>& g, float (&s)[4]) {
+  if constexpr (sizeof(Tin) == 2) {
+    uint32_t hi[2] = {0x80008000u, 0x80008000u}, lo[2] = {0x7FFF7FFFu, 0x7FFF7FFFu};
 #pragma unroll
-  for (int k = 2; k <= N; k <<= 1) {
+    for (int j = 0; j < NVR; j++)
 #pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j >= 64 * RG) {
-#pragma unroll
-        for (int h = 0; h < RG; h++) buf[(w * RG + h) * 64 + lane] = x[h];
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < RG; h++) {
-          const int i = (w * RG + h) * 64 + lane;
-          const T y = buf[i ^ j];
-          const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
-          x[h] = keep_max ? (y > x[h] ? y : x[h]) : (y < x[h] ? y : x[h]);
-        }
-        __syncthreads();
-      } else if (j >= 64) {
-        if constexpr (RG == 2) {
-          const bool desc = (((w * 2) * 64 + lane) & k) == 0;
-          const T hi = x[0] > x[1] ? x[0] : x[1], lo = x[0] > x[1] ? x[1] : x[0];
-          x[0] = desc ? hi : lo;
-          x[1] = desc ? lo : hi;
-        }
-      } else {
-#pragma unroll
-        for (int h = 0; h < RG; h++) {
-          const int i = (w * RG + h) * 64 + lane;
-          const T y = xor_lane_s(x[h], j);
-          const bool keep_max = ((lane & j) == 0) == ((i & k) == 0);
-          x[h] = keep_max ? (y > x[h] ? y : x[h]) : (y < x[h] ? y : x[h]);
-        }
+      for (int w = 0; w < 4; w++) {
+        const int h = (j * 2) / NVR;
+        hi[h] = pk_max_i16(hi[h], word_of(g.raw[j], w));
+        lo[h] = pk_min_i16(lo[h], word_of(g.raw[j], w));
       }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t b0 = (hi[h] & 0x8000u) ? (lo[h] & 0xFFFFu) : (hi[h] & 0xFFFFu);
+      const uint32_t b1 = (hi[h] & 0x80000000u) ? (lo[h] >> 16) : (hi[h] >> 16);
+      s[2 * h] = nan_to_ninf(tg_u2f(b0 << 16));
+      s[2 * h + 1] = nan_to_ninf(tg_u2f(b1 << 16));
     }
+  } else {
+    int hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      hi[i] = (int)0x80000000u;
+      lo[i] = 0x7FFFFFFF;
+    }
+#pragma unroll
+    for (int j = 0; j < NVR; j++)
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        const int i = (j * 4) / NVR;
+        const int x = (int)word_of(g.raw[j], w);
+        hi[i] = x > hi[i] ? x : hi[i];
+        lo[i] = x < lo[i] ? x : lo[i];
+      }
+#pragma unroll
+    for (int i = 0; i < 4; i++) s[i] = nan_to_ninf(tg_u2f((uint32_t)(hi[i] >= 0 ? hi[i] : lo[i])));
   }
 }
 
-// Softmax masses of the n sorted kept composites R, top-p cut, draw and the
-// outputs (row b, sampling mode).  C gets the inclusive mass prefix.
-__device__ __forceinline__ void finish(const SampleArgs& a, const Row& r, const u64* R, u64* C, int n, Scratch& ts) {
-  const int b = r.b;
-  const float m = comp_y(R[0]);
-  const u64 q = (int)threadIdx.x < n ? tg_q40(tg_weight(comp_y(R[threadIdx.x]), m)) : 0ull;
-  const u64 wi = wave_incl_scan(q);
-  if (lane_id() == 63) ts.red64[threadIdx.x >> 6] = wi;
-  if (threadIdx.x == 0) {
-    ts.imin0 = n - 1;
-    ts.imin1 = 0x7FFFFFFF;
+// 16-bit key prefix T16 with at least kp slots whose key >> 16 is >= T16
+// (kp <= 4 * BT).  One histogram of each slot's distance (in 16-bit key
+// steps) below the largest slot, bins 0..254 exact, 255 for the rest; a
+// radix selection restricted to that last bin when the k'-th lies there.
+__device__ __forceinline__ uint32_t bound_key16(const float (&s)[4], unsigned kp, Scratch& ts, BlockScratch& bs) {
+  uint32_t k16[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) k16[i] = tg_key(s[i]) >> 16;
+  uint32_t mx = k16[0];
+#pragma unroll
+  for (int i = 1; i < 4; i++) mx = k16[i] > mx ? k16[i] : mx;
+  mx = wave_max(mx);
+  if (lane_id() == 0) ts.red32[threadIdx.x >> 6] = mx;
+  if (threadIdx.x < 256) bs.hc[threadIdx.x] = 0;
+  __syncthreads();
+  uint32_t K0 = ts.red32[0];
+#pragma unroll
+  for (int i = 1; i < WT; i++) K0 = ts.red32[i] > K0 ? ts.red32[i] : K0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t d = K0 - k16[i];
+    atomicAdd(&bs.hc[d < 255u ? d : 255u], 1u);
   }
   __syncthreads();
-  u64 off = 0;
-  for (int i = 0; i < (int)(threadIdx.x >> 6); i++) off += ts.red64[i];
-  if ((int)threadIdx.x < n) C[threadIdx.x] = off + wi;
-  __syncthreads();
-  const u64 S = C[n - 1];
-  if (r.top_p < 1.0f) {
-    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
-    const u64 P = mul_shr24(S, pq);
-    const int i = threadIdx.x;
-    if (i < n && C[i] >= P && (i == 0 || C[i - 1] < P)) atomicMin(&ts.imin0, i);
-    __syncthreads();
-  }
-  const int istar = ts.imin0;
-  const u64 Sp = C[istar];
-  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
-  const u64 t = mul_shr24(Sp, uq);
-  {
-    const int i = threadIdx.x;
-    if (i <= istar && C[i] > t && (i == 0 || C[i - 1] <= t)) atomicMin(&ts.imin1, i);
-  }
-  __syncthreads();
-  int pick = ts.imin1;
-  if (pick > istar) pick = istar;
-  if (threadIdx.x == 0) {
-    a.out[b] = comp_id(R[pick]);
-    write_row_diag(a, b, n, istar + 1, S, Sp, comp_id(R[istar]));
-  }
-  if (a.dbg.kept_ids) {
-    int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT) kid[i] = i < n ? comp_id(R[i]) : -1;
-  }
-  if (a.dbg.kept_probs) {
-    float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
-    const float fs = tg_u64_to_f32(Sp);
-    for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT) {
-      float pv = 0.0f;
-      if (i <= istar) pv = tg_u64_to_f32(C[i] - (i ? C[i - 1] : 0ull)) / fs;
-      kp[i] = pv;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    unsigned cs[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) cs[j] = bs.hc[4 * lane + j];
+    const unsigned lsum = cs[0] + cs[1] + cs[2] + cs[3];
+    unsigned cum = wave_incl_scan(lsum) - lsum;
+    int found = -1;
+    unsigned above = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if (found < 0 && cs[j] > 0 && cum + cs[j] >= kp) {
+        found = 4 * lane + j;
+        above = cum;
+      }
+      cum += cs[j];
+    }
+    const u64 bal = __ballot(found >= 0);
+    const int first = bal ? __ffsll((long long)bal) - 1 : 0;
+    const int fd = __shfl(found, first, 64);
+    const unsigned fa = __shfl(above, first, 64);
+    if (lane == 0) {
+      ts.dsel = fd;
+      ts.need = kp - fa;
     }
   }
+  __syncthreads();
+  const int d = ts.dsel;
+  const unsigned need = ts.need;
+  if (d < 255) return K0 - (uint32_t)d;
+  return block_select_kth<uint32_t, 16, BT>(
+      [&](auto f) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (K0 - k16[i] >= 255u) f(k16[i]);
+      },
+      need, bs);
+}
+
+// Bucket of a candidate's y below the maximum m: 0 at y == m, NB for
+// y - m <= -32 (mass 0), else floor((m - y) * 32).
+__device__ __forceinline__ int bucket_of(float y, float m) {
+  if (y == m) return 0;
+  const float x = y - m;
+  if (!(x > -32.0f)) return NB;
+  return (int)(-x * 32.0f);
+}
+
+// Exact mass of a composite under the maximum m: floor(exp(y - m) 2^40).
+__device__ __forceinline__ u64 mass_of(u64 c, float m) {
+  const float y = comp_y(c);
+  return tg_q40(y == m ? 1.0f : tg_expf_nonpos(y - m));
 }
 
 __device__ __forceinline__ void finish_greedy(const SampleArgs& a, int b, u64 best) {
@@ -225,20 +277,378 @@ __device__ __forceinline__ void finish_greedy(const SampleArgs& a, int b, u64 be
   }
 }
 
+// Block bitonic sort, descending, of BT values, one per thread (thread i
+// holds element i).  Partners within a wave move through lane permutes,
+// wider strides through LDS (buf: BT entries).  Every thread calls it.
+__device__ __forceinline__ u64 block_sort_desc(u64 x, u64* buf) {
+  const int i = threadIdx.x;
+#pragma unroll 1
+  for (int k = 2; k <= BT; k <<= 1) {
+#pragma unroll 1
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      u64 y;
+      if (j >= 64) {
+        buf[i] = x;
+        __syncthreads();
+        y = buf[i ^ j];
+        __syncthreads();
+      } else {
+        y = xor_lane_s(x, j);
+      }
+      const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
+      x = keep_max ? (y > x ? y : x) : (y < x ? y : x);
+    }
+  }
+  return x;
+}
+
+// The candidates of one row, four per thread, and their buckets.
+struct Cands {
+  u64 c[CPT];
+  int bk[CPT];  // -1: no candidate
+};
+
+// Ranks the members of bucket bq (n of them, n uniform): R[0, n) their
+// composites descending, Q[0, n) the inclusive mass prefix.  Returns false
+// (nothing ranked) when n > LCAP.  ts.ng is 0 on entry and on return.
+__device__ __forceinline__ bool rank_bucket(const Cands& cd, int bq, unsigned n, float m, u64* L, u64* R, u64* Q,
+                                            Scratch& ts) {
+  if (n > (unsigned)LCAP) return false;
+  if (threadIdx.x == 0 && (n & 1)) L[n] = 0ull;  // pad below every composite
+#pragma unroll
+  for (int j = 0; j < CPT; j++)
+    if (cd.bk[j] == bq) L[atomicAdd(&ts.ng, 1u)] = cd.c[j];
+  __syncthreads();
+  const int w = threadIdx.x >> 6, lane = lane_id();
+  if (n <= 64) {
+    if (w == 0) {
+      u64 x = lane < (int)n ? L[lane] : 0ull;
+      x = wave_sort_desc(x);
+      const u64 q = lane < (int)n ? mass_of(x, m) : 0ull;
+      const u64 ci = wave_incl_scan(q);
+      if (lane < (int)n) {
+        R[lane] = x;
+        Q[lane] = ci;
+      }
+      if (lane == 0) ts.ng = 0;
+    }
+    __syncthreads();
+    return true;
+  }
+  // rank = number of larger composites (composites are distinct), counted by
+  // the waves that hold members, two entries per 16-byte broadcast read
+  const int i = threadIdx.x;
+  if (w * 64 < (int)n) {
+    const u64 x = i < (int)n ? L[i] : ~0ull;
+    int rk = 0;
+    const int np = ((int)n + 1) / 2;
+    const u64x2* L2 = (const u64x2*)L;
+#pragma unroll 4
+    for (int p = 0; p < np; p++) {
+      const u64x2 e = L2[p];
+      rk += (e.x > x) + (e.y > x);
+    }
+    if (i < (int)n) R[rk] = x;
+  }
+  __syncthreads();
+  const u64 q = i < (int)n ? mass_of(R[i], m) : 0ull;
+  const u64 wi = wave_incl_scan(q);
+  if (lane == 63) ts.red64b[w] = wi;
+  if (i == 0) ts.ng = 0;
+  __syncthreads();
+  u64 off = 0;
+  for (int v = 0; v < w; v++) off += ts.red64b[v];
+  if (i < (int)n) Q[i] = off + wi;
+  __syncthreads();
+  return true;
+}
+
+// First rank of a ranked bucket whose inclusive prefix reaches target (>= 1).
+__device__ __forceinline__ int first_rank(const u64* Q, unsigned n, u64 target, Scratch& ts) {
+  const int i = threadIdx.x;
+  if (i < (int)n && Q[i] >= target && (i == 0 || Q[i - 1] < target)) ts.first = i;
+  __syncthreads();
+  const int f = ts.first;
+  __syncthreads();
+  return f;
+}
+
+// The row's tail over nc candidates in cand[] (composites, 0 = none).
+template <bool DIAG>
+__device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, u64* cand, u64* L, u64* R, u64* Q,
+                                     unsigned* CI, u64* MI, Scratch& ts, BlockScratch& bs) {
+  const int b = r.b;
+  const int k = r.mode == 0 ? 1 : r.k;
+  const int lane = lane_id(), w = threadIdx.x >> 6;
+  Cands cd;
+  u64 mx = 0;
+#pragma unroll
+  for (int j = 0; j < CPT; j++) {
+    const int i = threadIdx.x + j * BT;
+    cd.c[j] = i < nc ? cand[i] : 0ull;
+    mx = cd.c[j] > mx ? cd.c[j] : mx;
+  }
+  mx = wave_max(mx);
+  if (lane == 0) ts.red64[w] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) ts.ng = 0;  // every thread has read the candidate count
+  u64 M = ts.red64[0];
+#pragma unroll
+  for (int i = 1; i < WT; i++) M = ts.red64[i] > M ? ts.red64[i] : M;
+  if (r.mode == 0) {  // greedy: the largest composite
+    finish_greedy(a, b, M);
+    return;
+  }
+  if (M == 0ull) {  // no allowed id
+    if (threadIdx.x == 0) {
+      a.out[b] = -1;
+      write_row_diag(a, b, 0, 0, 0, 0, -1);
+    }
+    if (a.dbg.kept_ids)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
+    if (a.dbg.kept_probs)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
+    return;
+  }
+  const float m = comp_y(M);
+
+  // count and mass histogram over the buckets (CI, MI cleared by the caller)
+#pragma unroll
+  for (int j = 0; j < CPT; j++) {
+    cd.bk[j] = -1;
+    if (cd.c[j]) {
+      const int bq = bucket_of(comp_y(cd.c[j]), m);
+      cd.bk[j] = bq;
+      atomicAdd(&CI[bq], 1u);
+      if (bq < NB) {
+        const u64 q = mass_of(cd.c[j], m);
+        if (q) atomicAdd(&MI[bq], q);
+      }
+    }
+  }
+  __syncthreads();
+  // inclusive prefixes in place: CI over buckets 0..NB, MI over 0..NB-1
+  // (MI[NB] = MI[NB-1]: the last bucket holds mass 0)
+  {
+    const int t = threadIdx.x;
+    const unsigned cc = CI[t];
+    const u64 cm = MI[t];
+    const unsigned tailc = (t == BT - 1) ? CI[NB] : 0u;
+    unsigned ci = wave_incl_scan(cc);
+    u64 mi = wave_incl_scan(cm);
+    if (lane == 63) {
+      ts.red32[w] = ci;
+      ts.red64[w] = mi;
+    }
+    __syncthreads();
+    unsigned oc = 0;
+    u64 om = 0;
+    for (int v = 0; v < w; v++) {
+      oc += ts.red32[v];
+      om += ts.red64[v];
+    }
+    ci += oc;
+    mi += om;
+    CI[t] = ci;
+    MI[t] = mi;
+    if (t == BT - 1) {
+      CI[NB] = ci + tailc;
+      MI[NB] = mi;
+    }
+    __syncthreads();
+  }
+  auto cex = [&](int bq) -> unsigned { return bq ? CI[bq - 1] : 0u; };
+  auto mex = [&](int bq) -> u64 { return bq ? MI[bq - 1] : 0ull; };
+  // the bucket whose inclusive count (mass) first reaches target
+  auto find_count = [&](unsigned target, int slot) -> int {
+    const int t = threadIdx.x;
+    if (CI[t] >= target && (t == 0 || CI[t - 1] < target)) ts.sel[slot] = t;
+    if (t == 0 && CI[NB] >= target && CI[NB - 1] < target) ts.sel[slot] = NB;
+    __syncthreads();
+    return ts.sel[slot];
+  };
+  auto find_mass = [&](u64 target, int slot) -> int {
+    const int t = threadIdx.x;
+    if (MI[t] >= target && (t == 0 || MI[t - 1] < target)) ts.sel[slot] = t;
+    __syncthreads();
+    return ts.sel[slot];
+  };
+  // the ranked bucket (-1: none) and its size
+  int rb = -1;
+  unsigned rn = 0;
+  auto ensure_ranked = [&](int bq) -> bool {
+    if (rb == bq) return true;
+    const unsigned n = CI[bq] - cex(bq);
+    if (!rank_bucket(cd, bq, n, m, L, R, Q, ts)) return false;
+    rb = bq;
+    rn = n;
+    return true;
+  };
+  // element of bucket bq whose within-bucket inclusive prefix first reaches
+  // target (>= 1): its composite, the mass ahead of it in the bucket, its rank
+  auto resolve_mass = [&](int bq, u64 target, u64* before, unsigned* rank) -> u64 {
+    if (ensure_ranked(bq)) {
+      const int i = first_rank(Q, rn, target, ts);
+      *before = i > 0 ? Q[i - 1] : 0ull;
+      *rank = (unsigned)i;
+      return R[i];
+    }
+    auto en = [&](auto f) {
+#pragma unroll
+      for (int j = 0; j < CPT; j++)
+        if (cd.bk[j] == bq) f(cd.c[j], mass_of(cd.c[j], m));
+    };
+    return block_mass_select<BT>(en, target, bs, before, rank);
+  };
+  // the rr-th largest member of bucket bq (1-based) and the mass of the rr
+  // largest
+  auto resolve_count = [&](int bq, unsigned rr, u64* mass) -> u64 {
+    if (ensure_ranked(bq)) {
+      *mass = Q[rr - 1];
+      return R[rr - 1];
+    }
+    auto en = [&](auto f) {
+#pragma unroll
+      for (int j = 0; j < CPT; j++)
+        if (cd.bk[j] == bq) f(cd.c[j]);
+    };
+    const u64 T = block_select_kth<u64, 64, BT>(en, rr, bs);
+    u64 lo = ~0ull, ms = 0;
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+      if (cd.bk[j] == bq && cd.c[j] >= T) {
+        lo = cd.c[j] < lo ? cd.c[j] : lo;
+        ms += mass_of(cd.c[j], m);
+      }
+    lo = ~wave_max(~lo);
+    ms = wave_sum(ms);
+    if (lane == 0) {
+      ts.red64[w] = lo;
+      ts.red64b[w] = ms;
+    }
+    __syncthreads();
+    u64 x = ~0ull, s = 0;
+    for (int v = 0; v < WT; v++) {
+      x = ts.red64[v] < x ? ts.red64[v] : x;
+      s += ts.red64b[v];
+    }
+    __syncthreads();
+    *mass = s;
+    return x;
+  };
+
+  // top-k: the bucket of the k-th composite and the kept mass S
+  const unsigned nz = CI[NB];
+  const unsigned nk = (unsigned)k < nz ? (unsigned)k : nz;
+  const int bk = find_count(nk, 0);
+  const unsigned rr = nk - cex(bk);  // kept members of bucket bk (its largest)
+  const unsigned nbk = CI[bk] - cex(bk);
+  u64 S;
+  u64 lastc = 0;  // smallest kept composite, when known
+  if (bk == NB) {
+    S = MI[NB - 1];
+  } else if (rr == nbk) {
+    S = MI[bk];
+  } else {
+    u64 mb;
+    lastc = resolve_count(bk, rr, &mb);
+    S = mex(bk) + mb;
+  }
+  // top-p: the cut, the first element whose inclusive prefix reaches P
+  unsigned istar;
+  u64 Sp, cutc = 0;
+  if (r.top_p < 1.0f) {
+    const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
+    const u64 P = mul_shr24(S, pq);
+    if (P == 0) {
+      istar = 0;
+      cutc = M;
+      Sp = tg_q40(1.0f);
+    } else {
+      const int bp = find_mass(P, 1);
+      u64 before;
+      unsigned rank;
+      cutc = resolve_mass(bp, P - mex(bp), &before, &rank);
+      istar = cex(bp) + rank;
+      Sp = mex(bp) + before + mass_of(cutc, m);
+    }
+  } else {
+    istar = nk - 1;
+    Sp = S;
+    if (DIAG) {
+      if (lastc == 0) {
+        u64 mb;
+        lastc = resolve_count(bk, rr, &mb);
+      }
+      cutc = lastc;
+    }
+  }
+  // the draw: the first element whose inclusive prefix exceeds t
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
+  const u64 t = mul_shr24(Sp, uq);
+  const int bt = find_mass(t + 1, 2);
+  u64 before;
+  unsigned rank;
+  const u64 pick = resolve_mass(bt, t + 1 - mex(bt), &before, &rank);
+  if (threadIdx.x == 0) {
+    a.out[b] = comp_id(pick);
+    write_row_diag(a, b, (int)nk, (int)istar + 1, S, Sp, comp_id(cutc));
+  }
+  if (a.dbg.kept_ids || a.dbg.kept_probs) {
+    // the kept set in order (diagnostics only): the exact k-th composite,
+    // the composites at or above it, a bitonic sort
+    u64 Tk = 1;
+    if (nz > (unsigned)k)
+      Tk = block_select_kth<u64, 64, BT>(
+          [&](auto f) {
+#pragma unroll
+            for (int j = 0; j < CPT; j++)
+              if (cd.c[j]) f(cd.c[j]);
+          },
+          (unsigned)k, bs);
+    if (threadIdx.x == 0) ts.nc = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+      if (cd.c[j] && cd.c[j] >= Tk) cand[atomicAdd(&ts.nc, 1u)] = cd.c[j];
+    __syncthreads();
+    u64 x = (int)threadIdx.x < (int)nk ? cand[threadIdx.x] : 0ull;
+    __syncthreads();
+    x = block_sort_desc(x, cand);
+    cand[threadIdx.x] = x;
+    __syncthreads();
+    if (a.dbg.kept_ids) {
+      int32_t* kid = a.dbg.kept_ids + (long long)b * a.dbg.kept_cap;
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT) kid[i] = i < (int)nk ? comp_id(cand[i]) : -1;
+    }
+    if (a.dbg.kept_probs) {
+      float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
+      const float fs = tg_u64_to_f32(Sp);
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT)
+        kp[i] = i <= (int)istar ? tg_u64_to_f32(mass_of(cand[i], m)) / fs : 0.0f;
+    }
+  }
+}
+
 template <typename Tin, int NVR, bool MASK>
 __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned char* smem, Scratch& ts,
                                          BlockScratch& bs) {
   using RG = Regs<Tin, NVR>;
   constexpr int EPV = RG::EPV;
+  constexpr int NEL = NVR * EPV;       // ids per thread
+  constexpr int NW = (NEL + 31) / 32;  // candidate mask words per thread
   const int b = r.b;
   const int V = a.V;
   const int bw = a.TS > 0 ? (V + 31) / 32 : 0;
   uint32_t* hbits = (uint32_t*)smem;
   int2* hash = (int2*)(smem + ((bw * 4 + 15) / 16) * 16);
-  u64* cand = (u64*)((unsigned char*)hash + (size_t)a.TS * 8);  // CAPK (+ pad)
-  u64* K = cand + CAPK + 2;                                      // KMAX (+ pad)
-  u64* R = K + KMAX + 2;                                         // KMAX
-  u64* C = R + KMAX;                                             // KMAX
+  u64* cand = (u64*)((unsigned char*)hash + (size_t)a.TS * 8);  // CAPK
+  u64* L = cand + CAPK;                                           // LCAP (+ pad)
+  u64* R = L + LCAP + 2;                                          // LCAP
+  u64* Q = R + LCAP;                                              // LCAP
+  unsigned* CI = (unsigned*)(Q + LCAP);                           // NB + 1 (+ pad)
+  u64* MI = (u64*)(CI + NB + 4);                                  // NB + 1
+  uint32_t* cid = (uint32_t*)L;                                   // CAPK ids, over L and R
   const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
   const int k = r.mode == 0 ? 1 : r.k;
 
@@ -255,112 +665,142 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
     for (int i = threadIdx.x; i < a.TS; i += BT) c += hash[i].x != -1;
     nh = bsum(c, ts.red32);
   }
-  const bool mask = MASK && r.mrow != nullptr;
+  if (MASK && r.mrow != nullptr) g.apply_mask(r, V);
 
-  // bound: the two largest x of this thread
-  float a1 = -__builtin_inff(), a2 = -__builtin_inff();
-#pragma unroll
-  for (int j = 0; j < NVR; j++) {
-    const uint32_t mw = MASK && mask ? RG::mword(r, V, j) : 0xFFFFFFFFu;
-#pragma unroll
-    for (int e = 0; e < EPV; e++) {
-      const float x = g.template xval<MASK>(j, e, mw);
-      a2 = fmaxf(a2, fminf(a1, x));
-      a1 = fmaxf(a1, x);
-    }
-  }
-  g.fence();
-  const unsigned kp = (unsigned)k + nh;
-  // (kp <= 2 * BT: the dispatch keeps top_k <= KMAX and the history to
-  // at most KMAX ids)
-  const uint32_t tkey = block_select_kth<uint32_t, 32, BT>(
-      [&](auto f) {
-        f(tg_key(a1));
-        f(tg_key(a2));
-      },
-      kp, bs);
+  // bound
+  float s[4];
+  slot_values<Tin, NVR>(g, s);
+  const unsigned kp = (unsigned)k + nh;  // <= 2 * KMAX (top_k and history capped at KMAX)
+  const uint32_t tkey = bound_key16(s, kp, ts, bs) << 16;
   // raw-logit bound, 16 representable values lower: a raw logit below it
   // scales (x / T, correctly rounded and monotone) strictly below the
   // scaled bound, also across a binade edge
   const uint32_t kneg = 0x007FFFFFu;  // key of -inf
   const float thz = tkey > kneg + 16u ? tg_unkey(tkey - 16u) : -__builtin_inff();
-
-  // collect: every non-history id at or above the bound (counted, placed by
-  // a wave scan, written), then every history id with its penalised logit
   const float thf = fmaxf(thz, -3.40282347e38f);  // -inf never qualifies
-  unsigned cnt = 0;
+
+  // collect: one bit per id at or above the bound (element el = j * EPV + e
+  // of this thread is bit 31 - (el & 31) of word el >> 5)
+  uint32_t mb[NW];
+  if constexpr (sizeof(Tin) == 2) {
+    // bf16 x >= thf exactly on the 16-bit patterns: for thf > 0 a signed
+    // compare with ceil(thf bits / 2^16); otherwise (sign set, or +0) an
+    // unsigned compare with the truncated pattern (every non-negative
+    // pattern lies below it)
+    const uint32_t tb = tg_f2u(thf);
+    const bool pos = !(tb >> 31) && tb != 0u;
+    const int ts16 = (int)((tb + 0xFFFFu) >> 16);
+    const uint32_t tu16 = tb == 0u ? 0x8000u : (tb >> 16);
 #pragma unroll
-  for (int j = 0; j < NVR; j++) {
-    const uint32_t mw = MASK && mask ? RG::mword(r, V, j) : 0xFFFFFFFFu;
+    for (int i = 0; i < NW; i++) {
+      uint32_t acc = 0;
+      if (pos) {
 #pragma unroll
-    for (int e = 0; e < EPV; e++) {
-      const float x = g.template xval<MASK>(j, e, mw);
-      if (x >= thf && !(r.use_pen && hist_bit(hbits, RG::vec_id(j) + e))) cnt++;
+        for (int t = 0; t < 16; t++) {
+          const int wi = i * 16 + t;
+          const uint32_t x = word_of(g.raw[wi >> 2], wi & 3);
+          acc = acc * 2u + (uint32_t)((int)(short)(x & 0xFFFFu) >= ts16);
+          acc = acc * 2u + (uint32_t)(((int)x >> 16) >= ts16);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+          const int wi = i * 16 + t;
+          const uint32_t x = word_of(g.raw[wi >> 2], wi & 3);
+          acc = acc * 2u + (uint32_t)((x & 0xFFFFu) <= tu16);
+          acc = acc * 2u + (uint32_t)((x >> 16) <= tu16);
+        }
+      }
+      mb[i] = acc;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int t = 0; t < 32; t++) {
+        const int el = i * 32 + t;
+        if (el < NEL) {
+          const int j = el / EPV, e = el % EPV;
+          acc = acc * 2u + (uint32_t)(tg_u2f(word_of(g.raw[j], e)) >= thf);
+        }
+      }
+      constexpr int last = NEL - (NW - 1) * 32;  // elements in the last word
+      mb[i] = (i == NW - 1 && last < 32) ? acc << (32 - last) : acc;
     }
   }
-  g.fence();
-  if (threadIdx.x == 0) ts.nc = 0;
+  unsigned cnt = 0;
+#pragma unroll
+  for (int i = 0; i < NW; i++) cnt += __builtin_popcount(mb[i]);
+  if (threadIdx.x == 0) {
+    ts.nc = 0;
+    ts.ng = 0;
+  }
+  for (int i = threadIdx.x; i < NB + 1; i += BT) {
+    CI[i] = 0u;
+    MI[i] = 0ull;
+  }
   __syncthreads();
-  const unsigned wincl = wave_incl_scan(cnt);
-  unsigned wbase = 0;
-  if (lane_id() == 63 && wincl) wbase = atomicAdd(&ts.nc, wincl);
-  wbase = __shfl(wbase, 63, 64);
-  unsigned slot = wbase + wincl - cnt;
-  if (cnt) {
+  {
+    const unsigned wincl = wave_incl_scan(cnt);
+    unsigned wbase = 0;
+    if (lane_id() == 63 && wincl) wbase = atomicAdd(&ts.nc, wincl);
+    wbase = __shfl(wbase, 63, 64);
+    unsigned slot = wbase + wincl - cnt;
 #pragma unroll
-    for (int j = 0; j < NVR; j++) {
-      const uint32_t mw = MASK && mask ? RG::mword(r, V, j) : 0xFFFFFFFFu;
+    for (int i = 0; i < NW; i++) {
+      uint32_t mw = mb[i];
+      while (mw) {
+        const int q = __builtin_clz(mw);
+        mw ^= 0x80000000u >> q;
+        const int el = i * 32 + q;
+        if (slot < (unsigned)CAPK) cid[slot] = (uint32_t)(RG::vec_id(el / EPV) + el % EPV);
+        slot++;
+      }
+    }
+  }
+  __syncthreads();
+  const unsigned ncb = ts.nc;  // ids at or above the bound
+  if (ncb <= (unsigned)CAPK) {
+    // their composites (history ids skipped: added below with their
+    // penalised logits), read again from memory
+    uint32_t id[CPT];
+    float x[CPT];
 #pragma unroll
-      for (int e = 0; e < EPV; e++) {
-        const float x = g.template xval<MASK>(j, e, mw);
-        const int id = RG::vec_id(j) + e;
-        if (x >= thf && !(r.use_pen && hist_bit(hbits, id))) {
-          if (slot < (unsigned)CAPK) cand[slot] = comp_of(x, true, r.invT, id);
-          slot++;  // a composite 0 (scaled to -inf) drops out below
+    for (int j = 0; j < CPT; j++) {
+      const int i = threadIdx.x + j * BT;
+      id[j] = i < (int)ncb ? cid[i] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; j++) x[j] = Elem<Tin>::scalar(rowp, id[j]);
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+      const int i = threadIdx.x + j * BT;
+      if (i < (int)ncb) {
+        const bool hist = r.use_pen && hist_bit(hbits, (int)id[j]);
+        cand[i] = hist ? 0ull : comp_of(x[j], true, r.invT, (int)id[j]);
+      }
+    }
+    if (r.use_pen) {
+      for (int i = threadIdx.x; i < a.TS; i += BT) {
+        const int2 h = hash[i];
+        if (h.x == -1) continue;
+        const int hid = h.x;
+        const float z = penalise(Elem<Tin>::scalar(rowp, hid), h.y, r);
+        const u64 c = comp_of(z, mask_allows(r, hid), r.invT, hid);
+        if (c) {
+          const unsigned sl = ncb + atomicAdd(&ts.ng, 1u);
+          if (sl < (unsigned)CAPK) cand[sl] = c;
         }
       }
     }
   }
-  if (r.use_pen) {
-    for (int i = threadIdx.x; i < a.TS; i += BT) {
-      const int2 h = hash[i];
-      if (h.x == -1) continue;
-      const int id = h.x;
-      const float z = penalise(Elem<Tin>::scalar(rowp, id), h.y, r);
-      const u64 c = comp_of(z, mask_allows(r, id), r.invT, id);
-      if (c) {
-        const unsigned sl = atomicAdd(&ts.nc, 1u);
-        if (sl < (unsigned)CAPK) cand[sl] = c;
-      }
-    }
-  }
   __syncthreads();
-  const int nc = (int)ts.nc;
-  int nk;
-  if (nc <= CAPK) {
-    // exact k-th composite of the candidates, then exactly those >= it
-    int nz = 0;
-    for (int i = threadIdx.x; i < nc; i += BT) nz += cand[i] != 0ull;
-    nz = (int)bsum((unsigned)nz, ts.red32);
-    u64 T = 1;
-    if (nz > k)
-      T = block_select_kth<u64, 64, BT>(
-          [&](auto f) {
-            for (int i = threadIdx.x; i < nc; i += BT)
-              if (cand[i]) f(cand[i]);
-          },
-          (unsigned)k, bs);
-    if (threadIdx.x == 0) ts.nc = 0;
-    __syncthreads();
-    for (int i = threadIdx.x; i < nc; i += BT) {
-      const u64 c = cand[i];
-      if (c && c >= T) K[atomicAdd(&ts.nc, 1u)] = c;
-    }
-    __syncthreads();
-    nk = (int)ts.nc;
-  } else {
+  int nc = (int)(ts.nc + ts.ng);  // ts.ng is cleared in the tail, past its first barrier
+  if (nc > CAPK) {
     // candidate overflow: radix selection over every id of the row, read
-    // again from L2 (rare: massive ties at the bound)
+    // again from L2 / MALL (rare: massive ties at the bound); the kept set
+    // becomes the candidate list
     auto en = [&](auto f) {
       const int nvec = (V + EPV - 1) / EPV;
 #pragma unroll 1
@@ -385,10 +825,10 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
     if (threadIdx.x == 0) ts.nc = 0;
     __syncthreads();
     en([&](u64 c) {
-      if (c >= T) K[atomicAdd(&ts.nc, 1u)] = c;
+      if (c >= T) cand[atomicAdd(&ts.nc, 1u)] = c;  // at most k (distinct composites)
     });
     __syncthreads();
-    nk = (int)ts.nc;
+    nc = (int)ts.nc;
   }
   if (a.dbg.post_logits) {
     float* post = a.dbg.post_logits + (long long)b * V;
@@ -407,31 +847,8 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
       }
     }
   }
-  if (nk == 0) {
-    if (r.mode == 0) {
-      finish_greedy(a, b, 0ull);
-    } else {
-      if (threadIdx.x == 0) {
-        a.out[b] = -1;
-        write_row_diag(a, b, 0, 0, 0, 0, -1);
-      }
-      if (a.dbg.kept_ids)
-        for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT) a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = -1;
-      if (a.dbg.kept_probs)
-        for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT) a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = 0.0f;
-    }
-    return;
-  }
-  {
-    // the kept set in order: a bitonic sort of one entry per thread (0 pads last)
-    u64 xs[1] = {(int)threadIdx.x < nk ? K[threadIdx.x] : 0ull};
-    __syncthreads();
-    block_sort_desc<1>(xs, K);
-    if ((int)threadIdx.x < nk) R[threadIdx.x] = xs[0];
-    __syncthreads();
-  }
-  if (r.mode == 0) finish_greedy(a, b, R[0]);
-  else finish(a, r, R, C, nk, ts);
+  if (a.dbg.cut_ids) tail<true>(a, r, nc, cand, L, R, Q, CI, MI, ts, bs);
+  else tail<false>(a, r, nc, cand, L, R, Q, CI, MI, ts, bs);
 }
 
 template <typename Tin, int NVR, bool MASK>
@@ -481,7 +898,8 @@ int topk_max_vocab(int dtype) { return topk::BT * 20 * (dtype == 1 ? 8 : 4); }
 
 size_t topk_lds_bytes(int V, int TS) {
   const int bw = TS > 0 ? (V + 31) / 32 : 0;
-  return (size_t)((bw * 4 + 15) / 16) * 16 + (size_t)TS * 8 + (size_t)(TOPK_CAP + 2 + 3 * KMAX + 2) * 8;
+  return (size_t)((bw * 4 + 15) / 16) * 16 + (size_t)TS * 8 + (size_t)(TOPK_CAP + 3 * topk::LCAP + 2) * 8 +
+         (size_t)(topk::NB + 4) * 4 + (size_t)(topk::NB + 1) * 8;
 }
 
 hipError_t launch_topk(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
