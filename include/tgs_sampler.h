@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define TGS_ABI_VERSION 1
+#define TGS_ABI_VERSION 2
 
 struct ihipStream_t;
 typedef struct ihipStream_t* tgs_stream;
@@ -105,10 +105,14 @@ typedef struct {
  * 1024 < top_k < V and the top-p kernel for rows without a top-k.  The hint
  * is a promise: a sampling row whose top_k exceeds max_top_k (a row without
  * a usable top-k counts as V) gets id -3.  Greedy rows are served under any
- * hint. */
+ * hint.  min_top_k == V (every sampling row without a usable top-k, as in
+ * grammar-constrained top-p decoding) lets the top-p kernel serve the whole
+ * batch, its greedy rows included, in one launch. */
 typedef struct {
   int32_t max_top_k; /* max over sampling rows of top_k when 1 <= top_k < V, else V;
                         0 when every row is greedy */
+  int32_t min_top_k; /* min over sampling rows of the same; V when every row is greedy.
+                        0 (unknown) is always safe */
 } tgs_batch_hint;
 
 /* Library / status helpers (no device work). */

@@ -34,10 +34,10 @@ int main(int argc, char** argv) {
   FILE* m = std::fopen((dir + "/meta.txt").c_str(), "r");
   if (!m) return 3;
   if (mode == "sample") {
-    int B, V, dtype, hist_cap, has_len, n_states, hint, kept_cap, post;
+    int B, V, dtype, hist_cap, has_len, n_states, hint, kept_cap, post, hint_min;
     long long stride;
-    if (std::fscanf(m, "%d %d %lld %d %d %d %d %d %d %d", &B, &V, &stride, &dtype, &hist_cap, &has_len,
-                    &n_states, &hint, &kept_cap, &post) != 10)
+    if (std::fscanf(m, "%d %d %lld %d %d %d %d %d %d %d %d", &B, &V, &stride, &dtype, &hist_cap, &has_len,
+                    &n_states, &hint, &kept_cap, &post, &hint_min) != 11)
       return 4;
     std::fclose(m);
     auto logits = slurp(dir + "/logits.bin");
@@ -58,7 +58,7 @@ int main(int argc, char** argv) {
     std::vector<uint64_t> mass(2 * (size_t)B);
     tgs_debug dbg = {kid.data(), kpr.data(), kept_cap, counts.data(), mass.data(), cut.data(),
                      post ? postv.data() : nullptr};
-    tgs_batch_hint hb = {hint};
+    tgs_batch_hint hb = {hint, hint_min};
     rc = tgs_sample(h, logits.data(), (tgs_dtype)dtype, B, V, stride, hist_cap ? (const int32_t*)hist.data() : nullptr,
                     has_len ? (const int32_t*)hlen.data() : nullptr, hist_cap, (const tgs_row_params*)params.data(),
                     (const float*)u.data(), out.data(), hint >= 0 ? &hb : nullptr, &dbg, nullptr);

@@ -39,7 +39,8 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
             np.ascontiguousarray(mask_table, np.uint32).tofile(os.path.join(d, "mask.bin"))
         with open(os.path.join(d, "meta.txt"), "w") as f:
             f.write(f"{B} {V} {logits.shape[1]} {dtype} {hist_cap} {int(hist_len is not None)} {n_states} "
-                    f"{-1 if hint is None else int(hint)} {kept_cap} {int(bool(post))}\n")
+                    f"{-1 if hint is None else int(hint)} {kept_cap} {int(bool(post))} "
+                    f"{int(getattr(hint, 'min_top_k', 0))}\n")
         env = dict(os.environ)
         if split is not None:
             env["TGS_SPLIT"] = str(split)

@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.tgs_abi_version() == 1
+    assert lib.tgs_abi_version() == 2
     assert lib.tgs_status_string(0) == b"ok"
     assert b"invalid" in lib.tgs_status_string(-1)
     assert lib.tgs_status_string(12345) == b"unknown status"
@@ -67,13 +67,19 @@ def test_hint_from_params(lib):
 
     V = 1000
     p = tg.make_params(4, temperature=[0.0, 0.7, 1.0, 0.5], top_k=[0, 50, 7, 3])
-    assert tg.batch_hint(p, V) == 50
+    h = tg.batch_hint(p, V)
+    assert h == 50 and h.min_top_k == 3
     p["top_k"][3] = 0  # top-k disabled on a sampling row: the full row
-    assert tg.batch_hint(p, V) == V
+    h = tg.batch_hint(p, V)
+    assert h == V and h.min_top_k == 7
     p["top_k"][3] = V + 3
     assert tg.batch_hint(p, V) == V
+    p["top_k"][1:] = [0, V, -1]  # no sampling row with a usable top-k
+    h = tg.batch_hint(p, V)
+    assert h == V and h.min_top_k == V
     p = tg.make_params(3, temperature=0.0, top_k=0)
-    assert tg.batch_hint(p, V) == 0  # all greedy
+    h = tg.batch_hint(p, V)
+    assert h == 0 and h.min_top_k == V  # all greedy
     p = tg.make_params(2, temperature=[np.nan, 0.9], top_k=[5, 9], flags=[0, 1])
     assert tg.batch_hint(p, V) == 0  # NaN rows are invalid, flagged rows greedy
 

@@ -250,6 +250,46 @@ def test_topp_kernel_bucket_overflow(sim, oracle):
     _check(sim, oracle, x, params, u, None, None)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_topp_kernel_serves_whole_batch(sim, oracle, bf16):
+    """Every sampling row without a usable top-k (the hint's min_top_k == V):
+    one top-p launch serves the greedy rows too.  Masked rows, an all-masked
+    row, an invalid row, quantized logits (buckets past one wave) and top-p
+    off are mixed in."""
+    import tinygpt_amd as tg
+
+    B, V = 9, 2048
+    g = np.random.default_rng(61)
+    x = g.normal(0.0, 2.5, (B, V)).astype(np.float32)
+    x[3] = np.round(x[3] * 2.0) / 2.0
+    x[4] = np.round(x[4])
+    words = V // 32
+    mask = g.integers(0, 1 << 32, size=(3, words), dtype=np.uint64).astype(np.uint32)
+    mask[1] = 0
+    params = oracle.make_params(B, temperature=1.0, top_k=0, top_p=0.95,
+                                mask_state=[0, -1, 2, -1, -1, 1, 0, -1, 2])
+    params["temperature"][[0, 2, 6]] = 0.0  # greedy
+    params["temperature"][7] = np.nan  # invalid: -2
+    params["top_p"][4] = 1.0
+    params["top_k"][8] = V + 5
+    u = g.random(B).astype(np.float32)
+    if bf16:
+        from tinygpt_amd import workloads as W
+
+        x = W.f32_to_bf16_bits(x)
+    hint = tg.batch_hint(params, V)
+    assert hint == V and hint.min_top_k == V
+    r, _, _ = _check(sim, oracle, x, params, u, None, None, mask=mask, hint=hint)
+    assert r["launches"] == [(B, 1024)]  # the top-p kernel alone
+    # a row with a usable top-k breaks the hint's promise: -3
+    params["top_k"][1] = 5
+    r = sim.run_sample(x, params, u, mask_table=mask, hint=hint, post=False)
+    o = oracle.sample_batch(x, params, u, mask_table=mask)
+    expect = o["ids"].copy()
+    expect[1] = -3
+    np.testing.assert_array_equal(r["ids"], expect)
+
+
 def _topk_batch(seed, B, V, oracle, bf16=False):
     x, params, u, hist, hist_len = _batch(seed, B, V, oracle)
     g = np.random.default_rng(seed)

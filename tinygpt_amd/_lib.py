@@ -69,7 +69,7 @@ class TgsDebug(C.Structure):
 
 
 class TgsHint(C.Structure):
-    _fields_ = [("max_top_k", C.c_int32)]
+    _fields_ = [("max_top_k", C.c_int32), ("min_top_k", C.c_int32)]
 
 
 class TgsError(RuntimeError):

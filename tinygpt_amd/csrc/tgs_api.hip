@@ -147,15 +147,17 @@ const char* tgs_status_string(int status) {
 
 int tgs_hint_from_params(const tgs_row_params* p, int B, int V, tgs_batch_hint* out) {
   if (!out || B < 0 || V < 1 || (B > 0 && !p)) return TGS_EINVAL;
-  int mk = 0;
+  int mk = 0, mn = V;
   for (int b = 0; b < B; b++) {
     const float T = p[b].temperature;
     const bool greedy = (p[b].flags & TGS_FLAG_GREEDY) || !(T > 0.0f);
     if (greedy) continue;
     const int k = (p[b].top_k >= 1 && p[b].top_k < V) ? p[b].top_k : V;
     mk = std::max(mk, k);
+    mn = std::min(mn, k);
   }
   out->max_top_k = mk;
+  out->min_top_k = mn;
   return TGS_OK;
 }
 
@@ -348,6 +350,18 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
     a.S = 1;
     a.L = V;
     hipError_t e = tgs::launch_topk(a, dt, tgs::topk_lds_bytes(V, a.TS), (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
+    return TGS_OK;
+  }
+  const int mink = hint ? hint->min_top_k : 0;
+  if (mk >= V && mink >= V && tgs::topp_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) <= h->lds_limit) {
+    // every sampling row without a usable top-k: the top-p kernel serves the
+    // batch alone, greedy rows included (one workgroup per row)
+    a.full_rows = 1;
+    a.topp_all = 1;
+    a.S = 1;
+    a.L = V;
+    hipError_t e = tgs::launch_topp(a, dt, tgs::topp_lds_bytes(V, a.TS), (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
     return TGS_OK;
   }

@@ -23,7 +23,7 @@ constexpr int K64_CNT_STRIDE = 32;
 // Top-p kernel (rows without a top-k): threads per workgroup and the most
 // ids of one histogram bucket ranked in LDS.
 constexpr int TOPP_NT = 1024;
-constexpr int TOPP_CAP = 2048;
+constexpr int TOPP_CAP = 1024;
 
 // Top-k kernel (1 <= top_k <= KMAX, the row held in registers): threads per
 // workgroup and candidate capacity.
@@ -56,6 +56,7 @@ struct SampleArgs {
   unsigned long long* lists;  // fused kernel: [B * S][64] chunk lists (all ~0 between calls)
   int full_rows;         // 1: full_kernel runs after the chunk kernels
   int hint_k;            // the launch hint's max_top_k (INT_MAX without a hint)
+  int topp_all;          // 1: the top-p kernel alone serves the batch (its greedy rows too)
   tgs_debug dbg;
 };
 

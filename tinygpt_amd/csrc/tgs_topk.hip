@@ -37,6 +37,7 @@
 // back to a radix selection over all ids of the row, read again from
 // L2 / MALL; a bucket beyond the ranking capacity to radix selections
 // restricted to it.
+#include "tgs_bucket.h"
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 #include "tgs_row.h"
@@ -48,14 +49,10 @@ constexpr int BT = TOPK_NT;    // threads per workgroup
 constexpr int WT = BT / 64;    // waves
 constexpr int CAPK = TOPK_CAP; // candidates
 constexpr int CPT = CAPK / BT; // candidates per thread in the tail
-constexpr int NB = 1024;       // mass buckets of width 1/32 below the maximum (+1 for mass 0)
+constexpr int NB = bucket::NB; // mass buckets below the maximum (+1 for mass 0)
 constexpr int LCAP = KMAX;     // ids of one bucket ranked in LDS
 static_assert(NB == BT, "one bucket per thread in the prefix");
 static_assert(2 * LCAP * 8 >= CAPK * 4, "candidate ids alias the ranking lists");
-
-struct alignas(16) u64x2 {
-  u64 x, y;
-};
 
 struct Scratch {
   u64 red64[WT];
@@ -246,21 +243,6 @@ __device__ __forceinline__ uint32_t bound_key16(const float (&s)[4], unsigned kp
       need, bs);
 }
 
-// Bucket of a candidate's y below the maximum m: 0 at y == m, NB for
-// y - m <= -32 (mass 0), else floor((m - y) * 32).
-__device__ __forceinline__ int bucket_of(float y, float m) {
-  if (y == m) return 0;
-  const float x = y - m;
-  if (!(x > -32.0f)) return NB;
-  return (int)(-x * 32.0f);
-}
-
-// Exact mass of a composite under the maximum m: floor(exp(y - m) 2^40).
-__device__ __forceinline__ u64 mass_of(u64 c, float m) {
-  const float y = comp_y(c);
-  return tg_q40(y == m ? 1.0f : tg_expf_nonpos(y - m));
-}
-
 __device__ __forceinline__ void finish_greedy(const SampleArgs& a, int b, u64 best) {
   const int id = best ? comp_id(best) : -1;
   if (threadIdx.x == 0) {
@@ -308,9 +290,9 @@ struct Cands {
   int bk[CPT];  // -1: no candidate
 };
 
-// Ranks the members of bucket bq (n of them, n uniform): R[0, n) their
-// composites descending, Q[0, n) the inclusive mass prefix.  Returns false
-// (nothing ranked) when n > LCAP.  ts.ng is 0 on entry and on return.
+// Ranks the members of bucket bq (n of them, n uniform) into R / Q (see
+// bucket::rank_list).  Returns false (nothing ranked) when n > LCAP.
+// ts.ng is 0 on entry and on return.
 __device__ __forceinline__ bool rank_bucket(const Cands& cd, int bq, unsigned n, float m, u64* L, u64* R, u64* Q,
                                             Scratch& ts) {
   if (n > (unsigned)LCAP) return false;
@@ -319,58 +301,9 @@ __device__ __forceinline__ bool rank_bucket(const Cands& cd, int bq, unsigned n,
   for (int j = 0; j < CPT; j++)
     if (cd.bk[j] == bq) L[atomicAdd(&ts.ng, 1u)] = cd.c[j];
   __syncthreads();
-  const int w = threadIdx.x >> 6, lane = lane_id();
-  if (n <= 64) {
-    if (w == 0) {
-      u64 x = lane < (int)n ? L[lane] : 0ull;
-      x = wave_sort_desc(x);
-      const u64 q = lane < (int)n ? mass_of(x, m) : 0ull;
-      const u64 ci = wave_incl_scan(q);
-      if (lane < (int)n) {
-        R[lane] = x;
-        Q[lane] = ci;
-      }
-      if (lane == 0) ts.ng = 0;
-    }
-    __syncthreads();
-    return true;
-  }
-  // rank = number of larger composites (composites are distinct), counted by
-  // the waves that hold members, two entries per 16-byte broadcast read
-  const int i = threadIdx.x;
-  if (w * 64 < (int)n) {
-    const u64 x = i < (int)n ? L[i] : ~0ull;
-    int rk = 0;
-    const int np = ((int)n + 1) / 2;
-    const u64x2* L2 = (const u64x2*)L;
-#pragma unroll 4
-    for (int p = 0; p < np; p++) {
-      const u64x2 e = L2[p];
-      rk += (e.x > x) + (e.y > x);
-    }
-    if (i < (int)n) R[rk] = x;
-  }
-  __syncthreads();
-  const u64 q = i < (int)n ? mass_of(R[i], m) : 0ull;
-  const u64 wi = wave_incl_scan(q);
-  if (lane == 63) ts.red64b[w] = wi;
-  if (i == 0) ts.ng = 0;
-  __syncthreads();
-  u64 off = 0;
-  for (int v = 0; v < w; v++) off += ts.red64b[v];
-  if (i < (int)n) Q[i] = off + wi;
-  __syncthreads();
+  if (threadIdx.x == 0) ts.ng = 0;  // read again only after rank_list's barriers
+  bucket::rank_list<BT>(L, n, m, R, Q, ts.red64b);
   return true;
-}
-
-// First rank of a ranked bucket whose inclusive prefix reaches target (>= 1).
-__device__ __forceinline__ int first_rank(const u64* Q, unsigned n, u64 target, Scratch& ts) {
-  const int i = threadIdx.x;
-  if (i < (int)n && Q[i] >= target && (i == 0 || Q[i - 1] < target)) ts.first = i;
-  __syncthreads();
-  const int f = ts.first;
-  __syncthreads();
-  return f;
 }
 
 // The row's tail over nc candidates in cand[] (composites, 0 = none).
@@ -417,62 +350,22 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
   for (int j = 0; j < CPT; j++) {
     cd.bk[j] = -1;
     if (cd.c[j]) {
-      const int bq = bucket_of(comp_y(cd.c[j]), m);
+      const int bq = bucket::of(comp_y(cd.c[j]), m);
       cd.bk[j] = bq;
       atomicAdd(&CI[bq], 1u);
       if (bq < NB) {
-        const u64 q = mass_of(cd.c[j], m);
+        const u64 q = bucket::mass_c(cd.c[j], m);
         if (q) atomicAdd(&MI[bq], q);
       }
     }
   }
   __syncthreads();
-  // inclusive prefixes in place: CI over buckets 0..NB, MI over 0..NB-1
-  // (MI[NB] = MI[NB-1]: the last bucket holds mass 0)
-  {
-    const int t = threadIdx.x;
-    const unsigned cc = CI[t];
-    const u64 cm = MI[t];
-    const unsigned tailc = (t == BT - 1) ? CI[NB] : 0u;
-    unsigned ci = wave_incl_scan(cc);
-    u64 mi = wave_incl_scan(cm);
-    if (lane == 63) {
-      ts.red32[w] = ci;
-      ts.red64[w] = mi;
-    }
-    __syncthreads();
-    unsigned oc = 0;
-    u64 om = 0;
-    for (int v = 0; v < w; v++) {
-      oc += ts.red32[v];
-      om += ts.red64[v];
-    }
-    ci += oc;
-    mi += om;
-    CI[t] = ci;
-    MI[t] = mi;
-    if (t == BT - 1) {
-      CI[NB] = ci + tailc;
-      MI[NB] = mi;
-    }
-    __syncthreads();
-  }
+  bucket::prefix<BT>(CI, MI, ts.red32, ts.red64);
   auto cex = [&](int bq) -> unsigned { return bq ? CI[bq - 1] : 0u; };
   auto mex = [&](int bq) -> u64 { return bq ? MI[bq - 1] : 0ull; };
   // the bucket whose inclusive count (mass) first reaches target
-  auto find_count = [&](unsigned target, int slot) -> int {
-    const int t = threadIdx.x;
-    if (CI[t] >= target && (t == 0 || CI[t - 1] < target)) ts.sel[slot] = t;
-    if (t == 0 && CI[NB] >= target && CI[NB - 1] < target) ts.sel[slot] = NB;
-    __syncthreads();
-    return ts.sel[slot];
-  };
-  auto find_mass = [&](u64 target, int slot) -> int {
-    const int t = threadIdx.x;
-    if (MI[t] >= target && (t == 0 || MI[t - 1] < target)) ts.sel[slot] = t;
-    __syncthreads();
-    return ts.sel[slot];
-  };
+  auto find_count = [&](unsigned target, int slot) -> int { return bucket::find_count<BT>(CI, target, &ts.sel[slot]); };
+  auto find_mass = [&](u64 target, int slot) -> int { return bucket::find_mass<BT>(MI, target, &ts.sel[slot]); };
   // the ranked bucket (-1: none) and its size
   int rb = -1;
   unsigned rn = 0;
@@ -488,7 +381,7 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
   // target (>= 1): its composite, the mass ahead of it in the bucket, its rank
   auto resolve_mass = [&](int bq, u64 target, u64* before, unsigned* rank) -> u64 {
     if (ensure_ranked(bq)) {
-      const int i = first_rank(Q, rn, target, ts);
+      const int i = bucket::first_rank<BT>(Q, rn, target, &ts.first);
       *before = i > 0 ? Q[i - 1] : 0ull;
       *rank = (unsigned)i;
       return R[i];
@@ -496,7 +389,7 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
     auto en = [&](auto f) {
 #pragma unroll
       for (int j = 0; j < CPT; j++)
-        if (cd.bk[j] == bq) f(cd.c[j], mass_of(cd.c[j], m));
+        if (cd.bk[j] == bq) f(cd.c[j], bucket::mass_c(cd.c[j], m));
     };
     return block_mass_select<BT>(en, target, bs, before, rank);
   };
@@ -518,7 +411,7 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
     for (int j = 0; j < CPT; j++)
       if (cd.bk[j] == bq && cd.c[j] >= T) {
         lo = cd.c[j] < lo ? cd.c[j] : lo;
-        ms += mass_of(cd.c[j], m);
+        ms += bucket::mass_c(cd.c[j], m);
       }
     lo = ~wave_max(~lo);
     ms = wave_sum(ms);
@@ -570,7 +463,7 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
       unsigned rank;
       cutc = resolve_mass(bp, P - mex(bp), &before, &rank);
       istar = cex(bp) + rank;
-      Sp = mex(bp) + before + mass_of(cutc, m);
+      Sp = mex(bp) + before + bucket::mass_c(cutc, m);
     }
   } else {
     istar = nk - 1;
@@ -625,7 +518,7 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
       float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
       const float fs = tg_u64_to_f32(Sp);
       for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT)
-        kp[i] = i <= (int)istar ? tg_u64_to_f32(mass_of(cand[i], m)) / fs : 0.0f;
+        kp[i] = i <= (int)istar ? tg_u64_to_f32(bucket::mass_c(cand[i], m)) / fs : 0.0f;
     }
   }
 }

@@ -40,14 +40,24 @@ def make_params(n, temperature=1.0, top_k=0, top_p=1.0, repetition=1.0, presence
     return p
 
 
-def batch_hint(params: np.ndarray, vocab: int) -> int:
-    """max_top_k of tgs_batch_hint computed from host params (see the C helper)."""
+class BatchHint(int):
+    """A batch's max_top_k (an int) carrying its min_top_k too."""
+
+    def __new__(cls, max_top_k: int, min_top_k: int = 0):
+        obj = super().__new__(cls, max_top_k)
+        obj.min_top_k = int(min_top_k)
+        return obj
+
+
+def batch_hint(params: np.ndarray, vocab: int) -> BatchHint:
+    """tgs_batch_hint computed from host params (see the C helper): an int,
+    max_top_k, with the batch's min_top_k as an attribute."""
     p = np.ascontiguousarray(params, dtype=ROW_PARAMS_DTYPE)
     h = TgsHint()
     rc = _lib.load().tgs_hint_from_params(p.ctypes.data_as(C.c_void_p), p.size, vocab, C.byref(h))
     if rc != 0:
         raise TgsError(rc, "tgs_hint_from_params")
-    return int(h.max_top_k)
+    return BatchHint(h.max_top_k, h.min_top_k)
 
 
 def params_to_device(params: np.ndarray, device):
@@ -110,7 +120,7 @@ class Sampler:
         """logits: [B, >=V] float32 or bfloat16 (row stride = logits.stride(0));
         params_dev: uint8 tensor of B*32 bytes (see params_to_device);
         u: float32 [B]; hist: int32 [B, hist_cap]; hist_len: int32 [B].
-        hint: max_top_k of the batch (see batch_hint) or None (general kernel).
+        hint: the batch's batch_hint (or a plain int max_top_k) or None (general kernel).
         debug: dict of preallocated tensors (kept_ids, kept_probs, counts,
         mass, cut_ids, post_logits).  Returns the int32 [B] ids tensor."""
         torch = _torch()
@@ -140,6 +150,7 @@ class Sampler:
         if hint is not None:
             hs = TgsHint()
             hs.max_top_k = int(hint)
+            hs.min_top_k = int(getattr(hint, "min_top_k", 0))  # 0: unknown
         rc = self._L.tgs_sample(
             self._h, _ptr(logits), dt, B, V, logits.stride(0), _ptr(hist), _ptr(hist_len), hist_cap,
             _ptr(params_dev), _ptr(u), _ptr(out), C.byref(hs) if hs is not None else None,
