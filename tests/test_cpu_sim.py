@@ -250,6 +250,24 @@ def test_topp_kernel_bucket_overflow(sim, oracle):
     _check(sim, oracle, x, params, u, None, None)
 
 
+def test_topp_kernel_dense_rows_in_registers(sim, oracle):
+    """Register-resident rows whose allowed ids outnumber the LDS packing
+    capacity: the later passes run over the registers (one row masked down
+    to a packable count for contrast)."""
+    import tinygpt_amd as tg
+
+    B, V = 3, 24576
+    g = np.random.default_rng(62)
+    x = g.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    mask = np.full((1, V // 32), 0x0F0F0F0F, np.uint32)
+    params = oracle.make_params(B, temperature=[1.0, 0.8, 1.2], top_k=0, top_p=[0.9, 0.5, 1.0],
+                                mask_state=[-1, -1, 0])
+    u = g.random(B).astype(np.float32)
+    hint = tg.batch_hint(params, V)
+    r, _, _ = _check(sim, oracle, x, params, u, None, None, mask=mask, hint=hint, kept_cap=64)
+    assert r["launches"] == [(B, 1024)]
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_topp_kernel_serves_whole_batch(sim, oracle, bf16):
     """Every sampling row without a usable top-k (the hint's min_top_k == V):

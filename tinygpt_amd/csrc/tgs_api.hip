@@ -361,7 +361,8 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
     a.topp_all = 1;
     a.S = 1;
     a.L = V;
-    hipError_t e = tgs::launch_topp(a, dt, tgs::topp_lds_bytes(V, a.TS), (hipStream_t)stream);
+    a.topp_cap = tgs::topp_pack_cap(V, a.TS, h->lds_limit - 2 * sizeof(tgs::BlockScratch));
+    hipError_t e = tgs::launch_topp(a, dt, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
     return TGS_OK;
   }
@@ -381,6 +382,7 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
     return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
   if (a.full_rows && tgs::topp_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) > h->lds_limit)
     return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS (top-p rows)");
+  a.topp_cap = tgs::topp_pack_cap(V, a.TS, h->lds_limit - 2 * sizeof(tgs::BlockScratch));
   hipError_t e = tgs::launch_sample(a, dt, lds, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
   return TGS_OK;

@@ -57,6 +57,7 @@ struct SampleArgs {
   int full_rows;         // 1: full_kernel runs after the chunk kernels
   int hint_k;            // the launch hint's max_top_k (INT_MAX without a hint)
   int topp_all;          // 1: the top-p kernel alone serves the batch (its greedy rows too)
+  int topp_cap;          // top-p kernel: allowed ids packed into LDS (beyond topp_lds_bytes)
   tgs_debug dbg;
 };
 
@@ -95,7 +96,10 @@ hipError_t set_k64_lds_limit(size_t bytes);
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
 // Rows sampling top-p over the whole vocabulary (top_k disabled).
 size_t topp_lds_bytes(int V, int TS);
-hipError_t launch_topp(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
+// Packed-id capacity of the top-p kernel given lds_avail bytes of dynamic LDS.
+int topp_pack_cap(int V, int TS, size_t lds_avail);
+// Dynamic LDS: topp_lds_bytes + a.topp_cap packed ids.
+hipError_t launch_topp(const SampleArgs& a, int dtype, hipStream_t st);
 hipError_t set_topp_lds_limit(size_t bytes);
 // Batches of greedy rows and rows with 1 <= top_k <= KMAX whose rows fit the
 // top-k kernel's registers (V <= topk_max_vocab(dtype)).

@@ -708,7 +708,7 @@ hipError_t launch_sample(const SampleArgs& a, int dtype, size_t lds, hipStream_t
     else hipLaunchKernelGGL(full_kernel<float>, dim3(a.B), blk, lds, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    e = launch_topp(a, dtype, topp_lds_bytes(a.V, a.TS), st);
+    e = launch_topp(a, dtype, st);
   }
   return e;
 }

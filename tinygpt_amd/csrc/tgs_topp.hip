@@ -48,6 +48,7 @@ struct Scratch {
   u64 red64b[WT];
   unsigned red32[WT];
   unsigned ng;    // gathered ids
+  unsigned ncomp; // allowed ids packed
   int sel[2];     // buckets of the cut and of the draw
   int first;      // first rank meeting a mass target
 };
@@ -86,11 +87,17 @@ struct RowView {
     }
   }
 
-  __device__ __forceinline__ void load() {
+  // the row's vectors of this thread (issued before the row's parameters are
+  // read, so the two latencies overlap)
+  __device__ __forceinline__ static void fetch(const SampleArgs& a, const Tin* p, uint4 (&raw)[NV]) {
     if constexpr (RES) {
-      uint4 raw[NV];
 #pragma unroll
-      for (int j = 0; j < NV; j++) raw[j] = load_vec<Tin>(rowp, (threadIdx.x + j * BT) * EPV, a.V, a.aligned);
+      for (int j = 0; j < NV; j++) raw[j] = load_vec<Tin>(p, (threadIdx.x + j * BT) * EPV, a.V, a.aligned);
+    }
+  }
+
+  __device__ __forceinline__ void load(const uint4 (&raw)[NV]) {
+    if constexpr (RES) {
 #pragma unroll
       for (int j = 0; j < NV; j++) {
         float yv[EPV];
@@ -144,6 +151,30 @@ struct RowView {
   }
 };
 
+// One allowed id and its canonical logit, packed in LDS.
+struct alignas(8) Packed {
+  float y;
+  int id;
+};
+
+// The allowed ids of a row packed in LDS: E[0, n).
+struct CompactView {
+  const Packed* E;
+  int n;
+  template <class F>
+  __device__ __forceinline__ void each(F f) const {
+#pragma unroll 2
+    for (int i = threadIdx.x; i < n; i += BT) {
+      const Packed e = E[i];
+      f(e.id, e.y);
+    }
+  }
+  template <class F>
+  __device__ __forceinline__ void each_stream(F f) const {
+    each(f);
+  }
+};
+
 template <typename T>
 __device__ __forceinline__ T block_reduce_sum(T x, T* red) {
   x = wave_sum(x);
@@ -173,6 +204,7 @@ struct Tail {
   unsigned* CI;  // NB + 1 inclusive counts
   u64* MI;       // NB + 1 inclusive masses
   u64 *L, *R, *Q;
+  Packed* E;     // a.topp_cap packed allowed ids
   float m;
   int rb = -1;   // ranked bucket (-1: none)
   unsigned rn = 0;
@@ -220,76 +252,13 @@ __device__ __forceinline__ u64 resolve_mass(const View& rv, Tail& tl, int bq, u6
   return block_mass_select<BT>(en, target, bs, before, rank);
 }
 
-template <typename Tin, bool RES>
-__device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned char* smem, Scratch& ts,
-                                         BlockScratch& bs) {
+// The row after pass 1 (m, the largest composite Mc, nv allowed ids): the
+// mass histogram, the cut and the draw over the allowed ids of view v.
+template <class View>
+__device__ __forceinline__ void topp_rest(const SampleArgs& a, const Row& r, const View& rv, Tail& tl, u64 Mc,
+                                          unsigned nv, Scratch& ts, BlockScratch& bs) {
   const int b = r.b;
-  const int bw = a.TS > 0 ? (a.V + 31) / 32 : 0;
-  uint32_t* hbits = (uint32_t*)smem;
-  int2* hash = (int2*)(smem + ((bw * 4 + 15) / 16) * 16);
-  Tail tl;
-  tl.L = (u64*)((unsigned char*)hash + (size_t)a.TS * 8);  // CAPG (+ pad)
-  tl.R = tl.L + CAPG + 2;                                   // CAPG
-  tl.Q = tl.R + CAPG;                                       // CAPG
-  tl.CI = (unsigned*)(tl.Q + CAPG);                         // NB + 1 (+ pad)
-  tl.MI = (u64*)(tl.CI + NB + 4);                           // NB + 1
-  r.v0 = 0;
-  r.v1 = a.V;
-  if (r.use_pen) hash_build<BT>(a, r, hash, hbits, bw);
-  RowView<Tin, RES> rv(a, r, hash, hbits, (const Tin*)a.logits + (long long)b * a.row_stride);
-  rv.load();
-  if (a.dbg.post_logits) {
-    float* post = a.dbg.post_logits + (long long)b * a.V;
-    for (int v = threadIdx.x; v < a.V; v += BT) post[v] = -__builtin_inff();
-    __syncthreads();
-    rv.each([&](int id, float y) { post[id] = y; });
-  }
-
-  // pass 1: the largest composite (the greedy answer; its y is the maximum m)
-  // and the allowed count
-  u64 mcl = 0;
-  unsigned nvl = 0;
-  rv.each([&](int id, float y) {
-    const u64 c = comp_key(tg_key(y), id);
-    mcl = c > mcl ? c : mcl;
-    nvl++;
-  });
-  for (int i = threadIdx.x; i < NB + 1; i += BT) {
-    tl.CI[i] = 0u;
-    tl.MI[i] = 0ull;
-  }
-  mcl = wave_max(mcl);
-  nvl = wave_sum(nvl);
-  if (lane_id() == 0) {
-    ts.red64[threadIdx.x >> 6] = mcl;
-    ts.red32[threadIdx.x >> 6] = nvl;
-  }
-  __syncthreads();
-  u64 Mc = 0;
-  unsigned nv = 0;
-#pragma unroll
-  for (int i = 0; i < WT; i++) {
-    Mc = ts.red64[i] > Mc ? ts.red64[i] : Mc;
-    nv += ts.red32[i];
-  }
-  if (nv == 0 || r.mode == 0) {
-    // nothing allowed (-1), or a greedy row (the largest composite)
-    const int id = nv ? comp_id(Mc) : -1;
-    if (threadIdx.x == 0) {
-      a.out[b] = id;
-      write_row_diag(a, b, id >= 0, id >= 0, 0, 0, id);
-    }
-    if (a.dbg.kept_ids)
-      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT)
-        a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = (i == 0 && r.mode == 0) ? id : -1;
-    if (a.dbg.kept_probs)
-      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT)
-        a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = (i == 0 && r.mode == 0 && id >= 0) ? 1.0f : 0.0f;
-    return;
-  }
-  const float m = comp_y(Mc);
-  tl.m = m;
-
+  const float m = tl.m;
   // pass 2: count and exact-mass histogram over the buckets below m
   rv.each([&](int, float y) {
     const int bq = bucket::of(y, m);
@@ -352,12 +321,104 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
 }
 
 template <typename Tin, bool RES>
+__device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned char* smem, Scratch& ts,
+                                         BlockScratch& bs, const uint4 (&raw)[RowView<Tin, RES>::NV]) {
+  const int b = r.b;
+  const int bw = a.TS > 0 ? (a.V + 31) / 32 : 0;
+  uint32_t* hbits = (uint32_t*)smem;
+  int2* hash = (int2*)(smem + ((bw * 4 + 15) / 16) * 16);
+  Tail tl;
+  tl.L = (u64*)((unsigned char*)hash + (size_t)a.TS * 8);  // CAPG (+ pad)
+  tl.R = tl.L + CAPG + 2;                                   // CAPG
+  tl.Q = tl.R + CAPG;                                       // CAPG
+  tl.CI = (unsigned*)(tl.Q + CAPG);                         // NB + 1 (+ pad)
+  tl.MI = (u64*)(tl.CI + NB + 4);                           // NB + 1
+  tl.E = (Packed*)(tl.MI + NB + 1);                         // a.topp_cap
+  r.v0 = 0;
+  r.v1 = a.V;
+  if (r.use_pen) hash_build<BT>(a, r, hash, hbits, bw);
+  RowView<Tin, RES> rv(a, r, hash, hbits, (const Tin*)a.logits + (long long)b * a.row_stride);
+  rv.load(raw);
+  if (a.dbg.post_logits) {
+    float* post = a.dbg.post_logits + (long long)b * a.V;
+    for (int v = threadIdx.x; v < a.V; v += BT) post[v] = -__builtin_inff();
+    __syncthreads();
+    rv.each([&](int id, float y) { post[id] = y; });
+  }
+
+  // pass 1: the largest composite (the greedy answer; its y is the maximum m)
+  // and the allowed count
+  u64 mcl = 0;
+  unsigned nvl = 0;
+  rv.each([&](int id, float y) {
+    const u64 c = comp_key(tg_key(y), id);
+    mcl = c > mcl ? c : mcl;
+    nvl++;
+  });
+  for (int i = threadIdx.x; i < NB + 1; i += BT) {
+    tl.CI[i] = 0u;
+    tl.MI[i] = 0ull;
+  }
+  const unsigned nown = nvl;  // this thread's allowed ids
+  mcl = wave_max(mcl);
+  nvl = wave_sum(nvl);
+  if (lane_id() == 0) {
+    ts.red64[threadIdx.x >> 6] = mcl;
+    ts.red32[threadIdx.x >> 6] = nvl;
+  }
+  __syncthreads();
+  u64 Mc = 0;
+  unsigned nv = 0;
+#pragma unroll
+  for (int i = 0; i < WT; i++) {
+    Mc = ts.red64[i] > Mc ? ts.red64[i] : Mc;
+    nv += ts.red32[i];
+  }
+  if (nv == 0 || r.mode == 0) {
+    // nothing allowed (-1), or a greedy row (the largest composite)
+    const int id = nv ? comp_id(Mc) : -1;
+    if (threadIdx.x == 0) {
+      a.out[b] = id;
+      write_row_diag(a, b, id >= 0, id >= 0, 0, 0, id);
+    }
+    if (a.dbg.kept_ids)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT)
+        a.dbg.kept_ids[(long long)b * a.dbg.kept_cap + i] = (i == 0 && r.mode == 0) ? id : -1;
+    if (a.dbg.kept_probs)
+      for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT)
+        a.dbg.kept_probs[(long long)b * a.dbg.kept_cap + i] = (i == 0 && r.mode == 0 && id >= 0) ? 1.0f : 0.0f;
+    return;
+  }
+  tl.m = comp_y(Mc);
+  if constexpr (RES) {
+    if (nv <= (unsigned)a.topp_cap) {
+      // few allowed ids (a grammar mask): they alone, packed into LDS, feed
+      // every later pass (the exact exp and the bucket gathers run on
+      // allowed ids only)
+      if (threadIdx.x == 0) ts.ncomp = 0;
+      __syncthreads();
+      const unsigned wincl = wave_incl_scan(nown);
+      unsigned wbase = 0;
+      if (lane_id() == 63 && wincl) wbase = atomicAdd(&ts.ncomp, wincl);
+      unsigned off = __shfl(wbase, 63, 64) + wincl - nown;
+      rv.each([&](int id, float y) { tl.E[off++] = Packed{y, id}; });
+      __syncthreads();
+      topp_rest(a, r, CompactView{tl.E, (int)nv}, tl, Mc, nv, ts, bs);
+      return;
+    }
+  }
+  topp_rest(a, r, rv, tl, Mc, nv, ts, bs);
+}
+
+template <typename Tin, bool RES>
 __global__ __launch_bounds__(BT) void topp_kernel(SampleArgs a) {
   TGS_DYN_SMEM(smem);
   __shared__ Scratch ts;
   __shared__ BlockScratch bs;
   const int b = blockIdx.x;
   if (b >= a.B) return;
+  uint4 raw[RowView<Tin, RES>::NV];
+  RowView<Tin, RES>::fetch(a, (const Tin*)a.logits + (long long)b * a.row_stride, raw);
   Row r;
   const bool valid = row_setup(a, b, 0, r);
   const bool mine = valid && (r.mode == 2 ? !(r.k >= 1 && r.k < a.V) : (r.mode == 0 && a.topp_all));
@@ -370,7 +431,7 @@ __global__ __launch_bounds__(BT) void topp_kernel(SampleArgs a) {
     }
     return;
   }
-  topp_row<Tin, RES>(a, r, smem, ts, bs);
+  topp_row<Tin, RES>(a, r, smem, ts, bs, raw);
 }
 
 }  // namespace topp
@@ -381,7 +442,15 @@ size_t topp_lds_bytes(int V, int TS) {
          (size_t)(bucket::NB + 4) * 4 + (size_t)(bucket::NB + 1) * 8;
 }
 
-hipError_t launch_topp(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
+int topp_pack_cap(int V, int TS, size_t lds_avail) {
+  const size_t base = topp_lds_bytes(V, TS);
+  if (lds_avail <= base) return 0;
+  const size_t n = (lds_avail - base) / sizeof(topp::Packed);
+  return (int)(n < (size_t)V ? n : (size_t)V);
+}
+
+hipError_t launch_topp(const SampleArgs& a, int dtype, hipStream_t st) {
+  const size_t lds = topp_lds_bytes(a.V, a.TS) + (size_t)a.topp_cap * sizeof(topp::Packed);
   const bool res = a.V <= TOPP_NT * topp::RES_EPT;  // the row fits in registers
   const dim3 g(a.B), blk(TOPP_NT);
   if (dtype == 1) {
