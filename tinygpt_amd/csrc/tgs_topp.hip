@@ -350,11 +350,29 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
   // and the allowed count
   u64 mcl = 0;
   unsigned nvl = 0;
-  rv.each([&](int id, float y) {
-    const u64 c = comp_key(tg_key(y), id);
-    mcl = c > mcl ? c : mcl;
-    nvl++;
-  });
+  if constexpr (RES) {
+    // branch free over the registers: a thread's ids rise with the index,
+    // so a strict > keeps the smallest id among its equal maxima
+    float mx = -__builtin_inff();
+    int mid = 0;
+#pragma unroll
+    for (int q = 0; q < RES_EPT; q++) {
+      const float y = rv.y[q];
+      const bool gt = y > mx;
+      mid = gt ? ((int)threadIdx.x + (q / RowView<Tin, RES>::EPV) * BT) * RowView<Tin, RES>::EPV +
+                     q % RowView<Tin, RES>::EPV
+               : mid;
+      mx = gt ? y : mx;
+      nvl += (uint32_t)(y > -__builtin_inff());
+    }
+    mcl = mx > -__builtin_inff() ? comp_key(tg_key(mx), mid) : 0ull;
+  } else {
+    rv.each([&](int id, float y) {
+      const u64 c = comp_key(tg_key(y), id);
+      mcl = c > mcl ? c : mcl;
+      nvl++;
+    });
+  }
   for (int i = threadIdx.x; i < NB + 1; i += BT) {
     tl.CI[i] = 0u;
     tl.MI[i] = 0ull;
