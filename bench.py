@@ -12,6 +12,8 @@ same generator set (tinygpt_amd/workloads.py):
   c3  B=128, V=32000 fp32, grammar mask table of 4096 states, greedy + top-p
   c4  B=1024, V=151936 bf16, per-row top-k/top-p/T/repetition
   c5  B=32 sequences, k=8 draft tokens, V=128256 speculative verification
+  lp  teacher-forced token log-probabilities: 2048 positions, V=128256 fp32
+      (tgs_token_logprobs; a row outside the sampling chain)
 
 Inputs are resident in HBM before timing; distinct input sets rotate so the
 256 MB Infinity Cache cannot serve repeats (at least 512 MB in rotation
@@ -47,7 +49,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "lp"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
@@ -220,6 +222,53 @@ class SpecVerify:
         return fn
 
 
+class TokenLogprobs:
+    """lp: one tgs_token_logprobs call per step over B=2048 positions of
+    V=128256 fp32 logits (generated on the device from a seed); the oracle
+    checks the first SAMPLE rows of each set."""
+
+    SAMPLE = 128
+    TOL = (1e-4, 1e-6)  # |gpu - oracle| <= atol + rtol |oracle|
+
+    def __init__(self, name, torch, tg, W):
+        dev = "cuda:0"
+        self.name = name
+        self.rot, self.B, self.V = 2, 2048, 128256
+        self.sampler = tg.Sampler(device=0, max_batch=64, max_vocab=self.V, max_hist=1)
+        self.d, self.host = [], []
+        for i in range(self.rot):
+            gen = torch.Generator(device=dev).manual_seed(900 + i)
+            x = torch.randn(self.B, self.V, device=dev, generator=gen) * 3.0
+            tok = torch.randint(0, self.V, (self.B,), device=dev, generator=gen, dtype=torch.int32)
+            self.d.append(dict(x=x, tok=tok, out=torch.empty(self.B, dtype=torch.float32, device=dev)))
+            self.host.append(dict(x=x[: self.SAMPLE].cpu().numpy(), tok=tok[: self.SAMPLE].cpu().numpy()))
+        self.alg_bytes = self.B * (self.V * 4 + 4 + 4)
+        self.units_per_step = self.B
+        self.unit = "positions/s"
+        self.metric = "scored positions/sec (teacher-forced token log-probabilities), workload lp_scoring"
+        self.config = {"workload": "lp_scoring", "B": self.B, "V": self.V, "logits": "fp32 N(0, 3^2)"}
+        self.dtype = "f32"
+
+    def launch(self, i, stream):
+        x = self.d[i % self.rot]
+        self.sampler.token_logprobs(x["x"], x["tok"], out=x["out"], stream=stream)
+
+    def gpu_outputs(self):
+        return {i: self.d[i]["out"][: self.SAMPLE].cpu().numpy() for i in range(self.rot)}
+
+    def agreement(self, gpu_out, cpu_out):
+        atol, rtol = self.TOL
+        return float(np.mean([np.mean(np.abs(gpu_out[i] - cpu_out[i]) <= atol + rtol * np.abs(cpu_out[i]))
+                              for i in cpu_out]))
+
+    def cpu_call(self, pyoracle, nthreads):
+        def fn(i):
+            h = self.host[i]
+            lp, _ = pyoracle.token_logprobs(h["x"], h["tok"])
+            return lp, self.SAMPLE
+        return fn
+
+
 def cpu_baseline(wl, seconds):
     """The oracle (C restatement of the reference sampler) on this host:
     units/s with all host threads (up to 16) and with one thread."""
@@ -227,6 +276,11 @@ def cpu_baseline(wl, seconds):
     nthr = cpu_threads()
     rate_n, units_n, outs = timed_loop(wl.cpu_call(pyoracle, nthr), wl.rot, seconds * 0.6)
     rate_1, units_1, _ = timed_loop(wl.cpu_call(pyoracle, 1), wl.rot, seconds * 0.4)
+    if isinstance(wl, TokenLogprobs):  # numpy, one thread
+        rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), wl.rot, seconds)
+        return dict(value=round(rate, 2), unit=wl.unit, cores=1, kind="port",
+                    sample=f"{units} positions of lp_scoring (the first {wl.SAMPLE} rows of each of {wl.rot} "
+                           f"seeded sets, float64 numpy log-softmax) on 1 thread"), outs
     return dict(
         value=round(rate_n, 2), unit=wl.unit, cores=nthr, kind="port",
         sample=f"{units_n} rows of {wl.config['workload']} (batches of {wl.B} cycling over {wl.rot} seeded sets) "
@@ -255,8 +309,11 @@ def calibrate_copy(torch, mib, reps=8):
 
 TRAFFIC_FILES = {"c2": "k64_kernel_c2_traffic.json", "c3": "c3_grammar_traffic.json",
                  "c4": "c4_large_batch_traffic.json", "c5": "c5_spec_verify_traffic.json"}
-KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c3": "chunk_kernel + full_kernel (one call)",
-           "c4": "chunk_kernel + merge_kernel (one call)", "c5": "spec_stats_kernel + spec_verify_kernel (one call)"}
+TRAFFIC_FILES["lp"] = "lp_scoring_traffic.json"
+KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c3": "topp_kernel<float, true>",
+           "c4": "topk_kernel<bf16, 20>",
+           "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
+           "lp": "lp::chunk_kernel<float>"}
 
 
 def main():
@@ -275,7 +332,12 @@ def main():
     import tinygpt_amd as tg
     from tinygpt_amd import workloads as W
 
-    wl = SpecVerify(args.workload, torch, tg, W) if args.workload == "c5" else Sampling(args.workload, torch, tg, W)
+    if args.workload == "c5":
+        wl = SpecVerify(args.workload, torch, tg, W)
+    elif args.workload == "lp":
+        wl = TokenLogprobs(args.workload, torch, tg, W)
+    else:
+        wl = Sampling(args.workload, torch, tg, W)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream(device="cuda:0")  # default priority
     ROT = wl.rot
@@ -320,8 +382,11 @@ def main():
     agreement = None
     if not args.no_cpu:
         cpu, cpu_out = cpu_baseline(wl, args.cpu_seconds)
-        agreement = float(np.mean([np.mean(gpu_out[i] == cpu_out[i]) for i in cpu_out]))
-        if not all(np.array_equal(gpu_out[i], cpu_out[i]) for i in cpu_out):
+        if isinstance(wl, TokenLogprobs):
+            agreement = wl.agreement(gpu_out, cpu_out)
+        else:
+            agreement = float(np.mean([np.mean(gpu_out[i] == cpu_out[i]) for i in cpu_out]))
+        if agreement != 1.0:
             print("WARNING: GPU outputs differ from the oracle", file=sys.stderr)
 
     achieved = wl.alg_bytes / (ms_per_step * 1e-3) / 1e9

@@ -168,6 +168,21 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
                     const float* d_u_acc, const float* d_u_res, int32_t* d_n_acc, int32_t* d_out,
                     tgs_stream stream);
 
+/* Log-probability of one given token per row under the softmax of the raw
+ * logits: out_logprob[b] = x[b][tok[b]] - logsumexp(x[b]) (teacher-forced
+ * scoring; replaces `MLX.log(MLX.softmax(logits))[0, i, next]` in
+ * scoreLogprobs, native-mac/Sources/TinyGPTServe/Serve.swift:983-993, computed
+ * here in fp32 from fp32 or bf16 logits).  No penalty, temperature or mask
+ * applies.
+ *   d_logits      [B] rows of V logits, row_stride elements apart
+ *   d_tokens      [B] token ids (outside [0,V): NaN)
+ *   d_out_logprob [B] log-probabilities
+ *   d_out_lse     [B] logsumexp of each row (nullable)
+ * A row holding NaN or +inf, or only -inf, gives NaN.  B and V are not
+ * bounded by the handle's limits (no per-row workspace beyond a few bytes). */
+int tgs_token_logprobs(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
+                       const int32_t* d_tokens, float* d_out_logprob, float* d_out_lse, tgs_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -208,3 +208,30 @@ def spec_row_stats(y):
     m = np.zeros(1, dtype=np.float32)
     s = lib().tgo_spec_row_stats(_p(y), y.size, _p(m))
     return float(m[0]), float(s)
+
+
+def token_logprobs(logits, tokens, V=None):
+    """log(softmax(x))[b, tokens[b]] and logsumexp(x[b]) of each row, in
+    float64: the restatement of scoreLogprobs' `MLX.log(MLX.softmax(logits,
+    axis: -1))` gathered at the next token
+    (native-mac/Sources/TinyGPTServe/Serve.swift:983-993).
+
+    logits: float32 or bf16 bits (uint16), [B, row_stride], the first V
+    columns used.  A row holding NaN or +inf, or only -inf, gives NaN; a token
+    outside [0, V) gives NaN.  Returns (logprob [B], lse [B]) float64."""
+    x = np.asarray(logits)
+    if x.dtype == np.uint16:
+        x = (x.astype(np.uint32) << np.uint32(16)).view(np.float32)
+    V = x.shape[1] if V is None else V
+    x = x[:, :V].astype(np.float64)
+    tokens = np.asarray(tokens, dtype=np.int64)
+    bad = np.isnan(x).any(axis=1) | np.isposinf(x).any(axis=1)
+    m = np.max(np.where(np.isnan(x), -np.inf, x), axis=1)
+    bad |= m == -np.inf
+    mm = np.where(bad, 0.0, m)
+    with np.errstate(invalid="ignore", over="ignore"):
+        lse = mm + np.log(np.exp(x - mm[:, None]).sum(axis=1))
+    lse[bad] = np.nan
+    ok = (tokens >= 0) & (tokens < V)
+    xt = np.where(ok, x[np.arange(x.shape[0]), np.clip(tokens, 0, V - 1)], np.nan)
+    return xt - lse, lse

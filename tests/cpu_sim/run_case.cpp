@@ -96,5 +96,24 @@ int main(int argc, char** argv) {
     tgs_destroy(h);
     return 0;
   }
+  if (mode == "logprob") {
+    int B, V, dtype;
+    long long stride;
+    if (std::fscanf(m, "%d %d %lld %d", &B, &V, &stride, &dtype) != 4) return 4;
+    std::fclose(m);
+    auto logits = slurp(dir + "/logits.bin");
+    auto tok = slurp(dir + "/tokens.bin");
+    tgs_handle h;
+    int rc = tgs_create(&h, 0, 1, 1, 0);
+    if (rc) return 5;
+    std::vector<float> lp(B), lse(B);
+    rc = tgs_token_logprobs(h, logits.data(), (tgs_dtype)dtype, B, V, stride, (const int32_t*)tok.data(), lp.data(),
+                            lse.data(), nullptr);
+    if (rc) { std::printf("logprob %d %s\n", rc, tgs_last_error(h)); return 7; }
+    dump(dir + "/out_lp.bin", lp.data(), lp.size() * 4);
+    dump(dir + "/out_lse.bin", lse.data(), lse.size() * 4);
+    tgs_destroy(h);
+    return 0;
+  }
   return 2;
 }

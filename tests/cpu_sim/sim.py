@@ -67,6 +67,25 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
         return r
 
 
+def run_logprob(logits, tokens, V=None, timeout=600):
+    """tgs_token_logprobs through the simulation: (logprob [B], lse [B]).
+    logits [B, row_stride] float32 or bf16 bits (uint16); V <= row_stride."""
+    logits = np.ascontiguousarray(logits)
+    B, stride = logits.shape
+    V = stride if V is None else V
+    dtype = 1 if logits.dtype == np.uint16 else 0
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        logits.tofile(os.path.join(d, "logits.bin"))
+        np.ascontiguousarray(tokens, np.int32).tofile(os.path.join(d, "tokens.bin"))
+        with open(os.path.join(d, "meta.txt"), "w") as f:
+            f.write(f"{B} {V} {stride} {dtype}\n")
+        r = subprocess.run([BIN, "logprob", d], capture_output=True, text=True, timeout=timeout)
+        if r.returncode != 0:
+            raise RuntimeError(f"simulation failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")
+        return (np.fromfile(os.path.join(d, "out_lp.bin"), np.float32),
+                np.fromfile(os.path.join(d, "out_lse.bin"), np.float32))
+
+
 def run_spec(target, draft, dtok, T, u_acc, u_res, timeout=600):
     """tgs_spec_verify through the simulation: (n_acc [B], out [B, k+1])."""
     target = np.ascontiguousarray(target)

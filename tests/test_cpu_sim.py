@@ -141,6 +141,34 @@ def test_k64_bf16_and_mask(sim, oracle):
            hint=tg.batch_hint(params, V), split=3, kept_cap=64)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_token_logprobs(sim, oracle, bf16):
+    """tgs_token_logprobs: one workgroup per row, rows split into chunks
+    (few rows of 20000 ids), an odd stride (unaligned rows, scalar path) and
+    special values, within 1e-4 + 1e-6 |x| of the float64 oracle."""
+    from tinygpt_amd import workloads as W
+
+    g = np.random.default_rng(70)
+    for B, V, stride in ((5, 3000, 3000), (3, 20000, 20000), (4, 999, 1001)):
+        x = g.normal(0.0, 3.0, (B, stride)).astype(np.float32)
+        x[0, 5] = -np.inf
+        if B > 3:
+            x[3, :] = -np.inf
+            x[2, 9] = np.nan
+        if bf16:
+            if stride % 8:
+                continue
+            x = W.f32_to_bf16_bits(x)
+        tok = g.integers(0, V, B)
+        tok[-1] = V  # outside: NaN
+        lp, lse = sim.run_logprob(x, tok, V=V)
+        r_lp, r_lse = oracle.token_logprobs(x, tok, V=V)
+        for got, ref in ((lp, r_lp), (lse, r_lse)):
+            nan = np.isnan(ref)
+            np.testing.assert_array_equal(np.isnan(got), nan)
+            assert np.all(np.abs(got[~nan] - ref[~nan]) <= 1e-4 + 1e-6 * np.abs(ref[~nan]))
+
+
 def _spec_case(seed, B, k, V, T, bf16=False):
     from tinygpt_amd import workloads as W
 

@@ -39,6 +39,7 @@ EXPORTS = (
     "tgs_sample",
     "tgs_reserve_spec",
     "tgs_spec_verify",
+    "tgs_token_logprobs",
 )
 
 ROW_PARAMS_DTYPE = np.dtype(
@@ -119,6 +120,8 @@ def load() -> C.CDLL:
     L.tgs_reserve_spec.argtypes = [P, I, I]
     L.tgs_spec_verify.restype = I
     L.tgs_spec_verify.argtypes = [P, P, P, I, P, I, I, I, P, P, P, P, P, P]
+    L.tgs_token_logprobs.restype = I
+    L.tgs_token_logprobs.argtypes = [P, P, I, I, I, C.c_int64, P, P, P, P]
     _lib = L
     return L
 

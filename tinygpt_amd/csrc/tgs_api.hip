@@ -388,6 +388,46 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   return TGS_OK;
 }
 
+int tgs_token_logprobs(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
+                       const int32_t* d_tokens, float* d_out_logprob, float* d_out_lse, tgs_stream stream) {
+  if (!h) return TGS_EINVAL;
+  if (dt != TGS_F32 && dt != TGS_BF16) return fail(h, TGS_EINVAL, "dtype");
+  if (B < 0 || V < 1 || row_stride < V) return fail(h, TGS_EINVAL, "shape");
+  if (B == 0) return TGS_OK;
+  if (!d_logits || !d_tokens || !d_out_logprob) return fail(h, TGS_EINVAL, "null buffer");
+  DeviceGuard g(h->device);
+  if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
+  const size_t esz = dt == TGS_BF16 ? 2 : 4;
+  const int epv = dt == TGS_BF16 ? 8 : 4;
+  tgs::LogprobArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.logits = d_logits;
+  a.row_stride = row_stride;
+  a.B = B;
+  a.V = V;
+  a.aligned = ((uintptr_t)d_logits % 16 == 0) && (((uint64_t)row_stride * esz) % 16 == 0);
+  a.tokens = d_tokens;
+  a.out_lp = d_out_logprob;
+  a.out_lse = d_out_lse;
+  // enough workgroups for the chip: short batches split rows into chunks of
+  // at least 4096 ids (whole vectors) whose partial sums a second launch
+  // combines through the handle's workspace
+  const int target = 4 * h->num_cu;
+  int S = B >= target ? 1 : (target + B - 1) / B;
+  S = std::min(S, (V + 4095) / 4096);
+  S = std::max(S, 1);
+  const size_t ws_floats = (size_t)h->ws_rows * tgs::KMAX * 2;
+  if ((size_t)B * S * 2 > ws_floats) S = 1;
+  int L = (V + S - 1) / S;
+  L = (L + epv - 1) / epv * epv;
+  a.S = (V + L - 1) / L;
+  a.L = L;
+  a.part = (float*)h->ws;
+  hipError_t e = tgs::launch_logprob(a, dt == TGS_BF16 ? 1 : 0, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(h, e, "logprob kernel launch");
+  return TGS_OK;
+}
+
 int tgs_reserve_spec(tgs_handle h, int max_batch, int max_k) {
   if (!h) return TGS_EINVAL;
   if (max_batch < 1 || max_k < 0 || max_k > 64) return fail(h, TGS_EINVAL, "spec reserve");

@@ -61,6 +61,21 @@ struct SampleArgs {
   tgs_debug dbg;
 };
 
+// Token log-probabilities (tgs_logprob.hip).
+constexpr int LP_NT = 256;
+struct LogprobArgs {
+  const void* logits;
+  long long row_stride;  // elements
+  int B, V;
+  int aligned;           // rows start 16-byte aligned: vector loads
+  const int* tokens;     // [B]
+  float* out_lp;         // [B]
+  float* out_lse;        // [B] or nullptr
+  float* part;           // [B * S][2] chunk (max, sum of exp) pairs when S > 1
+  int S, L;              // chunks per row, chunk length in ids (whole vectors)
+};
+hipError_t launch_logprob(const LogprobArgs& a, int dtype, hipStream_t st);
+
 struct SpecArgs {
   const void* target;
   const void* draft;

@@ -185,3 +185,22 @@ class Sampler:
         )
         self._check(rc, "tgs_spec_verify")
         return n_acc, out
+
+    def token_logprobs(self, logits, tokens, out=None, lse=None, stream=None):
+        """log(softmax(logits))[b, tokens[b]] for each row b of logits [B, V]
+        (float32 or bfloat16, rows may be strided); tokens int32 [B].
+        Returns out float32 [B] (and fills lse [B] with each row's
+        logsumexp when given)."""
+        torch = _torch()
+        B, V = logits.shape
+        dt = TGS_BF16 if logits.dtype == torch.bfloat16 else TGS_F32
+        if logits.stride(1) != 1:
+            raise ValueError("logits rows must be contiguous")
+        if out is None:
+            out = torch.empty(B, dtype=torch.float32, device=logits.device)
+        st = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
+        rc = self._L.tgs_token_logprobs(
+            self._h, _ptr(logits), dt, B, V, logits.stride(0), _ptr(tokens), _ptr(out), _ptr(lse), C.c_void_p(st),
+        )
+        self._check(rc, "tgs_token_logprobs")
+        return out
