@@ -36,36 +36,50 @@ __device__ __forceinline__ u64 mass_c(u64 c, float m) { return mass(comp_y(c), m
 
 // In place: CI[0..NB] bucket counts become inclusive prefixes, MI[0..NB)
 // bucket masses inclusive prefixes with MI[NB] = MI[NB - 1] (the last bucket
-// holds mass 0).  BT == NB threads, thread t owns bucket t; red32 / red64
-// hold BT / 64 entries.  Starts and ends with a barrier's worth of ordering:
-// the histogram must be complete (a barrier) before the call.
+// holds mass 0).  BT threads (NB a multiple of BT), thread t owns buckets
+// [t NB/BT, (t + 1) NB/BT); red32 / red64 hold BT / 64 entries.  The
+// histogram must be complete (a barrier) before the call; ends with a
+// barrier.
 template <int BT>
 __device__ __forceinline__ void prefix(unsigned* CI, u64* MI, unsigned* red32, u64* red64) {
-  static_assert(BT == NB, "one bucket per thread");
+  static_assert(NB % BT == 0, "whole buckets per thread");
+  constexpr int PER = NB / BT;
   const int t = threadIdx.x, w = t >> 6, lane = lane_id();
-  const unsigned cc = CI[t];
-  const u64 cm = MI[t];
+  unsigned cc[PER];
+  u64 cm[PER];
+  unsigned ct = 0;
+  u64 mt = 0;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    cc[i] = CI[t * PER + i];
+    cm[i] = MI[t * PER + i];
+    ct += cc[i];
+    mt += cm[i];
+  }
   const unsigned tailc = (t == BT - 1) ? CI[NB] : 0u;
-  unsigned ci = wave_incl_scan(cc);
-  u64 mi = wave_incl_scan(cm);
+  unsigned ci = wave_incl_scan(ct);
+  u64 mi = wave_incl_scan(mt);
   if (lane == 63) {
     red32[w] = ci;
     red64[w] = mi;
   }
   __syncthreads();
-  unsigned oc = 0;
-  u64 om = 0;
+  unsigned oc = ci - ct;
+  u64 om = mi - mt;
   for (int v = 0; v < w; v++) {
     oc += red32[v];
     om += red64[v];
   }
-  ci += oc;
-  mi += om;
-  CI[t] = ci;
-  MI[t] = mi;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    oc += cc[i];
+    om += cm[i];
+    CI[t * PER + i] = oc;
+    MI[t * PER + i] = om;
+  }
   if (t == BT - 1) {
-    CI[NB] = ci + tailc;
-    MI[NB] = mi;
+    CI[NB] = oc + tailc;
+    MI[NB] = om;
   }
   __syncthreads();
 }
@@ -78,9 +92,13 @@ __device__ __forceinline__ u64 mass_before(const u64* MI, int bq) { return bq ? 
 // thread reads again before the next barrier.
 template <int BT>
 __device__ __forceinline__ int find_count(const unsigned* CI, unsigned target, int* sel) {
-  const int t = threadIdx.x;
-  if (CI[t] >= target && (t == 0 || CI[t - 1] < target)) *sel = t;
-  if (t == 0 && CI[NB] >= target && CI[NB - 1] < target) *sel = NB;
+  constexpr int PER = NB / BT;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int t = threadIdx.x * PER + i;
+    if (CI[t] >= target && (t == 0 || CI[t - 1] < target)) *sel = t;
+  }
+  if (threadIdx.x == 0 && CI[NB] >= target && CI[NB - 1] < target) *sel = NB;
   __syncthreads();
   return *sel;
 }
@@ -89,8 +107,12 @@ __device__ __forceinline__ int find_count(const unsigned* CI, unsigned target, i
 // MI[NB - 1]); as find_count.
 template <int BT>
 __device__ __forceinline__ int find_mass(const u64* MI, u64 target, int* sel) {
-  const int t = threadIdx.x;
-  if (MI[t] >= target && (t == 0 || MI[t - 1] < target)) *sel = t;
+  constexpr int PER = NB / BT;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int t = threadIdx.x * PER + i;
+    if (MI[t] >= target && (t == 0 || MI[t - 1] < target)) *sel = t;
+  }
   __syncthreads();
   return *sel;
 }
