@@ -14,6 +14,8 @@ same generator set (tinygpt_amd/workloads.py):
   c5  B=32 sequences, k=8 draft tokens, V=128256 speculative verification
   lp  teacher-forced token log-probabilities: 2048 positions, V=128256 fp32
       (tgs_token_logprobs; a row outside the sampling chain)
+  mask  grammar mask rows built on the device (tgs_mask_rows_from_dfa): 64
+      new tool-tag FSM states per call over a 151,936-token byte vocabulary
 
 Inputs are resident in HBM before timing; distinct input sets rotate so the
 256 MB Infinity Cache cannot serve repeats (at least 512 MB in rotation
@@ -49,7 +51,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "lp"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "lp", "mask"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
@@ -269,6 +271,88 @@ class TokenLogprobs:
         return fn
 
 
+def synthetic_vocab(V, seed=31):
+    """A BPE-like byte vocabulary: word pieces of printable ASCII, tag
+    pieces, multi-byte UTF-8, and the empty token 0."""
+    g = np.random.default_rng(seed)
+    pieces = [b"[", b"]", b"POINT", b":", b"none", b",", b"CLICK", b"TYPE", b"SCROLL", b"up", b"KEY", b"+",
+              b"OPEN_APP", b" ", b"_", b"-", b"12", b"9"]
+    toks = [b""]
+    letters = np.frombuffer(b"abcdefghijklmnopqrstuvwxyzABCDEFGHIJ etaoinshr.,", dtype=np.uint8)
+    while len(toks) < V:
+        r = g.random()
+        if r < 0.7:
+            n = int(g.integers(1, 13))
+            toks.append((b" " if g.random() < 0.4 else b"") + letters[g.integers(0, len(letters), n)].tobytes())
+        elif r < 0.9:
+            toks.append(b"".join(g.choice(pieces) for _ in range(g.integers(1, 4))))
+        else:
+            toks.append("".join(chr(int(c)) for c in g.integers(0xC0, 0x2FF, g.integers(1, 4))).encode())
+    return toks[:V]
+
+
+class MaskRows:
+    """mask: one tgs_mask_rows_from_dfa call per step building 64 rows (one
+    new tool-tag FSM state per sequence of a 64-row batch) over V=151936
+    token byte strings; rows rotate over the DFA's states."""
+
+    def __init__(self, name, torch, tg, W):
+        from tinygpt_amd import grammar as G
+
+        dev = "cuda:0"
+        self.name = name
+        self.rot, self.B, self.V = 4, 64, 151936
+        self.dfa = G.compile_gbnf(G.PACE_TOOL_TAGS)
+        self.toks = synthetic_vocab(self.V)
+        off, data = G.token_csr(self.toks)
+        self.sampler = tg.Sampler(device=0, max_batch=self.B, max_vocab=self.V, max_hist=1)
+        words = (self.V + 31) // 32
+        self.sampler.set_mask_table(np.zeros((self.B, words), np.uint32), self.V)
+        T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        self.trans, self.complete = T(self.dfa.trans), T(self.dfa.complete.astype(np.uint8))
+        self.off, self.data = T(off), T(data)
+        g = np.random.default_rng(5)
+        live = np.nonzero(~self.dfa.complete)[0]
+        self.states = [g.choice(live, self.B).astype(np.int32) for _ in range(self.rot)]
+        self.d_states = [T(s) for s in self.states]
+        self.rows = T(np.arange(self.B, dtype=np.int32))
+        self.alg_bytes = int(off.nbytes + data.nbytes + self.B * words * 4)
+        self.units_per_step = self.B
+        self.unit = "rows/s"
+        self.metric = "grammar mask rows built/sec (tool-tag DFA, V=151936), workload mask_rows"
+        self.config = {"workload": "mask_rows", "B": self.B, "V": self.V, "dfa_states": int(self.dfa.n),
+                       "bound_note": "dependent L2 transition lookups (about 6 per token), not HBM"}
+        self.dtype = "u8"
+
+    def launch(self, i, stream):
+        self.sampler.mask_rows_from_dfa(self.trans, self.complete, self.off, self.data, self.d_states[i % self.rot],
+                                        self.rows, stream=stream)
+
+    def gpu_outputs(self):
+        # the table after the last set's call: read back through greedy rows over zero logits
+        import torch
+
+        import tinygpt_amd as tg
+
+        dev = "cuda:0"
+        i = (self.rot - 1)
+        self.launch(i, torch.cuda.current_stream().cuda_stream)
+        params = tg.make_params(self.B, temperature=0.0, mask_state=list(range(self.B)))
+        post = torch.empty(self.B, self.V, dtype=torch.float32, device=dev)
+        self.sampler.sample(torch.zeros(self.B, self.V, device=dev), tg.params_to_device(params, dev),
+                            torch.zeros(self.B, device=dev), vocab=self.V, debug={"post_logits": post})
+        torch.cuda.synchronize()
+        return {i: (post[:4] == 0).cpu().numpy()}
+
+    def cpu_call(self, pyoracle, nthreads):
+        def fn(i):
+            s = self.states[self.rot - 1][:4]
+            w = pyoracle.dfa_mask_rows(self.dfa.trans, self.dfa.complete, self.toks, s)
+            bits = np.unpackbits(w.view(np.uint8).reshape(len(s), -1), axis=1, bitorder="little")[:, :self.V]
+            return bits.astype(bool), len(s)
+        return fn
+
+
 def cpu_baseline(wl, seconds):
     """The oracle (C restatement of the reference sampler) on this host:
     units/s with all host threads (up to 16) and with one thread."""
@@ -276,6 +360,12 @@ def cpu_baseline(wl, seconds):
     nthr = cpu_threads()
     rate_n, units_n, outs = timed_loop(wl.cpu_call(pyoracle, nthr), wl.rot, seconds * 0.6)
     rate_1, units_1, _ = timed_loop(wl.cpu_call(pyoracle, 1), wl.rot, seconds * 0.4)
+    if isinstance(wl, MaskRows):  # vectorised numpy DFA replay, one thread
+        rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), 1, seconds)
+        outs = {wl.rot - 1: outs[0]}
+        return dict(value=round(rate, 2), unit=wl.unit, cores=1, kind="port",
+                    sample=f"{units} rows (4 states of the last set, V={wl.V}, numpy vectorised byte replay) "
+                           f"on 1 thread"), outs
     if isinstance(wl, TokenLogprobs):  # numpy, one thread
         rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), wl.rot, seconds)
         return dict(value=round(rate, 2), unit=wl.unit, cores=1, kind="port",
@@ -310,10 +400,11 @@ def calibrate_copy(torch, mib, reps=8):
 TRAFFIC_FILES = {"c2": "k64_kernel_c2_traffic.json", "c3": "c3_grammar_traffic.json",
                  "c4": "c4_large_batch_traffic.json", "c5": "c5_spec_verify_traffic.json"}
 TRAFFIC_FILES["lp"] = "lp_scoring_traffic.json"
+TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
 KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c3": "topp_kernel<float, true>",
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
-           "lp": "lp::chunk_kernel<float>"}
+           "lp": "lp::chunk_kernel<float>", "mask": "maskb::build_kernel"}
 
 
 def main():
@@ -336,6 +427,8 @@ def main():
         wl = SpecVerify(args.workload, torch, tg, W)
     elif args.workload == "lp":
         wl = TokenLogprobs(args.workload, torch, tg, W)
+    elif args.workload == "mask":
+        wl = MaskRows(args.workload, torch, tg, W)
     else:
         wl = Sampling(args.workload, torch, tg, W)
     torch.cuda.synchronize()

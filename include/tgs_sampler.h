@@ -168,6 +168,26 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
                     const float* d_u_acc, const float* d_u_res, int32_t* d_n_acc, int32_t* d_out,
                     tgs_stream stream);
 
+/* Rows of the handle's mask table computed on the device from a byte-level
+ * DFA (a grammar compiled on the host, e.g. tinygpt_amd/grammar.py): row
+ * rows[i] gets bit v set when token v is non-empty and each of its bytes has
+ * a transition walking from DFA state states[i]; a complete state allows
+ * only eos_id (-1: no token).  Replaces the per-token byte replay of
+ * ServeTokenMasker.mask(for:), native-mac/Sources/TinyGPTServe/
+ * Serve.swift:2005-2025 (and LogitsMasker.mask(forFSM:),
+ * ConstrainedGen.swift:805-822), one row per FSM state, and the upload of
+ * that row: the table is written in place on the stream.
+ *   d_trans    [n_dfa][256] next state (-1 rejects the byte)
+ *   d_complete [n_dfa] 1 for accepting states with no transition
+ *   d_tok_off  [n_tokens + 1] offsets of each token's bytes in d_tok_bytes
+ *   d_states, d_rows [n] DFA states and the table rows to fill
+ * The table (tgs_mask_table_set) must hold at least n_tokens ids; bits of ids
+ * at or past n_tokens are cleared.  Rows outside the table are skipped; a
+ * next state outside [0, n_dfa) rejects. */
+int tgs_mask_rows_from_dfa(tgs_handle h, const int32_t* d_trans, const uint8_t* d_complete, int n_dfa,
+                           const int32_t* d_tok_off, const uint8_t* d_tok_bytes, int n_tokens, int eos_id,
+                           const int32_t* d_states, const int32_t* d_rows, int n, tgs_stream stream);
+
 /* Log-probability of one given token per row under the softmax of the raw
  * logits: out_logprob[b] = x[b][tok[b]] - logsumexp(x[b]) (teacher-forced
  * scoring; replaces `MLX.log(MLX.softmax(logits))[0, i, next]` in

@@ -235,3 +235,38 @@ def token_logprobs(logits, tokens, V=None):
     ok = (tokens >= 0) & (tokens < V)
     xt = np.where(ok, x[np.arange(x.shape[0]), np.clip(tokens, 0, V - 1)], np.nan)
     return xt - lse, lse
+
+
+def dfa_mask_rows(trans, complete, tokens, states, eos=-1):
+    """Mask words (uint32 [n, ceil(V / 32)]) of DFA states: bit v set when
+    token v is non-empty and every byte of it has a transition walking from
+    the state (the per-token byte replay of ServeTokenMasker.mask(for:),
+    native-mac/Sources/TinyGPTServe/Serve.swift:2005-2025, and
+    LogitsMasker.mask(forFSM:), ConstrainedGen.swift:805-822); a complete
+    state allows only token eos (none when eos < 0).  Vectorised over the
+    tokens, one byte position at a time."""
+    trans = np.asarray(trans, dtype=np.int64)
+    complete = np.asarray(complete, dtype=bool)
+    V = len(tokens)
+    L = max((len(t) for t in tokens), default=0)
+    mat = np.zeros((V, max(L, 1)), dtype=np.int64)
+    lens = np.array([len(t) for t in tokens], dtype=np.int64)
+    for v, t in enumerate(tokens):
+        mat[v, :len(t)] = np.frombuffer(t, dtype=np.uint8)
+    words = (V + 31) // 32
+    out = np.zeros((len(states), words), dtype=np.uint32)
+    for i, s in enumerate(states):
+        if complete[s]:
+            ok = np.zeros(V, dtype=bool)
+            if 0 <= eos < V:
+                ok[eos] = True
+        else:
+            cur = np.full(V, s, dtype=np.int64)
+            for p in range(L):
+                step = (p < lens) & (cur >= 0)
+                cur = np.where(step, trans[np.where(cur >= 0, cur, 0), mat[:, p]], cur)
+            ok = (lens > 0) & (cur >= 0)
+        pad = np.zeros(words * 32, dtype=bool)
+        pad[:V] = ok
+        out[i] = np.packbits(pad.reshape(-1, 32)[:, ::-1], axis=1).view(">u4").ravel().astype(np.uint32)
+    return out

@@ -115,7 +115,8 @@ inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args
   if (std::getenv("TGS_SIM_TRACE"))  // launch log (tests check which kernel ran)
     std::fprintf(stderr, "launch grid=%u block=%u lds=%zu\n", grid.x, block.x, shmem);
   const unsigned nt = block.x;
-  for (unsigned bx = 0; bx < grid.x; bx++) {
+  for (unsigned bi = 0; bi < grid.x * grid.y; bi++) {
+    const unsigned bx = bi % grid.x, by = bi / grid.x;
     BlockCtx ctx;
     ctx.bar = std::make_unique<std::barrier<>>(nt);
     ctx.waves.resize((nt + 63) / 64);
@@ -131,7 +132,7 @@ inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args
     for (unsigned t = 0; t < nt; t++)
       th.emplace_back([&, t]() {
         t_thread = dim3(t);
-        t_block = dim3(bx);
+        t_block = dim3(bx, by);
         k(args...);
         ctx.waves[t / 64].bar->arrive_and_drop();
         ctx.bar->arrive_and_drop();

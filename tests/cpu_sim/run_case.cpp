@@ -96,6 +96,42 @@ int main(int argc, char** argv) {
     tgs_destroy(h);
     return 0;
   }
+  if (mode == "maskbuild") {
+    int n_dfa, V, n, eos, n_rows;
+    if (std::fscanf(m, "%d %d %d %d %d", &n_dfa, &V, &n, &eos, &n_rows) != 5) return 4;
+    std::fclose(m);
+    auto trans = slurp(dir + "/trans.bin");
+    auto comp = slurp(dir + "/complete.bin");
+    auto off = slurp(dir + "/tok_off.bin");
+    auto bytes = slurp(dir + "/tok_bytes.bin");
+    auto st = slurp(dir + "/states.bin");
+    auto rows = slurp(dir + "/rows.bin");
+    tgs_handle h;
+    int rc = tgs_create(&h, 0, n_rows, V, 0);
+    if (rc) return 5;
+    const int words = (V + 31) / 32;
+    std::vector<uint32_t> ones((size_t)n_rows * words, 0xFFFFFFFFu);
+    rc = tgs_mask_table_set(h, ones.data(), n_rows, V);
+    if (rc) return 6;
+    rc = tgs_mask_rows_from_dfa(h, (const int32_t*)trans.data(), (const uint8_t*)comp.data(), n_dfa,
+                                (const int32_t*)off.data(), (const uint8_t*)bytes.data(), V, eos,
+                                (const int32_t*)st.data(), (const int32_t*)rows.data(), n, nullptr);
+    if (rc) { std::printf("maskbuild %d %s\n", rc, tgs_last_error(h)); return 7; }
+    // read the rows back through greedy rows over zero logits
+    std::vector<float> zeros((size_t)n_rows * V, 0.0f), u(n_rows, 0.0f), post((size_t)n_rows * V);
+    std::vector<tgs_row_params> p(n_rows);
+    for (int i = 0; i < n_rows; i++) {
+      p[i] = tgs_row_params{0.0f, 0, 1.0f, 1.0f, 0.0f, 0.0f, i, 0};
+    }
+    std::vector<int32_t> out(n_rows);
+    tgs_debug dbg = {nullptr, nullptr, 0, nullptr, nullptr, nullptr, post.data()};
+    rc = tgs_sample(h, zeros.data(), TGS_F32, n_rows, V, V, nullptr, nullptr, 0, p.data(), u.data(), out.data(),
+                    nullptr, &dbg, nullptr);
+    if (rc) { std::printf("sample %d %s\n", rc, tgs_last_error(h)); return 8; }
+    dump(dir + "/out_post.bin", post.data(), post.size() * 4);
+    tgs_destroy(h);
+    return 0;
+  }
   if (mode == "logprob") {
     int B, V, dtype;
     long long stride;

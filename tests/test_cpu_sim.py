@@ -169,6 +169,30 @@ def test_token_logprobs(sim, oracle, bf16):
             assert np.all(np.abs(got[~nan] - ref[~nan]) <= 1e-4 + 1e-6 * np.abs(ref[~nan]))
 
 
+def test_mask_rows_from_dfa(sim, oracle):
+    """tgs_mask_rows_from_dfa under ASan: tool-tag rows for several states,
+    a complete state with an EOS id, rows outside the table skipped, a token
+    longer than the bytes read up front; read back through greedy rows."""
+    from tinygpt_amd import grammar as G
+
+    g = np.random.default_rng(80)
+    d = G.compile_gbnf(G.PACE_TOOL_TAGS)
+    pieces = [b"[", b"]", b"POINT", b":", b"none", b",", b"TYPE", b"up", b" ", b"-", b"\xc3\xa9", b"12", b"x"]
+    toks = [b""] + [b"".join(g.choice(pieces) for _ in range(g.integers(1, 4))) for _ in range(600)]
+    toks.append(bytes(range(65, 65 + 30)))
+    V = len(toks)
+    off, data = G.token_csr(toks)
+    hist = [b"", b"ok [", b"ok [POINT:1", b"[TYPE:ab", b"[POINT:none]"]
+    states = np.array([d.walk(0, h) for h in hist] + [0, 0], np.int32)
+    rows = np.array([0, 1, 2, 3, 4, -1, 99], np.int32)
+    post = sim.run_maskbuild(d.trans, d.complete.astype(np.uint8), off, data, states, rows, n_rows=6, eos=3)
+    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states[:5], eos=3)
+    for i in range(5):
+        allowed = np.array([(int(want[i, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
+        np.testing.assert_array_equal(post[i] == 0.0, allowed)
+    assert (post[5] == 0.0).all()  # untouched row
+
+
 def _spec_case(seed, B, k, V, T, bf16=False):
     from tinygpt_amd import workloads as W
 

@@ -1,0 +1,65 @@
+"""GPU parity of mask-table rows built on the device from a byte-level DFA
+(tgs_mask_rows_from_dfa) against the DFA replay oracle, read back through
+the sampler itself: a greedy row over zero logits with mask_state = the
+built row reports 0 for allowed ids and -inf for the rest in post_logits.
+Bit-exact."""
+import numpy as np
+import pytest
+
+import gpu_harness as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _vocab(g, V):
+    pieces = [b"[", b"]", b"POINT", b":", b"none", b",", b"CLICK", b"TYPE", b"SCROLL", b"up", b"down", b"KEY",
+              b"+", b"OPEN_APP", b" ", b"_", b"-", b"\n", b"\xc3\xa9", b"\xe2\x80", b"hello", b"12", b"9", b"x", b"A"]
+    toks = [b""]
+    for _ in range(V - 2):
+        if g.random() < 0.6:
+            toks.append(b"".join(g.choice(pieces) for _ in range(g.integers(1, 4))))
+        else:
+            toks.append(bytes(g.integers(32, 127, size=g.integers(1, 24)).astype(np.uint8)))
+    toks.append(bytes(range(65, 65 + 40)))  # longer than the bytes read up front
+    return toks
+
+
+def test_tool_tag_rows_built_on_device(sampler, oracle):
+    import torch
+
+    import tinygpt_amd as tg
+    from tinygpt_amd import grammar as G
+
+    g = np.random.default_rng(21)
+    V = 40000
+    d = G.compile_gbnf(G.PACE_TOOL_TAGS)
+    toks = _vocab(g, V)
+    off, data = G.token_csr(toks)
+    hist = [b"", b"ok ", b"ok [", b"ok [POINT:", b"ok [POINT:1", b"ok [POINT:12,3:Sa", b"[TYPE:abc",
+            b"[SCROLL:up:", b"[KEY:cmd", b"[OPEN_APP:Sa 1", b"[POINT:none]"]
+    states = np.array([d.walk(0, h) for h in hist], np.int32)
+    assert (states >= 0).all() and d.complete[states[-1]]
+    n = len(states)
+    sampler.set_mask_table(np.full((n + 1, (V + 31) // 32), 0xFFFFFFFF, np.uint32), V)
+    dev = "cuda:0"
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    rows = np.arange(n, dtype=np.int32)
+    H.log(f"case mask build: V={V} dfa={d.n} states={n}")
+    sampler.mask_rows_from_dfa(T(d.trans), T(d.complete.astype(np.uint8)), T(off), T(data), T(states), T(rows), eos=7)
+    # rows outside the table are skipped
+    sampler.mask_rows_from_dfa(T(d.trans), T(d.complete.astype(np.uint8)), T(off), T(data), T(states[:2]),
+                               T(np.array([-1, n + 1], np.int32)))
+    torch.cuda.synchronize()
+    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states, eos=7)
+    params = tg.make_params(n + 1, temperature=0.0, mask_state=list(range(n + 1)))
+    post = torch.full((n + 1, V), float("nan"), dtype=torch.float32, device=dev)
+    sampler.sample(torch.zeros(n + 1, V, dtype=torch.float32, device=dev), tg.params_to_device(params, dev),
+                   torch.zeros(n + 1, dtype=torch.float32, device=dev), vocab=V, debug={"post_logits": post})
+    torch.cuda.synchronize()
+    got = post.cpu().numpy()
+    for i in range(n):
+        allowed = np.array([(int(want[i, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
+        np.testing.assert_array_equal(got[i] == 0.0, allowed, err_msg=f"row {i} ({hist[i]!r})")
+        assert np.all(np.isneginf(got[i][~allowed]))
+    assert (got[n] == 0.0).all()  # the untouched last row still allows everything
+    H.log("case mask build: ok")

@@ -40,6 +40,7 @@ EXPORTS = (
     "tgs_reserve_spec",
     "tgs_spec_verify",
     "tgs_token_logprobs",
+    "tgs_mask_rows_from_dfa",
 )
 
 ROW_PARAMS_DTYPE = np.dtype(
@@ -122,6 +123,8 @@ def load() -> C.CDLL:
     L.tgs_spec_verify.argtypes = [P, P, P, I, P, I, I, I, P, P, P, P, P, P]
     L.tgs_token_logprobs.restype = I
     L.tgs_token_logprobs.argtypes = [P, P, I, I, I, C.c_int64, P, P, P, P]
+    L.tgs_mask_rows_from_dfa.restype = I
+    L.tgs_mask_rows_from_dfa.argtypes = [P, P, P, I, P, P, I, I, P, P, I, P]
     _lib = L
     return L
 

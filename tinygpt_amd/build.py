@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libtgs_sampler.so")
 SOURCES = ["tgs_kernels.hip", "tgs_k64.hip", "tgs_spec.hip", "tgs_topp.hip", "tgs_topk.hip", "tgs_logprob.hip",
-           "tgs_api.hip"]
+           "tgs_mask.hip", "tgs_api.hip"]
 ARCH = os.environ.get("TGS_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

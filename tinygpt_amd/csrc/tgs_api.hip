@@ -388,6 +388,40 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   return TGS_OK;
 }
 
+int tgs_mask_rows_from_dfa(tgs_handle h, const int32_t* d_trans, const uint8_t* d_complete, int n_dfa,
+                           const int32_t* d_tok_off, const uint8_t* d_tok_bytes, int n_tokens, int eos_id,
+                           const int32_t* d_states, const int32_t* d_rows, int n, tgs_stream stream) {
+  if (!h) return TGS_EINVAL;
+  if (n < 0 || n_dfa < 1 || n_tokens < 0 || eos_id < -1 || eos_id >= n_tokens)
+    return fail(h, TGS_EINVAL, "mask build: bad arguments");
+  if (n == 0) return TGS_OK;
+  if (!d_trans || !d_complete || !d_tok_off || (!d_tok_bytes && n_tokens > 0) || !d_states || !d_rows)
+    return fail(h, TGS_EINVAL, "null buffer");
+  if (!h->mask_table || h->n_states < 1) return fail(h, TGS_EINVAL, "mask build: no mask table (tgs_mask_table_set)");
+  if (n_tokens > h->mask_vocab) return fail(h, TGS_ETOOBIG, "mask build: more tokens than the table's vocabulary");
+  if (n > 65535) return fail(h, TGS_ETOOBIG, "mask build: at most 65535 rows per call");
+  DeviceGuard g(h->device);
+  if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
+  tgs::MaskBuildArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.trans = d_trans;
+  a.complete = d_complete;
+  a.n_dfa = n_dfa;
+  a.tok_off = d_tok_off;
+  a.tok_bytes = d_tok_bytes;
+  a.n_tokens = n_tokens;
+  a.eos = eos_id;
+  a.states = d_states;
+  a.rows = d_rows;
+  a.n = n;
+  a.table = h->mask_table;
+  a.n_rows = h->n_states;
+  a.words = h->mask_words;
+  hipError_t e = tgs::launch_mask_build(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(h, e, "mask build launch");
+  return TGS_OK;
+}
+
 int tgs_token_logprobs(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
                        const int32_t* d_tokens, float* d_out_logprob, float* d_out_lse, tgs_stream stream) {
   if (!h) return TGS_EINVAL;

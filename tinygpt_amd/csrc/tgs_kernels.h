@@ -61,6 +61,24 @@ struct SampleArgs {
   tgs_debug dbg;
 };
 
+// Mask-table rows from a byte-level DFA (tgs_mask.hip).
+constexpr int MASK_NT = 256;
+struct MaskBuildArgs {
+  const int* trans;          // [n_dfa][256] next state, -1 rejects
+  const uint8_t* complete;   // [n_dfa] accepting with no way on
+  int n_dfa;
+  const int* tok_off;        // [n_tokens + 1]
+  const uint8_t* tok_bytes;
+  int n_tokens;
+  int eos;                   // token allowed in a complete state (-1: none)
+  const int* states;         // [n]
+  const int* rows;           // [n]
+  int n;
+  uint32_t* table;           // the handle's mask table
+  int n_rows, words;         // its rows and words per row
+};
+hipError_t launch_mask_build(const MaskBuildArgs& a, hipStream_t st);
+
 // Token log-probabilities (tgs_logprob.hip).
 constexpr int LP_NT = 256;
 struct LogprobArgs {
