@@ -321,7 +321,7 @@ class MaskRows:
         self.unit = "rows/s"
         self.metric = "grammar mask rows built/sec (tool-tag DFA, V=151936), workload mask_rows"
         self.config = {"workload": "mask_rows", "B": self.B, "V": self.V, "dfa_states": int(self.dfa.n),
-                       "bound_note": "dependent L2 transition lookups (about 6 per token), not HBM"}
+                       "bound_note": "dependent L2 transition lookups (one per token byte, 3.4 per token), not HBM"}
         self.dtype = "u8"
 
     def launch(self, i, stream):

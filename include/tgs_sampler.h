@@ -183,7 +183,8 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
  *   d_states, d_rows [n] DFA states and the table rows to fill
  * The table (tgs_mask_table_set) must hold at least n_tokens ids; bits of ids
  * at or past n_tokens are cleared.  Rows outside the table are skipped; a
- * next state outside [0, n_dfa) rejects. */
+ * next state outside [0, n_dfa) rejects.  At most 524,280 pairs per call;
+ * the inputs must stay alive until the stream reaches the call. */
 int tgs_mask_rows_from_dfa(tgs_handle h, const int32_t* d_trans, const uint8_t* d_complete, int n_dfa,
                            const int32_t* d_tok_off, const uint8_t* d_tok_bytes, int n_tokens, int eos_id,
                            const int32_t* d_states, const int32_t* d_rows, int n, tgs_stream stream);

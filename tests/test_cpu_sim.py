@@ -182,15 +182,18 @@ def test_mask_rows_from_dfa(sim, oracle):
     toks.append(bytes(range(65, 65 + 30)))
     V = len(toks)
     off, data = G.token_csr(toks)
-    hist = [b"", b"ok [", b"ok [POINT:1", b"[TYPE:ab", b"[POINT:none]"]
+    # more states than one workgroup walks together, the last group partial
+    hist = [b"", b"ok [", b"ok [POINT:1", b"[TYPE:ab", b"[POINT:none]", b"[SCROLL:", b"[KEY:a", b"ok",
+            b"[POINT:1,2:x", b"[OPEN_APP:S"]
+    nh = len(hist)
     states = np.array([d.walk(0, h) for h in hist] + [0, 0], np.int32)
-    rows = np.array([0, 1, 2, 3, 4, -1, 99], np.int32)
-    post = sim.run_maskbuild(d.trans, d.complete.astype(np.uint8), off, data, states, rows, n_rows=6, eos=3)
-    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states[:5], eos=3)
-    for i in range(5):
+    rows = np.array(list(range(nh)) + [-1, 99], np.int32)
+    post = sim.run_maskbuild(d.trans, d.complete.astype(np.uint8), off, data, states, rows, n_rows=nh + 1, eos=3)
+    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states[:nh], eos=3)
+    for i in range(nh):
         allowed = np.array([(int(want[i, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
         np.testing.assert_array_equal(post[i] == 0.0, allowed)
-    assert (post[5] == 0.0).all()  # untouched row
+    assert (post[nh] == 0.0).all()  # untouched row
 
 
 def _spec_case(seed, B, k, V, T, bf16=False):

@@ -399,7 +399,7 @@ int tgs_mask_rows_from_dfa(tgs_handle h, const int32_t* d_trans, const uint8_t* 
     return fail(h, TGS_EINVAL, "null buffer");
   if (!h->mask_table || h->n_states < 1) return fail(h, TGS_EINVAL, "mask build: no mask table (tgs_mask_table_set)");
   if (n_tokens > h->mask_vocab) return fail(h, TGS_ETOOBIG, "mask build: more tokens than the table's vocabulary");
-  if (n > 65535) return fail(h, TGS_ETOOBIG, "mask build: at most 65535 rows per call");
+  if (n > 8 * 65535) return fail(h, TGS_ETOOBIG, "mask build: at most 524280 rows per call");
   DeviceGuard g(h->device);
   if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
   tgs::MaskBuildArgs a;
