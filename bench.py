@@ -309,24 +309,28 @@ class MaskRows:
         words = (self.V + 31) // 32
         self.sampler.set_mask_table(np.zeros((self.B, words), np.uint32), self.V)
         T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-        self.trans, self.complete = T(self.dfa.trans), T(self.dfa.complete.astype(np.uint8))
+        bc, ct = self.dfa.byte_classes()
+        self.byte_class, self.trans = T(bc), T(ct)
+        self.complete = T(self.dfa.complete.astype(np.uint8))
         self.off, self.data = T(off), T(data)
         g = np.random.default_rng(5)
         live = np.nonzero(~self.dfa.complete)[0]
         self.states = [g.choice(live, self.B).astype(np.int32) for _ in range(self.rot)]
         self.d_states = [T(s) for s in self.states]
         self.rows = T(np.arange(self.B, dtype=np.int32))
-        self.alg_bytes = int(off.nbytes + data.nbytes + self.B * words * 4)
+        # token CSR, class map and transition table read once, rows written
+        self.alg_bytes = int(off.nbytes + data.nbytes + bc.nbytes + ct.nbytes + self.B * words * 4)
         self.units_per_step = self.B
         self.unit = "rows/s"
         self.metric = "grammar mask rows built/sec (tool-tag DFA, V=151936), workload mask_rows"
         self.config = {"workload": "mask_rows", "B": self.B, "V": self.V, "dfa_states": int(self.dfa.n),
-                       "bound_note": "dependent L2 transition lookups (one per token byte, 3.4 per token), not HBM"}
+                       "dfa_classes": int(ct.shape[1]),
+                       "bound_note": "dependent transition lookups in LDS (one per token byte, 6.3 per token), not HBM"}
         self.dtype = "u8"
 
     def launch(self, i, stream):
-        self.sampler.mask_rows_from_dfa(self.trans, self.complete, self.off, self.data, self.d_states[i % self.rot],
-                                        self.rows, stream=stream)
+        self.sampler.mask_rows_from_dfa(self.byte_class, self.trans, self.complete, self.off, self.data,
+                                        self.d_states[i % self.rot], self.rows, stream=stream)
 
     def gpu_outputs(self):
         # the table after the last set's call: read back through greedy rows over zero logits
@@ -404,7 +408,7 @@ TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
 KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c3": "topp_kernel<float, true>",
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
-           "lp": "lp::chunk_kernel<float>", "mask": "maskb::build_kernel"}
+           "lp": "lp::chunk_kernel<float>", "mask": "maskb::build_lds"}
 
 
 def main():

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define TGS_ABI_VERSION 2
+#define TGS_ABI_VERSION 3
 
 struct ihipStream_t;
 typedef struct ihipStream_t* tgs_stream;
@@ -177,17 +177,20 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
  * Serve.swift:2005-2025 (and LogitsMasker.mask(forFSM:),
  * ConstrainedGen.swift:805-822), one row per FSM state, and the upload of
  * that row: the table is written in place on the stream.
- *   d_trans    [n_dfa][256] next state (-1 rejects the byte)
- *   d_complete [n_dfa] 1 for accepting states with no transition
- *   d_tok_off  [n_tokens + 1] offsets of each token's bytes in d_tok_bytes
+ *   d_byte_class [256] class of each byte (a class >= n_cls rejects)
+ *   d_trans      [n_dfa][n_cls] next state per class (-1 rejects)
+ *   d_complete   [n_dfa] 1 for accepting states with no transition
+ *   d_tok_off    [n_tokens + 1] offsets of each token's bytes in d_tok_bytes
  *   d_states, d_rows [n] DFA states and the table rows to fill
- * The table (tgs_mask_table_set) must hold at least n_tokens ids; bits of ids
- * at or past n_tokens are cleared.  Rows outside the table are skipped; a
- * next state outside [0, n_dfa) rejects.  At most 524,280 pairs per call;
- * the inputs must stay alive until the stream reaches the call. */
-int tgs_mask_rows_from_dfa(tgs_handle h, const int32_t* d_trans, const uint8_t* d_complete, int n_dfa,
-                           const int32_t* d_tok_off, const uint8_t* d_tok_bytes, int n_tokens, int eos_id,
-                           const int32_t* d_states, const int32_t* d_rows, int n, tgs_stream stream);
+ * (the identity class map with n_cls = 256 passes a plain [n_dfa][256]
+ * table).  The table (tgs_mask_table_set) must hold at least n_tokens ids;
+ * bits of ids at or past n_tokens are cleared.  Rows outside the table are
+ * skipped; a next state outside [0, n_dfa) rejects.  At most 1,048,560 pairs
+ * per call; the inputs must stay alive until the stream reaches the call. */
+int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int32_t* d_trans, int n_cls,
+                           const uint8_t* d_complete, int n_dfa, const int32_t* d_tok_off,
+                           const uint8_t* d_tok_bytes, int n_tokens, int eos_id, const int32_t* d_states,
+                           const int32_t* d_rows, int n, tgs_stream stream);
 
 /* Log-probability of one given token per row under the softmax of the raw
  * logits: out_logprob[b] = x[b][tok[b]] - logsumexp(x[b]) (teacher-forced

@@ -97,9 +97,10 @@ int main(int argc, char** argv) {
     return 0;
   }
   if (mode == "maskbuild") {
-    int n_dfa, V, n, eos, n_rows;
-    if (std::fscanf(m, "%d %d %d %d %d", &n_dfa, &V, &n, &eos, &n_rows) != 5) return 4;
+    int n_dfa, n_cls, V, n, eos, n_rows;
+    if (std::fscanf(m, "%d %d %d %d %d %d", &n_dfa, &n_cls, &V, &n, &eos, &n_rows) != 6) return 4;
     std::fclose(m);
+    auto bcls = slurp(dir + "/byte_class.bin");
     auto trans = slurp(dir + "/trans.bin");
     auto comp = slurp(dir + "/complete.bin");
     auto off = slurp(dir + "/tok_off.bin");
@@ -113,7 +114,8 @@ int main(int argc, char** argv) {
     std::vector<uint32_t> ones((size_t)n_rows * words, 0xFFFFFFFFu);
     rc = tgs_mask_table_set(h, ones.data(), n_rows, V);
     if (rc) return 6;
-    rc = tgs_mask_rows_from_dfa(h, (const int32_t*)trans.data(), (const uint8_t*)comp.data(), n_dfa,
+    rc = tgs_mask_rows_from_dfa(h, (const uint8_t*)bcls.data(), (const int32_t*)trans.data(), n_cls,
+                                (const uint8_t*)comp.data(), n_dfa,
                                 (const int32_t*)off.data(), (const uint8_t*)bytes.data(), V, eos,
                                 (const int32_t*)st.data(), (const int32_t*)rows.data(), n, nullptr);
     if (rc) { std::printf("maskbuild %d %s\n", rc, tgs_last_error(h)); return 7; }

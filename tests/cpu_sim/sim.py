@@ -67,16 +67,18 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
         return r
 
 
-def run_maskbuild(trans, complete, tok_off, tok_bytes, states, rows, n_rows, eos=-1, timeout=600):
-    """tgs_mask_rows_from_dfa through the simulation, read back as the
-    post_logits of greedy rows over zero logits: float32 [n_rows, V]."""
+def run_maskbuild(byte_class, trans, complete, tok_off, tok_bytes, states, rows, n_rows, eos=-1, timeout=600):
+    """tgs_mask_rows_from_dfa through the simulation (trans [n_dfa, n_cls]),
+    read back as the post_logits of greedy rows over zero logits: float32
+    [n_rows, V]."""
     V = len(tok_off) - 1
     with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as d:
-        for name, arr, dt in (("trans", trans, np.int32), ("complete", complete, np.uint8), ("tok_off", tok_off, np.int32),
+        for name, arr, dt in (("byte_class", byte_class, np.uint8), ("trans", trans, np.int32),
+                              ("complete", complete, np.uint8), ("tok_off", tok_off, np.int32),
                               ("tok_bytes", tok_bytes, np.uint8), ("states", states, np.int32), ("rows", rows, np.int32)):
             np.ascontiguousarray(arr, dt).tofile(os.path.join(d, name + ".bin"))
         with open(os.path.join(d, "meta.txt"), "w") as f:
-            f.write(f"{len(trans)} {V} {len(states)} {eos} {n_rows}\n")
+            f.write(f"{trans.shape[0]} {trans.shape[1]} {V} {len(states)} {eos} {n_rows}\n")
         r = subprocess.run([BIN, "maskbuild", d], capture_output=True, text=True, timeout=timeout)
         if r.returncode != 0:
             raise RuntimeError(f"simulation failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")

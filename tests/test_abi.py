@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.tgs_abi_version() == 2
+    assert lib.tgs_abi_version() == 3
     assert lib.tgs_status_string(0) == b"ok"
     assert b"invalid" in lib.tgs_status_string(-1)
     assert lib.tgs_status_string(12345) == b"unknown status"

@@ -172,7 +172,9 @@ def test_token_logprobs(sim, oracle, bf16):
 def test_mask_rows_from_dfa(sim, oracle):
     """tgs_mask_rows_from_dfa under ASan: tool-tag rows for several states,
     a complete state with an EOS id, rows outside the table skipped, a token
-    longer than the bytes read up front; read back through greedy rows."""
+    longer than the bytes read up front; the class table in LDS, the full
+    table in global memory, and a byte mapped to a class outside the table;
+    read back through greedy rows."""
     from tinygpt_amd import grammar as G
 
     g = np.random.default_rng(80)
@@ -188,12 +190,30 @@ def test_mask_rows_from_dfa(sim, oracle):
     nh = len(hist)
     states = np.array([d.walk(0, h) for h in hist] + [0, 0], np.int32)
     rows = np.array(list(range(nh)) + [-1, 99], np.int32)
-    post = sim.run_maskbuild(d.trans, d.complete.astype(np.uint8), off, data, states, rows, n_rows=nh + 1, eos=3)
-    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states[:nh], eos=3)
-    for i in range(nh):
+    bc, ct = d.byte_classes()
+    bad = bc.copy()
+    bad[ord("x")] = ct.shape[1]  # a class outside the table rejects the byte
+    t_bad = d.trans.copy()
+    t_bad[:, ord("x")] = -1
+    cases = [(bc, ct, d.trans),  # 40 classes: the table in LDS
+             (np.arange(256, dtype=np.uint8), d.trans, d.trans),  # 256 columns: the table in global memory
+             (bad, ct, t_bad)]
+    for byte_class, trans, full in cases:
+        post = sim.run_maskbuild(byte_class, trans, d.complete.astype(np.uint8), off, data, states, rows,
+                                 n_rows=nh + 1, eos=3)
+        want = oracle.dfa_mask_rows(full, d.complete, toks, states[:nh], eos=3)
+        for i in range(nh):
+            allowed = np.array([(int(want[i, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
+            np.testing.assert_array_equal(post[i] == 0.0, allowed)
+        assert (post[nh] == 0.0).all()  # untouched row
+    # more states than one workgroup takes (a second workgroup row)
+    st70 = np.resize(states[:nh], 70).astype(np.int32)
+    post = sim.run_maskbuild(bc, ct, d.complete.astype(np.uint8), off, data, st70, np.arange(70, dtype=np.int32),
+                             n_rows=70, eos=3)
+    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, st70, eos=3)
+    for i in (0, 63, 64, 69):
         allowed = np.array([(int(want[i, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
         np.testing.assert_array_equal(post[i] == 0.0, allowed)
-    assert (post[nh] == 0.0).all()  # untouched row
 
 
 def _spec_case(seed, B, k, V, T, bf16=False):

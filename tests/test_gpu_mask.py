@@ -40,26 +40,33 @@ def test_tool_tag_rows_built_on_device(sampler, oracle):
     states = np.array([d.walk(0, h) for h in hist], np.int32)
     assert (states >= 0).all() and d.complete[states[-1]]
     n = len(states)
-    sampler.set_mask_table(np.full((n + 1, (V + 31) // 32), 0xFFFFFFFF, np.uint32), V)
+    sampler.set_mask_table(np.full((2 * n + 1, (V + 31) // 32), 0xFFFFFFFF, np.uint32), V)
     dev = "cuda:0"
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     rows = np.arange(n, dtype=np.int32)
     H.log(f"case mask build: V={V} dfa={d.n} states={n}")
-    sampler.mask_rows_from_dfa(T(d.trans), T(d.complete.astype(np.uint8)), T(off), T(data), T(states), T(rows), eos=7)
+    bc, ct = d.byte_classes()
+    comp = T(d.complete.astype(np.uint8))
+    # the 40-class table (in LDS) fills rows [0, n), the full 256-column
+    # table (read from global memory) rows [n, 2n): both against one oracle
+    sampler.mask_rows_from_dfa(T(bc), T(ct), comp, T(off), T(data), T(states), T(rows), eos=7)
+    sampler.mask_rows_from_dfa(T(np.arange(256, dtype=np.uint8)), T(d.trans), comp, T(off), T(data), T(states),
+                               T(rows + n), eos=7)
     # rows outside the table are skipped
-    sampler.mask_rows_from_dfa(T(d.trans), T(d.complete.astype(np.uint8)), T(off), T(data), T(states[:2]),
-                               T(np.array([-1, n + 1], np.int32)))
+    sampler.mask_rows_from_dfa(T(bc), T(ct), comp, T(off), T(data), T(states[:2]),
+                               T(np.array([-1, 2 * n + 1], np.int32)))
     torch.cuda.synchronize()
     want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states, eos=7)
-    params = tg.make_params(n + 1, temperature=0.0, mask_state=list(range(n + 1)))
-    post = torch.full((n + 1, V), float("nan"), dtype=torch.float32, device=dev)
-    sampler.sample(torch.zeros(n + 1, V, dtype=torch.float32, device=dev), tg.params_to_device(params, dev),
-                   torch.zeros(n + 1, dtype=torch.float32, device=dev), vocab=V, debug={"post_logits": post})
+    R = 2 * n + 1
+    params = tg.make_params(R, temperature=0.0, mask_state=list(range(R)))
+    post = torch.full((R, V), float("nan"), dtype=torch.float32, device=dev)
+    sampler.sample(torch.zeros(R, V, dtype=torch.float32, device=dev), tg.params_to_device(params, dev),
+                   torch.zeros(R, dtype=torch.float32, device=dev), vocab=V, debug={"post_logits": post})
     torch.cuda.synchronize()
     got = post.cpu().numpy()
-    for i in range(n):
-        allowed = np.array([(int(want[i, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
-        np.testing.assert_array_equal(got[i] == 0.0, allowed, err_msg=f"row {i} ({hist[i]!r})")
+    for i in range(2 * n):
+        allowed = np.array([(int(want[i % n, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
+        np.testing.assert_array_equal(got[i] == 0.0, allowed, err_msg=f"row {i} ({hist[i % n]!r})")
         assert np.all(np.isneginf(got[i][~allowed]))
-    assert (got[n] == 0.0).all()  # the untouched last row still allows everything
+    assert (got[2 * n] == 0.0).all()  # the untouched last row still allows everything
     H.log("case mask build: ok")

@@ -388,25 +388,30 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   return TGS_OK;
 }
 
-int tgs_mask_rows_from_dfa(tgs_handle h, const int32_t* d_trans, const uint8_t* d_complete, int n_dfa,
-                           const int32_t* d_tok_off, const uint8_t* d_tok_bytes, int n_tokens, int eos_id,
-                           const int32_t* d_states, const int32_t* d_rows, int n, tgs_stream stream) {
+int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int32_t* d_trans, int n_cls,
+                           const uint8_t* d_complete, int n_dfa, const int32_t* d_tok_off,
+                           const uint8_t* d_tok_bytes, int n_tokens, int eos_id, const int32_t* d_states,
+                           const int32_t* d_rows, int n, tgs_stream stream) {
   if (!h) return TGS_EINVAL;
-  if (n < 0 || n_dfa < 1 || n_tokens < 0 || eos_id < -1 || eos_id >= n_tokens)
+  if (n < 0 || n_dfa < 1 || n_cls < 1 || n_cls > 256 || n_tokens < 0 || eos_id < -1 || eos_id >= n_tokens)
     return fail(h, TGS_EINVAL, "mask build: bad arguments");
   if (n == 0) return TGS_OK;
-  if (!d_trans || !d_complete || !d_tok_off || (!d_tok_bytes && n_tokens > 0) || !d_states || !d_rows)
+  if (!d_byte_class || !d_trans || !d_complete || !d_tok_off || (!d_tok_bytes && n_tokens > 0) || !d_states ||
+      !d_rows)
     return fail(h, TGS_EINVAL, "null buffer");
   if (!h->mask_table || h->n_states < 1) return fail(h, TGS_EINVAL, "mask build: no mask table (tgs_mask_table_set)");
   if (n_tokens > h->mask_vocab) return fail(h, TGS_ETOOBIG, "mask build: more tokens than the table's vocabulary");
-  if (n > 8 * 65535) return fail(h, TGS_ETOOBIG, "mask build: at most 524280 rows per call");
+  if (n > tgs::MASK_SPW_LDS * 65535) return fail(h, TGS_ETOOBIG, "mask build: at most 1048560 rows per call");
   DeviceGuard g(h->device);
   if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
   tgs::MaskBuildArgs a;
   std::memset(&a, 0, sizeof(a));
+  a.byte_class = d_byte_class;
   a.trans = d_trans;
+  a.n_cls = n_cls;
   a.complete = d_complete;
   a.n_dfa = n_dfa;
+  a.lds = tgs::mask_lds_table_bytes(n_dfa, n_cls) <= (size_t)tgs::MASK_LDS_TABLE;  // 16-bit offsets fit
   a.tok_off = d_tok_off;
   a.tok_bytes = d_tok_bytes;
   a.n_tokens = n_tokens;

@@ -63,10 +63,17 @@ struct SampleArgs {
 
 // Mask-table rows from a byte-level DFA (tgs_mask.hip).
 constexpr int MASK_NT = 256;
+constexpr int MASK_SPW = 64;             // requested states per workgroup (global-table kernel)
+constexpr int MASK_SPW_LDS = 16;         // requested states per workgroup (LDS-table kernel)
+constexpr int MASK_NSUB = 4;             // 256-token sub-chunks per LDS-table workgroup (whole lines per row)
+constexpr int MASK_LDS_TABLE = 60 * 1024;  // largest transition table held in LDS (16-bit row offsets)
 struct MaskBuildArgs {
-  const int* trans;          // [n_dfa][256] next state, -1 rejects
-  const uint8_t* complete;   // [n_dfa] accepting with no way on
+  const uint8_t* byte_class;  // [256] class of each byte (>= n_cls rejects)
+  const int* trans;           // [n_dfa][n_cls] next state, -1 rejects
+  int n_cls;
+  const uint8_t* complete;    // [n_dfa] accepting with no way on
   int n_dfa;
+  int lds;                    // 1: the table fits LDS (16-bit row offsets, dead state, reject and stay columns)
   const int* tok_off;        // [n_tokens + 1]
   const uint8_t* tok_bytes;
   int n_tokens;
@@ -78,6 +85,7 @@ struct MaskBuildArgs {
   int n_rows, words;         // its rows and words per row
 };
 hipError_t launch_mask_build(const MaskBuildArgs& a, hipStream_t st);
+size_t mask_lds_table_bytes(int n_dfa, int n_cls);  // 16-bit table with the dead state, reject and stay columns
 
 // Token log-probabilities (tgs_logprob.hip).
 constexpr int LP_NT = 256;

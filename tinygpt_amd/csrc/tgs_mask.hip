@@ -8,14 +8,22 @@
 // is complete (accepting, no way on) allows only the EOS token given (none
 // for -1).
 //
-// One lane per token; each workgroup walks its tokens from eight requested
-// states side by side (eight independent lookup chains per lane), reading
-// each token's first 16 bytes once, so the token table is read once per
-// eight rows and only the transition lookups (an L2-resident table of 1 KiB
-// per state) form dependent chains; a ballot per state gives two mask words
-// per wave, written straight into the table row.
-// Malformed input cannot read out of bounds: a next state outside the
-// table rejects, rows outside the table are skipped.
+// The DFA comes as a byte-class map and a [n_dfa][n_cls] transition table
+// (bytes of one class move every state alike).  One lane per token; a
+// workgroup takes 256 tokens and up to MASK_SPW requested states, a group at
+// a time: each lane reads its token's first 16 bytes once (as classes) and
+// walks them from several states side by side (independent lookup chains).
+// A ballot per state gives two mask words per wave; the LDS kernel stages
+// the workgroup's words and stores each row's eight consecutive words from
+// adjacent lanes, the global kernel stores them straight into the rows.
+//
+// When the table is small enough (16-bit entries, MASK_LDS_TABLE bytes) the
+// workgroup first copies it into LDS with an extra dead state and extra
+// reject and stay columns, so every invalid move lands in the dead state and
+// a walk is a chain of branch-free LDS reads.  Otherwise the walk reads the
+// table from global memory (L2).
+// Malformed input cannot read out of bounds: a class or next state outside
+// the table rejects, rows outside the table are skipped.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 
@@ -25,62 +33,21 @@ namespace maskb {
 constexpr int MT = MASK_NT;
 constexpr int PRE = 16;  // token bytes read before the walks
 constexpr int SG = 8;    // states walked together per lane (independent lookup chains)
+constexpr int SPW = MASK_SPW;
+static_assert(SPW % SG == 0, "whole groups per workgroup");
 
-// Workgroup (token chunk, group of SG requested states): each lane reads its
-// token's first PRE bytes once and walks them from the SG states side by
-// side, then one ballot per state gives the lane's wave two mask words.
-__global__ __launch_bounds__(MT) void build_kernel(MaskBuildArgs a) {
-  const int v = blockIdx.x * MT + (int)threadIdx.x;
-  const int i0 = blockIdx.y * SG;
-  int p0 = 0, len = 0;
-  if (v < a.n_tokens) {
-    p0 = a.tok_off[v];
-    len = a.tok_off[v + 1] - p0;
-  }
-  uint32_t pre[PRE];
-#pragma unroll
-  for (int k = 0; k < PRE; k++) pre[k] = k < len ? a.tok_bytes[p0 + k] : 0u;
-  int cur[SG];
-  bool eos_ok[SG];
-#pragma unroll
-  for (int g = 0; g < SG; g++) {
-    const int i = i0 + g;
-    const int s = i < a.n ? a.states[i] : -1;
-    const bool in = s >= 0 && s < a.n_dfa && v < a.n_tokens;
-    const bool comp = in && a.complete[s];
-    eos_ok[g] = comp && v == a.eos;
-    cur[g] = (in && !comp && len > 0) ? s : -1;
-  }
-#pragma unroll
-  for (int k = 0; k < PRE; k++) {
-    if (k < len) {
-#pragma unroll
-      for (int g = 0; g < SG; g++) {
-        if (cur[g] >= 0) {
-          const int nx = a.trans[(long long)cur[g] * 256 + pre[k]];
-          cur[g] = nx < a.n_dfa ? nx : -1;
-        }
-      }
-    }
-  }
-  for (int p = p0 + PRE; p < p0 + len; p++) {  // tokens longer than PRE bytes
-    const uint32_t byte = a.tok_bytes[p];
-#pragma unroll
-    for (int g = 0; g < SG; g++) {
-      if (cur[g] >= 0) {
-        const int nx = a.trans[(long long)cur[g] * 256 + byte];
-        cur[g] = nx < a.n_dfa ? nx : -1;
-      }
-    }
-  }
+// Writes the row bits of one group of G states (i0 .. i0 + G - 1); row(i)
+// gives the table row of requested state i.
+template <int G, class RowOf>
+__device__ __forceinline__ void store_rows(const MaskBuildArgs& a, int i0, const bool (&ok)[G], RowOf row_of) {
   const int lane = lane_id();
   const int w0 = (blockIdx.x * MT + ((int)threadIdx.x & ~63)) >> 5;  // this wave's first word
 #pragma unroll
-  for (int g = 0; g < SG; g++) {
+  for (int g = 0; g < G; g++) {
     const int i = i0 + g;
-    const u64 bal = __ballot(cur[g] >= 0 || eos_ok[g]);
+    const u64 bal = __ballot(ok[g]);
     if (i >= a.n) continue;
-    const int row = a.rows[i];
+    const int row = row_of(i);
     if (row < 0 || row >= a.n_rows) continue;
     uint32_t* dst = a.table + (long long)row * a.words;
     if (lane == 0 && w0 < a.words) dst[w0] = (uint32_t)bal;
@@ -88,11 +55,238 @@ __global__ __launch_bounds__(MT) void build_kernel(MaskBuildArgs a) {
   }
 }
 
+// Start of each requested state of group i0 for this lane's token: eos_ok
+// for a complete state's EOS token; live walks start at the state, others
+// at `none`.  state_of(i) gives requested state i and complete_of(i, s)
+// whether its DFA state s (in range) is complete.
+template <int G, class StateOf, class CompleteOf>
+__device__ __forceinline__ void group_start(const MaskBuildArgs& a, int i0, int v, int len, int none,
+                                            int (&st)[G], bool (&eos_ok)[G], StateOf state_of,
+                                            CompleteOf complete_of) {
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    const int i = i0 + g;
+    const int s = i < a.n ? state_of(i) : -1;
+    const bool in = s >= 0 && s < a.n_dfa && v < a.n_tokens;
+    const bool comp = in && complete_of(i, s);
+    eos_ok[g] = comp && v == a.eos;
+    st[g] = (in && !comp && len > 0) ? s : none;
+  }
+}
+
+// LDS table.  Columns: the n_cls classes, then `reject` (every state to the
+// dead state) and `stay` (every state to itself, for the steps past a
+// token's end); rows: the n_dfa states, then the dead state (every column
+// back to it).  Entries are byte offsets of the next state's row, so a step
+// is one add and one 16-bit LDS read; the table is at most MASK_LDS_TABLE
+// bytes, so offsets fit 16 bits.  The class map holds byte offsets of
+// columns.  Workgroup (token chunk, SPW requested states).
+constexpr int SGL = 16;         // states walked together in the LDS kernel
+constexpr int FB = 16;          // table loads issued together in the fill
+constexpr int NSUB = MASK_NSUB; // 256-token sub-chunks per LDS-kernel workgroup
+constexpr int SPWL = MASK_SPW_LDS;
+static_assert(SPWL % SGL == 0, "whole groups per workgroup");
+
+// A token's byte range and its first PRE bytes (0 past the end).
+struct Tok {
+  int p0, len;
+  uint32_t raw[PRE];
+};
+__device__ __forceinline__ void tok_range(const MaskBuildArgs& a, int v, Tok& k) {
+  k.p0 = 0;
+  k.len = 0;
+  if (v < a.n_tokens) {
+    k.p0 = a.tok_off[v];
+    k.len = a.tok_off[v + 1] - k.p0;
+  }
+}
+__device__ __forceinline__ void tok_bytes(const MaskBuildArgs& a, Tok& k) {
+#pragma unroll
+  for (int j = 0; j < PRE; j++) k.raw[j] = j < k.len ? a.tok_bytes[k.p0 + j] : 0u;
+}
+
+// Workgroup (NSUB * MT tokens, SPWL requested states): every row it writes
+// gets NSUB * MT / 32 consecutive words (whole 128-byte lines), staged in
+// LDS and stored by adjacent lanes.
+__global__ __launch_bounds__(MT) void build_lds(MaskBuildArgs a) {
+  TGS_DYN_SMEM(smem);
+  __shared__ int req_state[SPWL], req_row[SPWL];
+  __shared__ uint8_t req_complete[SPWL];
+  __shared__ u64 words[SPWL][NSUB * MT / 64];  // [state][sub-chunk wave]
+  uint16_t* cls2 = (uint16_t*)smem;             // [256] column byte offsets
+  unsigned char* tab = smem + 512;              // [(n_dfa + 1)][W] uint16
+  const int W = a.n_cls + 2, dead = a.n_dfa;
+  const int t = threadIdx.x;
+  const int vb = blockIdx.x * NSUB * MT + t;    // this lane's token in sub-chunk 0
+  Tok cur_tok, next_tok;
+  tok_range(a, vb, cur_tok);
+  tok_bytes(a, cur_tok);
+  const int ib = blockIdx.y * SPWL;
+  if (t < SPWL) {  // this workgroup's requested states, their rows and completeness
+    const int i = ib + t;
+    const int s = i < a.n ? a.states[i] : -1;
+    req_state[t] = s;
+    req_row[t] = i < a.n ? a.rows[i] : -1;
+    req_complete[t] = (s >= 0 && s < a.n_dfa) ? a.complete[s] : 0;
+  }
+  for (int i = t; i < 256; i += MT) {
+    const int c = a.byte_class[i];
+    cls2[i] = (uint16_t)(2 * (c < a.n_cls ? c : a.n_cls));
+  }
+  // The table: thread -> (first row, column) once, rows in steps of rpi;
+  // FB rows' loads are issued before any is used (an L2 round trip per
+  // batch, not per entry).
+  auto entry = [&](int s, int c, int q) {
+    int nx = dead;
+    if (s < a.n_dfa) {
+      if (c < a.n_cls) nx = (q >= 0 && q < a.n_dfa) ? q : dead;
+      else if (c == a.n_cls + 1) nx = s;
+    }
+    ((uint16_t*)tab)[s * W + c] = (uint16_t)(nx * W * 2);
+  };
+  if (W <= MT) {
+    const int rpi = MT / W;
+    const int r0 = t / W, c = t - r0 * W;
+    if (r0 < rpi) {
+      for (int s0 = r0; s0 <= a.n_dfa; s0 += FB * rpi) {
+        int q[FB];
+#pragma unroll
+        for (int j = 0; j < FB; j++) {
+          const int s = s0 + j * rpi;
+          q[j] = (s < a.n_dfa && c < a.n_cls) ? a.trans[(long long)s * a.n_cls + c] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < FB; j++) {
+          const int s = s0 + j * rpi;
+          if (s <= a.n_dfa) entry(s, c, q[j]);
+        }
+      }
+    }
+  } else {  // more than MT columns: one row at a time
+    for (int s = 0; s <= a.n_dfa; s++)
+      for (int c = t; c < W; c += MT) entry(s, c, (s < a.n_dfa && c < a.n_cls) ? a.trans[(long long)s * a.n_cls + c] : -1);
+  }
+  __syncthreads();
+  const uint32_t stay2 = 2u * (uint32_t)(a.n_cls + 1);
+  const uint32_t dead2 = (uint32_t)(dead * W * 2);
+
+#pragma unroll 1
+  for (int sub = 0; sub < NSUB; sub++) {
+    const int v = vb + sub * MT;
+    if (sub + 1 < NSUB) {  // the next sub-chunk's bytes load under this one's walks
+      tok_range(a, v + MT, next_tok);
+      tok_bytes(a, next_tok);
+    }
+    const int p0 = cur_tok.p0, len = cur_tok.len;
+    uint32_t pc[PRE];  // column offsets of the first PRE bytes; `stay` past the end
+#pragma unroll
+    for (int k = 0; k < PRE; k++) pc[k] = k < len ? (uint32_t)cls2[cur_tok.raw[k]] : stay2;
+    const int lmax = __builtin_amdgcn_readfirstlane(wave_max(len < PRE ? len : PRE));  // steps this wave needs
+#pragma unroll 1
+    for (int i0 = ib; i0 < ib + SPWL && i0 < a.n; i0 += SGL) {
+      int st[SGL];
+      bool eos_ok[SGL];
+      group_start<SGL>(a, i0, v, len, dead, st, eos_ok, [&](int i) { return req_state[i - ib]; },
+                       [&](int i, int) { return req_complete[i - ib] != 0; });
+      uint32_t cur[SGL];
+#pragma unroll
+      for (int g = 0; g < SGL; g++) cur[g] = (uint32_t)(st[g] * W * 2);
+#pragma unroll
+      for (int k = 0; k < PRE; k++) {
+        if (k < lmax) {
+#pragma unroll
+          for (int g = 0; g < SGL; g++) cur[g] = *(const uint16_t*)(tab + cur[g] + pc[k]);
+        }
+      }
+      for (int p = p0 + PRE; p < p0 + len; p++) {  // tokens longer than PRE bytes
+        const uint32_t c2 = cls2[a.tok_bytes[p]];
+#pragma unroll
+        for (int g = 0; g < SGL; g++) cur[g] = *(const uint16_t*)(tab + cur[g] + c2);
+      }
+#pragma unroll
+      for (int g = 0; g < SGL; g++) {
+        const u64 bal = __ballot(cur[g] != dead2 || eos_ok[g]);
+        if (lane_id() == 0) words[i0 - ib + g][sub * (MT / 64) + (t >> 6)] = bal;
+      }
+    }
+    if (sub + 1 < NSUB) cur_tok = next_tok;
+  }
+  // the rows' words of this token range, stored coalesced: each row gets
+  // its NSUB * MT / 32 consecutive words from adjacent lanes
+  __syncthreads();
+  constexpr int WPB = NSUB * MT / 32;  // words per row per workgroup
+  const int nst = (a.n - ib) < SPWL ? (a.n - ib) : SPWL;
+  const uint32_t* wsrc = (const uint32_t*)&words[0][0];
+  for (int j = t; j < nst * WPB; j += MT) {
+    const int r = j / WPB, q = j - r * WPB;
+    const int row = req_row[r];
+    const int word = blockIdx.x * WPB + q;
+    if (row >= 0 && row < a.n_rows && word < a.words) a.table[(long long)row * a.words + word] = wsrc[r * WPB + q];
+  }
+}
+
+// Global table (too large for LDS): the class map in LDS, transitions read
+// from memory with every index checked.
+__global__ __launch_bounds__(MT) void build_global(MaskBuildArgs a) {
+  __shared__ uint8_t cls[256];
+  const int v = blockIdx.x * MT + (int)threadIdx.x;
+  int p0 = 0, len = 0;
+  if (v < a.n_tokens) {
+    p0 = a.tok_off[v];
+    len = a.tok_off[v + 1] - p0;
+  }
+  uint32_t raw[PRE];
+#pragma unroll
+  for (int k = 0; k < PRE; k++) raw[k] = k < len ? a.tok_bytes[p0 + k] : 0u;
+  for (int i = threadIdx.x; i < 256; i += MT) {
+    const int c = a.byte_class[i];
+    cls[i] = (uint8_t)(c < a.n_cls ? c : 255);
+  }
+  __syncthreads();
+  uint32_t pre[PRE];
+#pragma unroll
+  for (int k = 0; k < PRE; k++) pre[k] = cls[raw[k]];
+  const int ib = blockIdx.y * SPW;
+#pragma unroll 1
+  for (int i0 = ib; i0 < ib + SPW && i0 < a.n; i0 += SG) {
+    int cur[SG];
+    bool eos_ok[SG];
+    group_start<SG>(a, i0, v, len, -1, cur, eos_ok, [&](int i) { return a.states[i]; },
+                    [&](int, int s) { return a.complete[s] != 0; });
+    auto step = [&](int c) {
+#pragma unroll
+      for (int g = 0; g < SG; g++) {
+        if (cur[g] >= 0) {
+          const int nx = c < a.n_cls ? a.trans[(long long)cur[g] * a.n_cls + c] : -1;
+          cur[g] = nx < a.n_dfa ? nx : -1;
+        }
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < PRE; k++)
+      if (k < len) step((int)pre[k]);
+    for (int p = p0 + PRE; p < p0 + len; p++) step((int)cls[a.tok_bytes[p]]);
+    bool ok[SG];
+#pragma unroll
+    for (int g = 0; g < SG; g++) ok[g] = cur[g] >= 0 || eos_ok[g];
+    store_rows<SG>(a, i0, ok, [&](int i) { return a.rows[i]; });
+  }
+}
+
 }  // namespace maskb
 
+size_t mask_lds_table_bytes(int n_dfa, int n_cls) { return (size_t)(n_dfa + 1) * (size_t)(n_cls + 2) * 2; }
+
 hipError_t launch_mask_build(const MaskBuildArgs& a, hipStream_t st) {
-  const dim3 g((a.words * 32 + maskb::MT - 1) / maskb::MT, (a.n + maskb::SG - 1) / maskb::SG);
-  hipLaunchKernelGGL(maskb::build_kernel, g, dim3(maskb::MT), 0, st, a);
+  if (a.lds) {
+    constexpr int TPW = maskb::NSUB * maskb::MT;  // tokens per workgroup
+    const dim3 g((a.words * 32 + TPW - 1) / TPW, (a.n + maskb::SPWL - 1) / maskb::SPWL);
+    const size_t lds = 512 + mask_lds_table_bytes(a.n_dfa, a.n_cls);
+    hipLaunchKernelGGL(maskb::build_lds, g, dim3(maskb::MT), lds, st, a);
+  } else {
+    const dim3 g((a.words * 32 + maskb::MT - 1) / maskb::MT, (a.n + maskb::SPW - 1) / maskb::SPW);
+    hipLaunchKernelGGL(maskb::build_global, g, dim3(maskb::MT), 0, st, a);
+  }
   return hipGetLastError();
 }
 

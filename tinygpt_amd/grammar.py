@@ -254,6 +254,18 @@ class Dfa:
     def n(self) -> int:
         return self.trans.shape[0]
 
+    def byte_classes(self) -> tuple[np.ndarray, np.ndarray]:
+        """(byte_class uint8 [256], trans int32 [n, n_cls]): bytes whose
+        columns agree in every state share a class, numbered by first byte;
+        trans[s, byte_class[b]] == self.trans[s, b]."""
+        _, first, inv = np.unique(self.trans.T, axis=0, return_index=True, return_inverse=True)
+        order = np.argsort(first)  # class ids in order of their first byte
+        rank = np.empty_like(order)
+        rank[order] = np.arange(len(order))
+        byte_class = rank[inv.reshape(-1)].astype(np.uint8)
+        ctrans = np.ascontiguousarray(self.trans[:, np.sort(first)], dtype=np.int32)
+        return byte_class, ctrans
+
     def walk(self, state: int, data: bytes) -> int:
         """State after data from state, or -1 when a byte is rejected."""
         s = state

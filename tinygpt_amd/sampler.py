@@ -186,19 +186,21 @@ class Sampler:
         self._check(rc, "tgs_spec_verify")
         return n_acc, out
 
-    def mask_rows_from_dfa(self, trans, complete, tok_off, tok_bytes, states, rows, eos=-1, stream=None):
+    def mask_rows_from_dfa(self, byte_class, trans, complete, tok_off, tok_bytes, states, rows, eos=-1,
+                           stream=None):
         """Fills rows of the mask table on the device from a byte-level DFA
-        (see tinygpt_amd.grammar): trans int32 [n_dfa, 256], complete uint8
-        [n_dfa], tok_off int32 [V + 1], tok_bytes uint8, states / rows int32
-        [n] (device tensors).  The table must exist (set_mask_table)."""
+        (see tinygpt_amd.grammar, Dfa.byte_classes): byte_class uint8 [256],
+        trans int32 [n_dfa, n_cls], complete uint8 [n_dfa], tok_off int32
+        [V + 1], tok_bytes uint8, states / rows int32 [n] (device tensors).
+        The table must exist (set_mask_table)."""
         torch = _torch()
-        n_dfa = trans.shape[0]
+        n_dfa, n_cls = trans.shape
         V = tok_off.numel() - 1
         n = states.numel()
         st = stream if stream is not None else torch.cuda.current_stream(trans.device).cuda_stream
         rc = self._L.tgs_mask_rows_from_dfa(
-            self._h, _ptr(trans), _ptr(complete), n_dfa, _ptr(tok_off), _ptr(tok_bytes), V, int(eos),
-            _ptr(states), _ptr(rows), n, C.c_void_p(st),
+            self._h, _ptr(byte_class), _ptr(trans), n_cls, _ptr(complete), n_dfa, _ptr(tok_off), _ptr(tok_bytes),
+            V, int(eos), _ptr(states), _ptr(rows), n, C.c_void_p(st),
         )
         self._check(rc, "tgs_mask_rows_from_dfa")
 
