@@ -70,3 +70,42 @@ def test_tool_tag_rows_built_on_device(sampler, oracle):
         assert np.all(np.isneginf(got[i][~allowed]))
     assert (got[2 * n] == 0.0).all()  # the untouched last row still allows everything
     H.log("case mask build: ok")
+
+
+@pytest.mark.gpu
+def test_mask_build_rejects_bad_arguments(sampler):
+    """Argument errors are reported on the host, before any launch."""
+    import ctypes as C
+
+    import torch
+
+    from tinygpt_amd import grammar as G
+
+    d = G.compile_gbnf(G.PACE_TOOL_TAGS)
+    bc, ct = d.byte_classes()
+    toks = [b"", b"[", b"ab"]
+    off, data = G.token_csr(toks)
+    dev = "cuda:0"
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    dbc, dct, dcomp = T(bc), T(ct), T(d.complete.astype(np.uint8))
+    doff, ddata, dst, drow = T(off), T(data), T(np.zeros(1, np.int32)), T(np.zeros(1, np.int32))
+    sampler.set_mask_table(np.full((2, 1), 0xFFFFFFFF, np.uint32), len(toks))
+    L, h = sampler._L, sampler._h
+    p = lambda t: C.c_void_p(t.data_ptr())
+    ncls = ct.shape[1]
+
+    def call(byte_class=dbc, n_cls=ncls, n_dfa=d.n, n_tokens=len(toks), eos=-1, n=1):
+        return L.tgs_mask_rows_from_dfa(h, byte_class if byte_class is None else p(byte_class), p(dct), n_cls,
+                                        p(dcomp), n_dfa, p(doff), p(ddata), n_tokens, eos, p(dst), p(drow), n, None)
+
+    assert call() == 0
+    assert call(n_cls=0) == -1
+    assert call(n_cls=257) == -1
+    assert call(n_dfa=0) == -1
+    assert call(eos=len(toks)) == -1
+    assert call(eos=-2) == -1
+    assert call(n=-1) == -1
+    assert call(byte_class=None) == -1
+    assert call(n_tokens=100) != 0  # more tokens than the table's vocabulary
+    assert call(n=0) == 0
+    torch.cuda.synchronize()
