@@ -110,7 +110,8 @@ __device__ __forceinline__ void tok_bytes(const MaskBuildArgs& a, Tok& k) {
 // LDS and stored by adjacent lanes.
 __global__ __launch_bounds__(MT) void build_lds(MaskBuildArgs a) {
   TGS_DYN_SMEM(smem);
-  __shared__ int req_state[SPWL], req_row[SPWL];
+  __shared__ uint32_t req_start2[SPWL];  // byte offset of the state's row; the dead row if it has no walk
+  __shared__ int req_row[SPWL];
   __shared__ uint8_t req_complete[SPWL];
   __shared__ u64 words[SPWL][NSUB * MT / 64];  // [state][sub-chunk wave]
   uint16_t* cls2 = (uint16_t*)smem;             // [256] column byte offsets
@@ -122,12 +123,14 @@ __global__ __launch_bounds__(MT) void build_lds(MaskBuildArgs a) {
   tok_range(a, vb, cur_tok);
   tok_bytes(a, cur_tok);
   const int ib = blockIdx.y * SPWL;
-  if (t < SPWL) {  // this workgroup's requested states, their rows and completeness
+  if (t < SPWL) {  // this workgroup's requested states: walk start, row, completeness
     const int i = ib + t;
     const int s = i < a.n ? a.states[i] : -1;
-    req_state[t] = s;
+    const bool in = s >= 0 && s < a.n_dfa;
+    const bool comp = in && a.complete[s];
+    req_start2[t] = (uint32_t)((in && !comp ? s : dead) * W * 2);
     req_row[t] = i < a.n ? a.rows[i] : -1;
-    req_complete[t] = (s >= 0 && s < a.n_dfa) ? a.complete[s] : 0;
+    req_complete[t] = comp;
   }
   for (int i = t; i < 256; i += MT) {
     const int c = a.byte_class[i];
@@ -182,15 +185,17 @@ __global__ __launch_bounds__(MT) void build_lds(MaskBuildArgs a) {
 #pragma unroll
     for (int k = 0; k < PRE; k++) pc[k] = k < len ? (uint32_t)cls2[cur_tok.raw[k]] : stay2;
     const int lmax = __builtin_amdgcn_readfirstlane(wave_max(len < PRE ? len : PRE));  // steps this wave needs
+    const bool walks = v < a.n_tokens && len > 0;
+    const bool is_eos = v == a.eos;  // eos < n_tokens
 #pragma unroll 1
     for (int i0 = ib; i0 < ib + SPWL && i0 < a.n; i0 += SGL) {
-      int st[SGL];
-      bool eos_ok[SGL];
-      group_start<SGL>(a, i0, v, len, dead, st, eos_ok, [&](int i) { return req_state[i - ib]; },
-                       [&](int i, int) { return req_complete[i - ib] != 0; });
       uint32_t cur[SGL];
+      bool eos_ok[SGL];
 #pragma unroll
-      for (int g = 0; g < SGL; g++) cur[g] = (uint32_t)(st[g] * W * 2);
+      for (int g = 0; g < SGL; g++) {  // slots past the request count start dead, not complete
+        cur[g] = walks ? req_start2[i0 - ib + g] : dead2;
+        eos_ok[g] = is_eos && req_complete[i0 - ib + g];
+      }
 #pragma unroll
       for (int k = 0; k < PRE; k++) {
         if (k < lmax) {
