@@ -408,7 +408,7 @@ TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
 KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c3": "topp_kernel<float, true>",
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
-           "lp": "lp::chunk_kernel<float>", "mask": "maskb::build_lds"}
+           "lp": "lp::chunk_kernel<float>", "mask": "maskb::prep_image + maskb::build_lds (one call)"}
 
 
 def main():

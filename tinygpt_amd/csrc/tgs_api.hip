@@ -411,7 +411,13 @@ int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int3
   a.n_cls = n_cls;
   a.complete = d_complete;
   a.n_dfa = n_dfa;
-  a.lds = tgs::mask_lds_table_bytes(n_dfa, n_cls) <= (size_t)tgs::MASK_LDS_TABLE;  // 16-bit offsets fit
+  // LDS path: the 16-bit table fits LDS (and its offsets 16 bits) and its image fits the
+  // handle's workspace, where it is prepared once per call (calls on one handle are ordered
+  // on one stream)
+  const size_t ws_bytes = sizeof(unsigned long long) * (size_t)h->ws_rows * tgs::KMAX;
+  a.lds = tgs::mask_lds_table_bytes(n_dfa, n_cls) <= (size_t)tgs::MASK_LDS_TABLE &&
+          tgs::mask_image_bytes(n_dfa, n_cls) <= ws_bytes;
+  a.image = (uint16_t*)h->ws;
   a.tok_off = d_tok_off;
   a.tok_bytes = d_tok_bytes;
   a.n_tokens = n_tokens;

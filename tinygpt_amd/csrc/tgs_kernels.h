@@ -74,6 +74,7 @@ struct MaskBuildArgs {
   const uint8_t* complete;    // [n_dfa] accepting with no way on
   int n_dfa;
   int lds;                    // 1: the table fits LDS (16-bit row offsets, dead state, reject and stay columns)
+  uint16_t* image;            // with lds: the LDS image (class offsets, then the table), written per call
   const int* tok_off;        // [n_tokens + 1]
   const uint8_t* tok_bytes;
   int n_tokens;
@@ -85,7 +86,14 @@ struct MaskBuildArgs {
   int n_rows, words;         // its rows and words per row
 };
 hipError_t launch_mask_build(const MaskBuildArgs& a, hipStream_t st);
-size_t mask_lds_table_bytes(int n_dfa, int n_cls);  // 16-bit table with the dead state, reject and stay columns
+// The 16-bit table with the dead state, reject and stay columns, and the LDS
+// image (512 bytes of class offsets, then the table, in whole 16 bytes).
+__host__ __device__ inline size_t mask_lds_table_bytes(int n_dfa, int n_cls) {
+  return (size_t)(n_dfa + 1) * (size_t)(n_cls + 2) * 2;
+}
+__host__ __device__ inline size_t mask_image_bytes(int n_dfa, int n_cls) {
+  return (512 + mask_lds_table_bytes(n_dfa, n_cls) + 15) / 16 * 16;
+}
 
 // Token log-probabilities (tgs_logprob.hip).
 constexpr int LP_NT = 256;

@@ -105,6 +105,33 @@ __device__ __forceinline__ void tok_bytes(const MaskBuildArgs& a, Tok& k) {
   for (int j = 0; j < PRE; j++) k.raw[j] = j < k.len ? a.tok_bytes[k.p0 + j] : 0u;
 }
 
+// The LDS image, once per call: entry i < 256 is the column offset of byte
+// i's class (the reject column for a class outside the table), entry
+// 256 + s W + c the byte offset of the row of state s's successor under
+// column c (the dead row for a rejection; s itself for `stay`).
+__global__ __launch_bounds__(MT) void prep_image(MaskBuildArgs a) {
+  const int W = a.n_cls + 2, dead = a.n_dfa;
+  const int i = blockIdx.x * MT + (int)threadIdx.x;
+  const int n = 256 + (a.n_dfa + 1) * W;
+  if (i >= n) return;
+  if (i < 256) {
+    const int c = a.byte_class[i];
+    a.image[i] = (uint16_t)(2 * (c < a.n_cls ? c : a.n_cls));
+    return;
+  }
+  const int j = i - 256, s = j / W, c = j - s * W;
+  int nx = dead;
+  if (s < a.n_dfa) {
+    if (c < a.n_cls) {
+      const int q = a.trans[(long long)s * a.n_cls + c];
+      nx = (q >= 0 && q < a.n_dfa) ? q : dead;
+    } else if (c == a.n_cls + 1) {
+      nx = s;
+    }
+  }
+  a.image[i] = (uint16_t)(nx * W * 2);
+}
+
 // Workgroup (NSUB * MT tokens, SPWL requested states): every row it writes
 // gets NSUB * MT / 32 consecutive words (whole 128-byte lines), staged in
 // LDS and stored by adjacent lanes.
@@ -132,42 +159,18 @@ __global__ __launch_bounds__(MT) void build_lds(MaskBuildArgs a) {
     req_row[t] = i < a.n ? a.rows[i] : -1;
     req_complete[t] = comp;
   }
-  for (int i = t; i < 256; i += MT) {
-    const int c = a.byte_class[i];
-    cls2[i] = (uint16_t)(2 * (c < a.n_cls ? c : a.n_cls));
-  }
-  // The table: thread -> (first row, column) once, rows in steps of rpi;
-  // FB rows' loads are issued before any is used (an L2 round trip per
-  // batch, not per entry).
-  auto entry = [&](int s, int c, int q) {
-    int nx = dead;
-    if (s < a.n_dfa) {
-      if (c < a.n_cls) nx = (q >= 0 && q < a.n_dfa) ? q : dead;
-      else if (c == a.n_cls + 1) nx = s;
-    }
-    ((uint16_t*)tab)[s * W + c] = (uint16_t)(nx * W * 2);
-  };
-  if (W <= MT) {
-    const int rpi = MT / W;
-    const int r0 = t / W, c = t - r0 * W;
-    if (r0 < rpi) {
-      for (int s0 = r0; s0 <= a.n_dfa; s0 += FB * rpi) {
-        int q[FB];
+  {  // the LDS image (class offsets, then the table), four 16-byte loads in flight per thread
+    const int nvec = (int)(mask_image_bytes(a.n_dfa, a.n_cls) / 16);
+    const uint4* src = (const uint4*)a.image;
+    uint4* dst = (uint4*)smem;
+    for (int i0 = t; i0 < nvec; i0 += 4 * MT) {
+      uint4 x[4];
 #pragma unroll
-        for (int j = 0; j < FB; j++) {
-          const int s = s0 + j * rpi;
-          q[j] = (s < a.n_dfa && c < a.n_cls) ? a.trans[(long long)s * a.n_cls + c] : -1;
-        }
+      for (int u = 0; u < 4; u++) x[u] = i0 + u * MT < nvec ? src[i0 + u * MT] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-        for (int j = 0; j < FB; j++) {
-          const int s = s0 + j * rpi;
-          if (s <= a.n_dfa) entry(s, c, q[j]);
-        }
-      }
+      for (int u = 0; u < 4; u++)
+        if (i0 + u * MT < nvec) dst[i0 + u * MT] = x[u];
     }
-  } else {  // more than MT columns: one row at a time
-    for (int s = 0; s <= a.n_dfa; s++)
-      for (int c = t; c < W; c += MT) entry(s, c, (s < a.n_dfa && c < a.n_cls) ? a.trans[(long long)s * a.n_cls + c] : -1);
   }
   __syncthreads();
   const uint32_t stay2 = 2u * (uint32_t)(a.n_cls + 1);
@@ -280,14 +283,13 @@ __global__ __launch_bounds__(MT) void build_global(MaskBuildArgs a) {
 
 }  // namespace maskb
 
-size_t mask_lds_table_bytes(int n_dfa, int n_cls) { return (size_t)(n_dfa + 1) * (size_t)(n_cls + 2) * 2; }
-
 hipError_t launch_mask_build(const MaskBuildArgs& a, hipStream_t st) {
   if (a.lds) {
     constexpr int TPW = maskb::NSUB * maskb::MT;  // tokens per workgroup
     const dim3 g((a.words * 32 + TPW - 1) / TPW, (a.n + maskb::SPWL - 1) / maskb::SPWL);
-    const size_t lds = 512 + mask_lds_table_bytes(a.n_dfa, a.n_cls);
-    hipLaunchKernelGGL(maskb::build_lds, g, dim3(maskb::MT), lds, st, a);
+    const int n_img = 256 + (a.n_dfa + 1) * (a.n_cls + 2);
+    hipLaunchKernelGGL(maskb::prep_image, dim3((n_img + maskb::MT - 1) / maskb::MT), dim3(maskb::MT), 0, st, a);
+    hipLaunchKernelGGL(maskb::build_lds, g, dim3(maskb::MT), mask_image_bytes(a.n_dfa, a.n_cls), st, a);
   } else {
     const dim3 g((a.words * 32 + maskb::MT - 1) / maskb::MT, (a.n + maskb::SPW - 1) / maskb::SPW);
     hipLaunchKernelGGL(maskb::build_global, g, dim3(maskb::MT), 0, st, a);
