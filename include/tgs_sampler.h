@@ -186,7 +186,9 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
  * table).  The table (tgs_mask_table_set) must hold at least n_tokens ids;
  * bits of ids at or past n_tokens are cleared.  Rows outside the table are
  * skipped; a next state outside [0, n_dfa) rejects.  At most 1,048,560 pairs
- * per call; the inputs must stay alive until the stream reaches the call. */
+ * per call; the inputs must stay alive until the stream reaches the call.
+ * Uses the handle's workspace (like every call on the handle: order calls on
+ * one stream); allocates nothing. */
 int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int32_t* d_trans, int n_cls,
                            const uint8_t* d_complete, int n_dfa, const int32_t* d_tok_off,
                            const uint8_t* d_tok_bytes, int n_tokens, int eos_id, const int32_t* d_states,
