@@ -44,6 +44,18 @@ def test_general_and_full_kernels(sim, oracle):
     _check(sim, oracle, x, params, u, hist, hist_len)
 
 
+def test_gpu_skipped_batch_v256(sim, oracle):
+    """The exact batch of the GPU test test_random_rows[256] (rng 500 + 256,
+    B=64, history 64, no hint: chunk, merge, full-path and top-p kernels),
+    which is skipped on the GPU because an earlier kernel layout faulted on
+    it.  Every access of the current kernels on it is bounds checked here."""
+    from test_gpu_sampler import _random_batch
+
+    x, params, u, hist, hist_len = _random_batch(np.random.default_rng(500 + 256), 64, 256, oracle)
+    r, _, _ = _check(sim, oracle, x, params, u, hist, hist_len)
+    assert len(r["launches"]) >= 3  # chunk, full and top-p kernels all ran
+
+
 def test_fast_kernel_with_hint(sim, oracle):
     import tinygpt_amd as tg
 

@@ -97,14 +97,14 @@ void free_spec(tgs_ctx* h) {
 // beyond that about two workgroups per CU with chunks of at least 2048
 // ids.  TGS_SPLIT raises the split (tuning).
 constexpr int kK64Tile = tgs::K64_TILE;
-int choose_split_k64(const tgs_ctx* h, int B, int V) {
+int choose_split_k64(int num_cu, int B, int V) {
   const int smin = (V + kK64Tile - 1) / kK64Tile;
   int S;
   const char* env = std::getenv("TGS_SPLIT");
   if (env && std::atoi(env) > 0) {
     S = std::min(std::atoi(env), kMaxSplit);
   } else {
-    const long long target = 2LL * h->num_cu;
+    const long long target = 2LL * num_cu;
     S = (int)std::min<long long>(kMaxSplit, std::max<long long>(1, (target + B - 1) / B));
     while (S > 1 && (V + S - 1) / S < 2048) S--;
   }
@@ -113,18 +113,155 @@ int choose_split_k64(const tgs_ctx* h, int B, int V) {
 
 // Chunks per row: about four workgroups per CU, chunks of at least one
 // 8192-id tile, at most kMaxSplit.  TGS_SPLIT overrides (tuning).
-int choose_split(const tgs_ctx* h, int B, int V) {
+int choose_split(int num_cu, int ws_rows, int B, int V) {
   const int tile = 8192;
   int S = 1;
   const char* env = std::getenv("TGS_SPLIT");
   if (env && std::atoi(env) > 0) {
     S = std::min(std::atoi(env), kMaxSplit);
   } else {
-    const int target = 4 * h->num_cu;
+    const int target = 4 * num_cu;
     while (S * 2 <= kMaxSplit && (long long)S * 2 * B <= target && (V + S * 2 - 1) / (S * 2) >= tile / 2) S *= 2;
   }
-  while (S > 1 && (long long)S * B > h->ws_rows) S >>= 1;
+  while (S > 1 && (long long)S * B > ws_rows) S >>= 1;
   return S;
+}
+
+// What a sampling call launches with: the device's size, and the workspace
+// and mask table it uses (a handle's allocations, or the allocation-free
+// entry point's static scratch and the caller's table).
+struct SampleRes {
+  int num_cu = 256;
+  size_t lds_limit = 65536;
+  unsigned long long* ws = nullptr;  // [ws_rows][KMAX] general-path chunk lists
+  int* ws_cnt = nullptr;             // [ws_rows * (KMAX / 64)]
+  int ws_rows = 0;
+  unsigned* k64_cnt = nullptr;              // [rows * K64_CNT_STRIDE], zero between calls
+  unsigned long long* k64_lists = nullptr;  // [rows * kMaxSplit][64], all ~0 between calls
+  const uint32_t* mask_table = nullptr;     // nullptr: no table
+  int n_states = 0, mask_words = 0;
+};
+
+int efail(std::string& err, int code, const std::string& msg) {
+  err = msg;
+  return code;
+}
+
+// Validates the call and launches the kernels the batch hint selects (the
+// body of tgs_sample, shared with tgs_sample_noalloc).  The device must be
+// current; B, V and hist_cap must be within what res was sized for.
+int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tgs_dtype dt, int B, int V,
+                int64_t row_stride, const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
+                const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids, const tgs_batch_hint* hint,
+                const tgs_debug* dbg, hipStream_t stream) {
+  if (dt != TGS_F32 && dt != TGS_BF16) return efail(err, TGS_EINVAL, "dtype");
+  if (B < 0 || V < 1 || row_stride < V) return efail(err, TGS_EINVAL, "shape");
+  if (B == 0) return TGS_OK;
+  if (hist_cap < 0 || (hist_cap > 0 && !d_hist)) return efail(err, TGS_EINVAL, "history");
+  if (!d_logits || !d_params || !d_u || !d_out_ids) return efail(err, TGS_EINVAL, "null buffer");
+  tgs_debug dz;
+  std::memset(&dz, 0, sizeof(dz));
+  if (dbg) {
+    dz = *dbg;
+    if (dz.kept_cap < 0 || ((dz.kept_ids || dz.kept_probs) && dz.kept_cap == 0))
+      return efail(err, TGS_EINVAL, "debug kept_cap");
+  }
+  const size_t esz = dt == TGS_BF16 ? 2 : 4;
+  tgs::SampleArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.logits = d_logits;
+  a.row_stride = row_stride;
+  a.B = B;
+  a.V = V;
+  a.aligned = ((uintptr_t)d_logits % 16 == 0) && (((uint64_t)row_stride * esz) % 16 == 0);
+  a.whole_vec = a.aligned && ((uint64_t)V * esz) % 16 == 0;
+  a.hist = d_hist;
+  a.hist_len = d_hist_len;
+  a.hist_cap = hist_cap;
+  a.params = d_params;
+  a.u = d_u;
+  a.out = d_out_ids;
+  a.mask_table = res.mask_table;
+  a.n_states = res.mask_table ? res.n_states : 0;
+  a.mask_words = res.mask_words;
+  a.ws = res.ws;
+  a.ws_cnt = res.ws_cnt;
+  a.cnt = res.k64_cnt;
+  a.lists = res.k64_lists;
+  a.dbg = dz;
+  // Kernels: the fused top_k <= 64 kernel when the hint says every row is
+  // greedy or has top_k <= 64; otherwise the chunk kernel (+ merge kernel
+  // for split rows), plus the full-path kernel when the hint allows rows
+  // without a usable top-k.
+  const int mk = hint ? hint->max_top_k : 0x7FFFFFFF;
+  a.hint_k = mk;
+  a.TS = hist_cap > 0 ? next_pow2(std::max(64, 2 * hist_cap)) : 0;
+  a.ts_shift = a.TS ? 32 - log2i(a.TS) : 0;
+  if (mk <= 64 && mk < V && hist_cap <= tgs::K64_MAX_HIST) {
+    a.full_rows = 0;
+    const int S = choose_split_k64(res.num_cu, B, V);
+    // whole tiles when the split allows them (their loads need no checks)
+    const int L = S == (V + kK64Tile - 1) / kK64Tile ? kK64Tile
+                                                     : std::min(kK64Tile, ((V + S - 1) / S + 63) / 64 * 64);
+    a.S = (V + L - 1) / L;
+    a.L = L;
+    a.BW = tgs::K64_BITMAP_WORDS;
+    a.off_hash = 0;                             // 16-bit history count per id of a tile
+    a.off_bitmap = tgs::K64_TILE / 2 * 4;       // history bitmap of a tile
+    a.off_cand = a.off_bitmap + a.BW * 4;       // candidate staging (16-byte aligned)
+    a.capt = tgs::K64_CAP;
+    a.ws_stride = 64;
+    const size_t lds = (size_t)a.off_cand + (size_t)tgs::K64_CAND_ENTRIES * 8;
+    if (lds + sizeof(tgs::BlockScratch) + 4096 > res.lds_limit)
+      return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS");
+    hipError_t e = tgs::launch_k64(a, dt, lds, stream);
+    if (e != hipSuccess) return efail(err, TGS_EHIP, std::string("sample kernel launch: ") + hipGetErrorString(e));
+    return TGS_OK;
+  }
+  if (mk <= tgs::KMAX && mk < V && V <= tgs::topk_max_vocab(dt) && a.whole_vec && hist_cap <= tgs::KMAX &&
+      tgs::topk_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) <= res.lds_limit) {
+    // every row greedy or 1 <= top_k <= KMAX, the row fits in registers: one
+    // workgroup per row
+    a.full_rows = 0;
+    a.S = 1;
+    a.L = V;
+    hipError_t e = tgs::launch_topk(a, dt, tgs::topk_lds_bytes(V, a.TS), stream);
+    if (e != hipSuccess) return efail(err, TGS_EHIP, std::string("sample kernel launch: ") + hipGetErrorString(e));
+    return TGS_OK;
+  }
+  const int mink = hint ? hint->min_top_k : 0;
+  if (mk >= V && mink >= V && tgs::topp_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) <= res.lds_limit) {
+    // every sampling row without a usable top-k: the top-p kernel serves the
+    // batch alone, greedy rows included (one workgroup per row)
+    a.full_rows = 1;
+    a.topp_all = 1;
+    a.S = 1;
+    a.L = V;
+    a.topp_cap = tgs::topp_pack_cap(V, a.TS, res.lds_limit - 2 * sizeof(tgs::BlockScratch));
+    hipError_t e = tgs::launch_topp(a, dt, stream);
+    if (e != hipSuccess) return efail(err, TGS_EHIP, std::string("sample kernel launch: ") + hipGetErrorString(e));
+    return TGS_OK;
+  }
+  a.full_rows = (mk > tgs::KMAX || mk >= V) ? 1 : 0;
+  const int S = choose_split(res.num_cu, res.ws_rows, B, V);
+  const int L = S > 1 ? ((V + S - 1) / S + 1023) / 1024 * 1024 : V;
+  a.ws_stride = tgs::KMAX;
+  a.S = (V + L - 1) / L;
+  a.L = L;
+  a.BW = hist_cap > 0 ? (L + 31) / 32 : 0;
+  a.capt = tgs::CAPB + hist_cap;
+  a.off_hash = 0;
+  a.off_bitmap = a.TS * 8;
+  a.off_cand = (a.off_bitmap + a.BW * 4 + 15) / 16 * 16;
+  const size_t lds = (size_t)a.off_cand + (size_t)a.capt * 8;
+  if (lds + sizeof(tgs::BlockScratch) > res.lds_limit)
+    return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS");
+  if (a.full_rows && tgs::topp_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) > res.lds_limit)
+    return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS (top-p rows)");
+  a.topp_cap = tgs::topp_pack_cap(V, a.TS, res.lds_limit - 2 * sizeof(tgs::BlockScratch));
+  hipError_t e = tgs::launch_sample(a, dt, lds, stream);
+  if (e != hipSuccess) return efail(err, TGS_EHIP, std::string("sample kernel launch: ") + hipGetErrorString(e));
+  return TGS_OK;
 }
 
 }  // namespace
@@ -277,115 +414,22 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   if (B == 0) return TGS_OK;
   if (B > h->max_batch || V > h->max_vocab || hist_cap > h->max_hist)
     return fail(h, TGS_ETOOBIG, "batch, vocab or history beyond the handle's limits");
-  if (hist_cap < 0 || (hist_cap > 0 && !d_hist)) return fail(h, TGS_EINVAL, "history");
-  if (!d_logits || !d_params || !d_u || !d_out_ids) return fail(h, TGS_EINVAL, "null buffer");
-  tgs_debug dz;
-  std::memset(&dz, 0, sizeof(dz));
-  if (dbg) {
-    dz = *dbg;
-    if (dz.kept_cap < 0 || ((dz.kept_ids || dz.kept_probs) && dz.kept_cap == 0))
-      return fail(h, TGS_EINVAL, "debug kept_cap");
-  }
   DeviceGuard g(h->device);
   if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
-
-  const size_t esz = dt == TGS_BF16 ? 2 : 4;
-  tgs::SampleArgs a;
-  std::memset(&a, 0, sizeof(a));
-  a.logits = d_logits;
-  a.row_stride = row_stride;
-  a.B = B;
-  a.V = V;
-  a.aligned = ((uintptr_t)d_logits % 16 == 0) && (((uint64_t)row_stride * esz) % 16 == 0);
-  a.whole_vec = a.aligned && ((uint64_t)V * esz) % 16 == 0;
-  a.hist = d_hist;
-  a.hist_len = d_hist_len;
-  a.hist_cap = hist_cap;
-  a.params = d_params;
-  a.u = d_u;
-  a.out = d_out_ids;
+  SampleRes res;
+  res.num_cu = h->num_cu;
+  res.lds_limit = h->lds_limit;
+  res.ws = h->ws;
+  res.ws_cnt = h->ws_cnt;
+  res.ws_rows = h->ws_rows;
+  res.k64_cnt = h->k64_cnt;
+  res.k64_lists = h->k64_lists;
   const bool table_ok = h->mask_table && h->mask_vocab >= V;
-  a.mask_table = table_ok ? h->mask_table : nullptr;
-  a.n_states = table_ok ? h->n_states : 0;
-  a.mask_words = h->mask_words;
-  a.ws = h->ws;
-  a.ws_cnt = h->ws_cnt;
-  a.cnt = h->k64_cnt;
-  a.lists = h->k64_lists;
-  a.dbg = dz;
-  // Kernels: the fused top_k <= 64 kernel when the hint says every row is
-  // greedy or has top_k <= 64; otherwise the chunk kernel (+ merge kernel
-  // for split rows), plus the full-path kernel when the hint allows rows
-  // without a usable top-k.
-  const int mk = hint ? hint->max_top_k : 0x7FFFFFFF;
-  a.hint_k = mk;
-  a.TS = hist_cap > 0 ? next_pow2(std::max(64, 2 * hist_cap)) : 0;
-  a.ts_shift = a.TS ? 32 - log2i(a.TS) : 0;
-  if (mk <= 64 && mk < V && hist_cap <= tgs::K64_MAX_HIST) {
-    a.full_rows = 0;
-    const int S = choose_split_k64(h, B, V);
-    // whole tiles when the split allows them (their loads need no checks)
-    const int L = S == (V + kK64Tile - 1) / kK64Tile ? kK64Tile
-                                                     : std::min(kK64Tile, ((V + S - 1) / S + 63) / 64 * 64);
-    a.S = (V + L - 1) / L;
-    a.L = L;
-    a.BW = tgs::K64_BITMAP_WORDS;
-    a.off_hash = 0;                             // 16-bit history count per id of a tile
-    a.off_bitmap = tgs::K64_TILE / 2 * 4;       // history bitmap of a tile
-    a.off_cand = a.off_bitmap + a.BW * 4;       // candidate staging (16-byte aligned)
-    a.capt = tgs::K64_CAP;
-    a.ws_stride = 64;
-    const size_t lds = (size_t)a.off_cand + (size_t)tgs::K64_CAND_ENTRIES * 8;
-    if (lds + sizeof(tgs::BlockScratch) + 4096 > h->lds_limit)
-      return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
-    hipError_t e = tgs::launch_k64(a, dt, lds, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
-    return TGS_OK;
-  }
-  if (mk <= tgs::KMAX && mk < V && V <= tgs::topk_max_vocab(dt) && a.whole_vec && hist_cap <= tgs::KMAX &&
-      tgs::topk_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) <= h->lds_limit) {
-    // every row greedy or 1 <= top_k <= KMAX, the row fits in registers: one
-    // workgroup per row
-    a.full_rows = 0;
-    a.S = 1;
-    a.L = V;
-    hipError_t e = tgs::launch_topk(a, dt, tgs::topk_lds_bytes(V, a.TS), (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
-    return TGS_OK;
-  }
-  const int mink = hint ? hint->min_top_k : 0;
-  if (mk >= V && mink >= V && tgs::topp_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) <= h->lds_limit) {
-    // every sampling row without a usable top-k: the top-p kernel serves the
-    // batch alone, greedy rows included (one workgroup per row)
-    a.full_rows = 1;
-    a.topp_all = 1;
-    a.S = 1;
-    a.L = V;
-    a.topp_cap = tgs::topp_pack_cap(V, a.TS, h->lds_limit - 2 * sizeof(tgs::BlockScratch));
-    hipError_t e = tgs::launch_topp(a, dt, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
-    return TGS_OK;
-  }
-  a.full_rows = (mk > tgs::KMAX || mk >= V) ? 1 : 0;
-  const int S = choose_split(h, B, V);
-  const int L = S > 1 ? ((V + S - 1) / S + 1023) / 1024 * 1024 : V;
-  a.ws_stride = tgs::KMAX;
-  a.S = (V + L - 1) / L;
-  a.L = L;
-  a.BW = hist_cap > 0 ? (L + 31) / 32 : 0;
-  a.capt = tgs::CAPB + hist_cap;
-  a.off_hash = 0;
-  a.off_bitmap = a.TS * 8;
-  a.off_cand = (a.off_bitmap + a.BW * 4 + 15) / 16 * 16;
-  const size_t lds = (size_t)a.off_cand + (size_t)a.capt * 8;
-  if (lds + sizeof(tgs::BlockScratch) > h->lds_limit)
-    return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS");
-  if (a.full_rows && tgs::topp_lds_bytes(V, a.TS) + 2 * sizeof(tgs::BlockScratch) > h->lds_limit)
-    return fail(h, TGS_ETOOBIG, "history / vocab too large for LDS (top-p rows)");
-  a.topp_cap = tgs::topp_pack_cap(V, a.TS, h->lds_limit - 2 * sizeof(tgs::BlockScratch));
-  hipError_t e = tgs::launch_sample(a, dt, lds, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(h, e, "sample kernel launch");
-  return TGS_OK;
+  res.mask_table = table_ok ? h->mask_table : nullptr;
+  res.n_states = table_ok ? h->n_states : 0;
+  res.mask_words = h->mask_words;
+  return sample_core(res, h->err, d_logits, dt, B, V, row_stride, d_hist, d_hist_len, hist_cap, d_params, d_u,
+                     d_out_ids, hint, dbg, (hipStream_t)stream);
 }
 
 int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int32_t* d_trans, int n_cls,

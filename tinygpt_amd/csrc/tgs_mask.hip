@@ -82,7 +82,6 @@ __device__ __forceinline__ void group_start(const MaskBuildArgs& a, int i0, int 
 // bytes, so offsets fit 16 bits.  The class map holds byte offsets of
 // columns.  Workgroup (token chunk, SPW requested states).
 constexpr int SGL = 16;         // states walked together in the LDS kernel
-constexpr int FB = 16;          // table loads issued together in the fill
 constexpr int NSUB = MASK_NSUB; // 256-token sub-chunks per LDS-kernel workgroup
 constexpr int SPWL = MASK_SPW_LDS;
 static_assert(SPWL % SGL == 0, "whole groups per workgroup");
