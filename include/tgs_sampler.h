@@ -127,6 +127,8 @@ int tgs_hint_from_params(const tgs_row_params* host_params, int B, int V, tgs_ba
  * every later call (workspace is sized once here; calls never allocate). */
 int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int max_hist);
 void tgs_destroy(tgs_handle h);
+/* Message of the handle's last error; NULL: the calling thread's last
+ * tgs_sample_noalloc error ("null handle" when there is none). */
 const char* tgs_last_error(tgs_handle h);
 
 /* Grammar mask table: n_states rows of ceil(vocab/32) uint32 words; bit v
@@ -150,6 +152,26 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
                const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
                const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids,
                const tgs_batch_hint* hint, const tgs_debug* dbg, tgs_stream stream);
+
+/* tgs_sample without a handle, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  It has no counterpart in the reference: the reference
+ * samples inline in Swift/MLX.  Same arguments, kernels and results as
+ * tgs_sample; the mask table is passed in (d_mask_table: n_states rows of
+ * ceil(mask_vocab / 32) words, mask_vocab >= V; NULL / 0 for none).  Its
+ * workspace is a static device array of about 6 MiB that every GPU the
+ * library runs on holds until the process ends; the first call on a device
+ * also prepares that array (and synchronises the device once).  Limits:
+ * B <= 256, V <= 262144, hist_cap <= 1024; beyond them it returns
+ * TGS_ETOOBIG.  It calls no hipMalloc or hipFree.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (several streams,
+ * several threads) race and must be ordered by the caller.  Errors:
+ * tgs_last_error(NULL) gives the calling thread's last message. */
+int tgs_sample_noalloc(int device, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
+                       const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
+                       const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids,
+                       const uint32_t* d_mask_table, int n_states, int mask_vocab, const tgs_batch_hint* hint,
+                       const tgs_debug* dbg, tgs_stream stream);
 
 /* Size the speculative-verification workspace for up to max_batch sequences
  * of up to max_k draft tokens (allocates; call once before capturing

@@ -59,10 +59,21 @@ int main(int argc, char** argv) {
     tgs_debug dbg = {kid.data(), kpr.data(), kept_cap, counts.data(), mass.data(), cut.data(),
                      post ? postv.data() : nullptr};
     tgs_batch_hint hb = {hint, hint_min};
-    rc = tgs_sample(h, logits.data(), (tgs_dtype)dtype, B, V, stride, hist_cap ? (const int32_t*)hist.data() : nullptr,
-                    has_len ? (const int32_t*)hlen.data() : nullptr, hist_cap, (const tgs_row_params*)params.data(),
-                    (const float*)u.data(), out.data(), hint >= 0 ? &hb : nullptr, &dbg, nullptr);
-    if (rc) { std::printf("sample %d %s\n", rc, tgs_last_error(h)); return 7; }
+    if (std::getenv("TGS_SIM_NOALLOC")) {  // the allocation-free entry point (static workspace)
+      rc = tgs_sample_noalloc(0, logits.data(), (tgs_dtype)dtype, B, V, stride,
+                              hist_cap ? (const int32_t*)hist.data() : nullptr,
+                              has_len ? (const int32_t*)hlen.data() : nullptr, hist_cap,
+                              (const tgs_row_params*)params.data(), (const float*)u.data(), out.data(),
+                              n_states > 0 ? (const uint32_t*)mask.data() : nullptr, n_states, V,
+                              hint >= 0 ? &hb : nullptr, &dbg, nullptr);
+      if (rc) { std::printf("sample_noalloc %d %s\n", rc, tgs_last_error(nullptr)); return 7; }
+    } else {
+      rc = tgs_sample(h, logits.data(), (tgs_dtype)dtype, B, V, stride,
+                      hist_cap ? (const int32_t*)hist.data() : nullptr,
+                      has_len ? (const int32_t*)hlen.data() : nullptr, hist_cap, (const tgs_row_params*)params.data(),
+                      (const float*)u.data(), out.data(), hint >= 0 ? &hb : nullptr, &dbg, nullptr);
+      if (rc) { std::printf("sample %d %s\n", rc, tgs_last_error(h)); return 7; }
+    }
     dump(dir + "/out_ids.bin", out.data(), out.size() * 4);
     dump(dir + "/out_kept_ids.bin", kid.data(), kid.size() * 4);
     dump(dir + "/out_kept_probs.bin", kpr.data(), kpr.size() * 4);

@@ -19,8 +19,9 @@ def build():
 
 
 def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=None, kept_cap=64,
-               post=True, hint=None, split=None, timeout=600):
-    """hint: None (general kernel) or an int max_top_k."""
+               post=True, hint=None, split=None, timeout=600, noalloc=False):
+    """hint: None (general kernel) or an int max_top_k.  noalloc: through
+    tgs_sample_noalloc (static workspace) instead of a handle."""
     B = logits.shape[0]
     V = logits.shape[1] if V is None else V
     dtype = 1 if logits.dtype == np.uint16 else 0
@@ -44,6 +45,8 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
         env = dict(os.environ)
         if split is not None:
             env["TGS_SPLIT"] = str(split)
+        if noalloc:
+            env["TGS_SIM_NOALLOC"] = "1"
         env.setdefault("ASAN_OPTIONS", "detect_leaks=0:abort_on_error=0")
         env.setdefault("UBSAN_OPTIONS", "halt_on_error=1:print_stacktrace=1")
         env["TGS_SIM_TRACE"] = "1"

@@ -92,3 +92,20 @@ def test_library_has_no_cpu_sampling_path():
     api = open(os.path.join(ROOT, "tinygpt_amd", "csrc", "tgs_api.hip")).read()
     for needle in ("tg_expf", "tg_q40", "qsort", "nth_element", "oracle"):
         assert needle not in api
+
+
+def test_noalloc_rejects_sizes_beyond_its_workspace(lib):
+    """tgs_sample_noalloc checks its fixed limits before any device work."""
+    import ctypes as C
+
+    p = C.c_void_p(16)  # never dereferenced: the call returns before any launch
+    args = lambda B, V, hc: (0, p, 0, B, V, V, p, None, hc, p, p, p, None, 0, 0, None, None, None)
+    assert lib.tgs_sample_noalloc(*args(257, 1000, 0)) == -5
+    assert b"at most 256 rows" in lib.tgs_last_error(None)
+    assert lib.tgs_sample_noalloc(*args(4, 262145, 0)) == -5
+    assert lib.tgs_sample_noalloc(*args(4, 1000, 1025)) == -5
+    assert lib.tgs_sample_noalloc(0, p, 0, 4, 1000, 1000, None, None, 0, p, p, p, None, 3, 1000, None, None,
+                                  None) == -1  # a table needs its pointer
+    assert lib.tgs_sample_noalloc(0, p, 5, 4, 1000, 1000, None, None, 0, p, p, p, None, 0, 0, None, None,
+                                  None) == -1  # dtype
+    assert lib.tgs_sample_noalloc(*args(0, 1000, 0)) == 0  # empty batch: nothing to do

@@ -32,8 +32,10 @@ def _batch(seed, B, V, oracle):
     return _random_batch(np.random.default_rng(seed), B, V, oracle)
 
 
-def _check(sim, oracle, x, params, u, hist, hist_len, mask=None, hint=None, split=None, kept_cap=1025):
-    r = sim.run_sample(x, params, u, hist, hist_len, mask_table=mask, kept_cap=kept_cap, hint=hint, split=split)
+def _check(sim, oracle, x, params, u, hist, hist_len, mask=None, hint=None, split=None, kept_cap=1025,
+           noalloc=False):
+    r = sim.run_sample(x, params, u, hist, hist_len, mask_table=mask, kept_cap=kept_cap, hint=hint, split=split,
+                       noalloc=noalloc)
     o = oracle.sample_batch(x, params, u, hist=hist, hist_len=hist_len, mask_table=mask, kept_cap=kept_cap,
                             want_post=True)
     return r, o, H.compare(r, o, params, x.shape[1], what="sim")
@@ -135,6 +137,26 @@ def test_k64_split_merge_16(sim, oracle):
     x, params, u, hist, hist_len = _batch(44, 7, V, oracle)
     params = _k64_params(g, params, V)
     _check(sim, oracle, x, params, u, hist, hist_len, hint=tg.batch_hint(params, V), split=16, kept_cap=64)
+
+
+@pytest.mark.parametrize("path", ["k64", "general"])
+def test_noalloc_entry_point(sim, oracle, path):
+    """tgs_sample_noalloc: the same kernels on the static workspace (k64
+    lists and counters as the first call on a device leaves them; the
+    general path's chunk lists) and a mask table passed by pointer."""
+    import tinygpt_amd as tg
+
+    g = np.random.default_rng(46)
+    V = 20000
+    x, params, u, hist, hist_len = _batch(46, 7, V, oracle)
+    mask = g.integers(0, 1 << 32, size=(3, (V + 31) // 32), dtype=np.uint64).astype(np.uint32)
+    params["mask_state"] = g.integers(-1, 3, size=7)
+    if path == "k64":
+        params = _k64_params(g, params, V)
+        _check(sim, oracle, x, params, u, hist, hist_len, mask=mask, hint=tg.batch_hint(params, V), split=4,
+               kept_cap=64, noalloc=True)
+    else:
+        _check(sim, oracle, x, params, u, hist, hist_len, mask=mask, split=2, noalloc=True)
 
 
 def test_k64_bf16_and_mask(sim, oracle):

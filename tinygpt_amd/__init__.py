@@ -3,9 +3,10 @@
 The product is libtgs_sampler.so (C ABI in include/tgs_sampler.h): gfx950
 HIP kernels for penalties, temperature, the grammar mask, top-k, top-p, the
 categorical draw and speculative verification.  This package holds the
-kernels' sources (csrc/), the in-tree build, a ctypes binding (`Sampler`),
-the host-side mirror of the reference sampling API (`host`), and the
-synthetic workloads of the benchmark configurations (`workloads`).
+kernels' sources (csrc/), the in-tree build, a ctypes binding (`Sampler`,
+`sample_noalloc`), the host grammar compiler that fills mask-table rows
+(`grammar`), and the synthetic workloads of the benchmark configurations
+(`workloads`).
 """
 from ._lib import (  # noqa: F401
     EXPORTS,
@@ -19,4 +20,4 @@ from ._lib import (  # noqa: F401
     TgsError,
     load,
 )
-from .sampler import Sampler, batch_hint, make_params, params_to_device  # noqa: F401
+from .sampler import Sampler, batch_hint, make_params, params_to_device, sample_noalloc  # noqa: F401

@@ -37,6 +37,7 @@ EXPORTS = (
     "tgs_mask_table_set",
     "tgs_mask_table_update",
     "tgs_sample",
+    "tgs_sample_noalloc",
     "tgs_reserve_spec",
     "tgs_spec_verify",
     "tgs_token_logprobs",
@@ -117,6 +118,9 @@ def load() -> C.CDLL:
     L.tgs_hint_from_params.argtypes = [P, I, I, C.POINTER(TgsHint)]
     L.tgs_sample.argtypes = [P, P, I, I, I, C.c_int64, P, P, I, P, P, P, C.POINTER(TgsHint),
                              C.POINTER(TgsDebug), P]
+    L.tgs_sample_noalloc.restype = I
+    L.tgs_sample_noalloc.argtypes = [I, P, I, I, I, C.c_int64, P, P, I, P, P, P, P, I, I, C.POINTER(TgsHint),
+                                     C.POINTER(TgsDebug), P]
     L.tgs_reserve_spec.restype = I
     L.tgs_reserve_spec.argtypes = [P, I, I]
     L.tgs_spec_verify.restype = I

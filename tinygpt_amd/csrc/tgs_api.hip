@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -264,6 +265,84 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
   return TGS_OK;
 }
 
+// ---------------------------------------------------------------- allocation-free sampling
+//
+// tgs_sample_noalloc takes its workspace from `scratch`, a static device
+// array of fixed size (each GPU the library runs on holds its own copy until
+// the process ends) instead of a handle's allocations:
+//   [k64 chunk lists: kNaRows * kMaxSplit * 64 u64, all ~0 between calls]
+//   [general-path chunk lists: kNaWsRows * KMAX u64]
+//   [k64 arrival counters: kNaRows * K64_CNT_STRIDE u32, zero between calls]
+//   [general-path list counts: kNaWsRows * (KMAX / 64) i32]
+// The k64 kernel leaves its lists and counters in that state after every
+// call; the first call on a device puts them there with a fill kernel.
+// Host code never passes `scratch` itself to a kernel: its address on each
+// device comes from hipGetSymbolAddress.
+constexpr int kNaRows = 256;    // rows per call
+constexpr int kNaWsRows = 512;  // general-path (row, chunk) lists
+constexpr int kNaHist = tgs::K64_MAX_HIST;
+constexpr size_t kNaListWords = (size_t)kNaRows * kMaxSplit * 64;
+constexpr size_t kNaWsWords = (size_t)kNaWsRows * tgs::KMAX;
+constexpr size_t kNaCntU32 = (size_t)kNaRows * tgs::K64_CNT_STRIDE;
+constexpr size_t kNaWsCntI32 = (size_t)kNaWsRows * (tgs::KMAX / 64);
+constexpr size_t kNaWords = kNaListWords + kNaWsWords + (kNaCntU32 + kNaWsCntI32) / 2;
+static_assert(kNaCntU32 % 2 == 0 && kNaWsCntI32 % 2 == 0, "whole 8-byte words");
+
+constexpr int kNaMaxDevices = 64;
+struct NoAllocDevice {
+  bool ready = false;
+  unsigned long long* ptr = nullptr;  // this device's copy of scratch
+  int num_cu = 256;
+  size_t lds_limit = 65536;
+};
+std::mutex g_na_mu;
+NoAllocDevice g_na[kNaMaxDevices];
+thread_local std::string g_na_err;
+
+__global__ void na_fill_kernel(unsigned long long* p, size_t n_ones, size_t n_zero) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_ones + n_zero; i += stride)
+    p[i] = i < n_ones ? ~0ull : 0ull;
+}
+
+}  // namespace
+
+static __device__ __align__(256) unsigned long long scratch[kNaWords];
+
+namespace {
+
+// Once per device, with that device current: the address of its scratch,
+// its size limits, the kernels' LDS ceilings and the lists' initial state.
+int noalloc_setup(int device, NoAllocDevice*& out) {
+  std::lock_guard<std::mutex> lock(g_na_mu);
+  NoAllocDevice& d = g_na[device];
+  if (!d.ready) {
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return efail(g_na_err, TGS_EHIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    d.ptr = (unsigned long long*)ptr;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && v > 0)
+      d.num_cu = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
+      d.lds_limit = (size_t)v;
+    if (tgs::set_sample_lds_limit(d.lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_k64_lds_limit(d.lds_limit - sizeof(tgs::BlockScratch) - 4096) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_topp_lds_limit(d.lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_topk_lds_limit(d.lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
+    // k64 lists "not written" (~0); everything after them zero
+    hipLaunchKernelGGL(na_fill_kernel, dim3(1024), dim3(256), 0, nullptr, d.ptr, kNaListWords,
+                       kNaWords - kNaListWords);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return efail(g_na_err, TGS_EHIP, std::string("scratch set-up: ") + hipGetErrorString(e));
+    d.ready = true;
+  }
+  out = &d;
+  return TGS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -361,7 +440,10 @@ void tgs_destroy(tgs_handle h) {
   delete h;
 }
 
-const char* tgs_last_error(tgs_handle h) { return h ? h->err.c_str() : "null handle"; }
+const char* tgs_last_error(tgs_handle h) {
+  if (h) return h->err.c_str();
+  return g_na_err.empty() ? "null handle" : g_na_err.c_str();
+}
 
 int tgs_mask_table_set(tgs_handle h, const uint32_t* host_words, int n_states, int vocab) {
   if (!h) return TGS_EINVAL;
@@ -429,6 +511,41 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   res.n_states = table_ok ? h->n_states : 0;
   res.mask_words = h->mask_words;
   return sample_core(res, h->err, d_logits, dt, B, V, row_stride, d_hist, d_hist_len, hist_cap, d_params, d_u,
+                     d_out_ids, hint, dbg, (hipStream_t)stream);
+}
+
+int tgs_sample_noalloc(int device, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,
+                       const int32_t* d_hist, const int32_t* d_hist_len, int hist_cap,
+                       const tgs_row_params* d_params, const float* d_u, int32_t* d_out_ids,
+                       const uint32_t* d_mask_table, int n_states, int mask_vocab, const tgs_batch_hint* hint,
+                       const tgs_debug* dbg, tgs_stream stream) {
+  if (dt != TGS_F32 && dt != TGS_BF16) return efail(g_na_err, TGS_EINVAL, "dtype");
+  if (B < 0 || V < 1 || row_stride < V) return efail(g_na_err, TGS_EINVAL, "shape");
+  if (B > kNaRows || V > kMaxVocab || hist_cap > kNaHist)
+    return efail(g_na_err, TGS_ETOOBIG,
+                 "tgs_sample_noalloc: at most " + std::to_string(kNaRows) + " rows, " + std::to_string(kMaxVocab) +
+                     " ids per row and " + std::to_string(kNaHist) + " history ids per row (its static workspace)");
+  if (n_states < 0 || (n_states > 0 && (!d_mask_table || mask_vocab < V)))
+    return efail(g_na_err, TGS_EINVAL, "mask table: n_states >= 0; a table needs a pointer and mask_vocab >= V");
+  if (device < 0 || device >= kNaMaxDevices) return efail(g_na_err, TGS_EINVAL, "device");
+  if (B == 0) return TGS_OK;
+  DeviceGuard g(device);
+  if (!g.ok) return efail(g_na_err, TGS_EHIP, "hipSetDevice");
+  NoAllocDevice* d = nullptr;
+  const int rc = noalloc_setup(device, d);
+  if (rc != TGS_OK) return rc;
+  SampleRes res;
+  res.num_cu = d->num_cu;
+  res.lds_limit = d->lds_limit;
+  res.k64_lists = d->ptr;
+  res.ws = d->ptr + kNaListWords;
+  res.ws_rows = kNaWsRows;
+  res.k64_cnt = (unsigned*)(d->ptr + kNaListWords + kNaWsWords);
+  res.ws_cnt = (int*)(res.k64_cnt + kNaCntU32);
+  res.mask_table = n_states > 0 ? d_mask_table : nullptr;
+  res.n_states = n_states;
+  res.mask_words = (mask_vocab + 31) / 32;
+  return sample_core(res, g_na_err, d_logits, dt, B, V, row_stride, d_hist, d_hist_len, hist_cap, d_params, d_u,
                      d_out_ids, hint, dbg, (hipStream_t)stream);
 }
 

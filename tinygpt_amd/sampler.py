@@ -66,6 +66,68 @@ def params_to_device(params: np.ndarray, device):
     return torch.from_numpy(raw.copy()).to(device)
 
 
+def _debug_struct(debug):
+    if not debug:
+        return None
+    dbg = TgsDebug()
+    for name in ("kept_ids", "kept_probs", "counts", "mass", "cut_ids", "post_logits"):
+        t = debug.get(name)
+        setattr(dbg, name, None if t is None else t.data_ptr())
+    kc = debug.get("kept_ids", debug.get("kept_probs"))
+    dbg.kept_cap = 0 if kc is None else kc.shape[1]
+    return dbg
+
+
+def _hint_struct(hint):
+    if hint is None:
+        return None
+    hs = TgsHint()
+    hs.max_top_k = int(hint)
+    hs.min_top_k = int(getattr(hint, "min_top_k", 0))  # 0: unknown
+    return hs
+
+
+def _dtype_code(logits):
+    torch = _torch()
+    if logits.dtype == torch.float32:
+        return TGS_F32
+    if logits.dtype == torch.bfloat16:
+        return TGS_BF16
+    raise TypeError("logits must be float32 or bfloat16")
+
+
+def sample_noalloc(logits, params_dev, u, hist=None, hist_len=None, out=None, vocab=None, mask_table=None,
+                   mask_vocab=None, debug=None, stream=None, hint=None):
+    """tgs_sample_noalloc: Sampler.sample without a handle (the library's
+    static device workspace; no allocation inside the call).  mask_table:
+    uint32 device tensor [n_states, ceil(mask_vocab / 32)] or None.  `out`
+    must be given by callers that cannot allocate (it is allocated here
+    otherwise)."""
+    torch = _torch()
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with unit stride along V")
+    B = logits.shape[0]
+    V = logits.shape[1] if vocab is None else vocab
+    dt = _dtype_code(logits)
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    hist_cap = 0 if hist is None else hist.shape[1]
+    n_states = 0 if mask_table is None else mask_table.shape[0]
+    mv = (V if mask_vocab is None else mask_vocab) if mask_table is not None else 0
+    dbg = _debug_struct(debug)
+    hs = _hint_struct(hint)
+    st = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
+    L = _lib.load()
+    rc = L.tgs_sample_noalloc(
+        logits.device.index or 0, _ptr(logits), dt, B, V, logits.stride(0), _ptr(hist), _ptr(hist_len), hist_cap,
+        _ptr(params_dev), _ptr(u), _ptr(out), _ptr(mask_table), n_states, mv,
+        C.byref(hs) if hs is not None else None, C.byref(dbg) if dbg is not None else None, C.c_void_p(st),
+    )
+    if rc != 0:
+        raise TgsError(rc, f"tgs_sample_noalloc: {L.tgs_last_error(None).decode()}")
+    return out
+
+
 class Sampler:
     """One sampler handle on one GPU.
 
@@ -128,29 +190,13 @@ class Sampler:
             raise ValueError("logits must be [B, V] with unit stride along V")
         B = logits.shape[0]
         V = logits.shape[1] if vocab is None else vocab
-        if logits.dtype == torch.float32:
-            dt = TGS_F32
-        elif logits.dtype == torch.bfloat16:
-            dt = TGS_BF16
-        else:
-            raise TypeError("logits must be float32 or bfloat16")
+        dt = _dtype_code(logits)
         if out is None:
             out = torch.empty(B, dtype=torch.int32, device=logits.device)
         hist_cap = 0 if hist is None else hist.shape[1]
-        dbg = None
-        if debug:
-            dbg = TgsDebug()
-            for name in ("kept_ids", "kept_probs", "counts", "mass", "cut_ids", "post_logits"):
-                t = debug.get(name)
-                setattr(dbg, name, None if t is None else t.data_ptr())
-            kc = debug.get("kept_ids", debug.get("kept_probs"))
-            dbg.kept_cap = 0 if kc is None else kc.shape[1]
+        dbg = _debug_struct(debug)
         st = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
-        hs = None
-        if hint is not None:
-            hs = TgsHint()
-            hs.max_top_k = int(hint)
-            hs.min_top_k = int(getattr(hint, "min_top_k", 0))  # 0: unknown
+        hs = _hint_struct(hint)
         rc = self._L.tgs_sample(
             self._h, _ptr(logits), dt, B, V, logits.stride(0), _ptr(hist), _ptr(hist_len), hist_cap,
             _ptr(params_dev), _ptr(u), _ptr(out), C.byref(hs) if hs is not None else None,
