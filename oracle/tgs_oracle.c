@@ -16,9 +16,9 @@
  *     (ConstrainedGen.swift:816-819 sets 0 for accepted ids, -inf otherwise).
  *  3. Greedy (T <= 0 or flag): argmax z, ties -> lowest id
  *     (model.cpp:491-493 strict '>').
- *  4. y = z * (1/T), 1/T rounded once per row.  (The reference divides,
- *     Serve.swift:1499; one rounding of the reciprocal is the documented
- *     contract here, shared by the kernels.)  Allowed <=> y > -inf.
+ *  4. y = z / T, the IEEE (correctly rounded) division, as the reference
+ *     divides (Serve.swift:1499, wasm/src/model.cpp:499).  A row whose 1/T
+ *     is not finite is invalid.  Allowed <=> y > -inf.
  *  5. Order allowed ids by (y desc, id asc).  Top-k keeps the first
  *     min(k, n_allowed) (the reference keeps all ties at the k-th value,
  *     model.py:222; ref_tie_extra counts the difference).
@@ -233,7 +233,7 @@ static int sample_row_impl(const float* x, int V, const int32_t* hist, int H, co
     }
     int allowed = 1;
     if (mask_row && !((mask_row[v >> 5] >> (v & 31)) & 1u)) allowed = 0;
-    float y = greedy ? z : z * invT;
+    float y = greedy ? z : z / T;
     if (!(y > -INFINITY)) allowed = 0; /* -inf and NaN */
     if (post_logits) post_logits[v] = allowed ? y : -INFINITY;
     if (!allowed) continue;
@@ -504,11 +504,12 @@ float tgo_spec_row_stats(const float* y, int V, float* m_out) {
   return S;
 }
 
-/* y = z * invT, -inf for NaN / -inf inputs (greedy rows: invT == 1). */
-static void spec_scale_row(const void* base, int dtype, int64_t off, int V, float invT, float* y) {
+/* y = z / T (IEEE division), -inf for NaN / -inf inputs (greedy rows: T == 1).
+ * SpeculativeDecode.swift:141,158 scales by the clamped temperature. */
+static void spec_scale_row(const void* base, int dtype, int64_t off, int V, float T, float* y) {
   for (int v = 0; v < V; v++) {
     float z = dtype == 1 ? bf16_to_f32(((const uint16_t*)base)[off + v]) : ((const float*)base)[off + v];
-    float t = z * invT;
+    float t = z / T;
     y[v] = (t > -INFINITY) ? t : -INFINITY;
   }
 }
@@ -611,8 +612,8 @@ int tgo_spec_verify_row(const void* target, const void* draft, int dtype, int64_
     int j;
     for (j = 0; j < k; j++) {
       float mt, md;
-      spec_scale_row(target, dtype, (int64_t)j * row_stride, V, invT, yt);
-      spec_scale_row(draft, dtype, (int64_t)j * row_stride, V, invT, yd);
+      spec_scale_row(target, dtype, (int64_t)j * row_stride, V, Tc, yt);
+      spec_scale_row(draft, dtype, (int64_t)j * row_stride, V, Tc, yd);
       float St = tgo_spec_row_stats(yt, V, &mt);
       float Sd = tgo_spec_row_stats(yd, V, &md);
       if (j < 16) {
@@ -661,7 +662,7 @@ int tgo_spec_verify_row(const void* target, const void* draft, int dtype, int64_
     }
     if (j == k) { /* all accepted: bonus token from target row k */
       float mt;
-      spec_scale_row(target, dtype, (int64_t)k * row_stride, V, invT, yt);
+      spec_scale_row(target, dtype, (int64_t)k * row_stride, V, Tc, yt);
       tgo_spec_row_stats(yt, V, &mt);
       if (!(mt > -INFINITY)) {
         out[0] = -1;

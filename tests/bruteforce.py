@@ -34,7 +34,7 @@ def post_logits(x, hist, params, mask_row=None):
         zi = (zi - freq * cnt[ids].astype(np.float32)).astype(np.float32)
         zi = (zi - pres).astype(np.float32)
         z[ids] = zi
-    y = z if greedy else (z * (np.float32(1) / T)).astype(np.float32)
+    y = z if greedy else (z / T).astype(np.float32)  # IEEE float32 division (Serve.swift:1499)
     allowed = y > -np.inf  # False for NaN
     if mask_row is not None:
         bits = (np.asarray(mask_row, dtype=np.uint32)[np.arange(V) >> 5] >> (np.arange(V) & 31).astype(np.uint32)) & 1

@@ -5,6 +5,7 @@
 //   numerics div N seed   tg_div_rcp(a, b, 1/b) == a / b, a in [0, 1], b in [1, 2^18]
 //   numerics exp N seed   tg_expf_nonpos(x) == tg_expf(x), x <= 0, -inf, NaN
 //   numerics q40 N seed   (u64)tg_q40d(e) == tg_q40(e), e in [0, 1]
+//   numerics divt N seed  tg_div_t(z, T, 1/T) == z / T, any z, T > 0 with 1/T finite
 // Prints the number of mismatches (and the first few).
 #include <hip/hip_runtime.h>
 
@@ -84,6 +85,37 @@ int main(int argc, char** argv) {
       if (i == 1) e = 1.0f;
       const u64 q1 = (u64)tg_q40d(e), q0 = tg_q40(e);
       if (q1 != q0) report("q40", e, 0, (double)q1, (double)q0);
+    }
+  } else if (mode == "divt") {
+    // z: every exponent of the fast range and beyond it, both signs, plus
+    // specials; T: every exponent from 2^-24 to 2^24 (around the fast range),
+    // including the powers of two and all-ones mantissas
+    for (long long i = 0; i < N; i++) {
+      const uint64_t r = g();
+      const int ez = (int)(r % 80) - 40, et = (int)((r >> 8) % 49) - 24;
+      const uint32_t mz = (uint32_t)(r >> 16) & 0x7FFFFFu, mt = (uint32_t)(r >> 40) & 0x7FFFFFu;
+      float z = bits(((uint32_t)(127 + ez) << 23) | mz);
+      if ((r >> 63) & 1) z = -z;
+      float T = bits(((uint32_t)(127 + et) << 23) | mt);
+      switch (i & 31) {
+        case 0: z = 0.0f; break;
+        case 1: z = -0.0f; break;
+        case 2: z = __builtin_inff(); break;
+        case 3: z = -__builtin_inff(); break;
+        case 4: z = bits(0x7FC00000u); break;
+        case 5: z = bits((uint32_t)(r >> 20) & 0x7FFFFFu); break;  // denormal
+        case 6: T = bits((uint32_t)(127 + et) << 23); break;        // power of two
+        case 7: T = bits(((uint32_t)(127 + et) << 23) | 0x7FFFFFu); break;
+        case 8: z = bits(((uint32_t)(127 + ez) << 23) | 0x7FFFFFu); break;
+        case 9: z = (float)((int)(r % 2001) - 1000) * 0.01f; T = (float)(1 + (r >> 32) % 200) * 0.01f; break;
+        case 10: T = bits(((uint32_t)(127 - 126) << 23) | mt); break;  // T near the smallest normal
+        case 11: z = bits(((uint32_t)(127 + 100) << 23) | mz); break;  // large logits
+        default: break;
+      }
+      const float rT = 1.0f / T;
+      if (!__builtin_isfinite(rT)) continue;
+      const float q1 = tg_div_t(z, T, rT, tg_div_t_mode(T)), q0 = z / T;
+      if (ubits(q1) != ubits(q0) && !(q0 != q0 && q1 != q1)) report("divt", z, T, q1, q0);
     }
   } else {
     return 2;

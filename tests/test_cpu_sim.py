@@ -307,9 +307,12 @@ def test_spec_invalid_rows(sim, oracle):
     _spec_check(sim, oracle, c)
 
 
-@pytest.mark.parametrize("mode,n", [("div", 20_000_000), ("exp", 20_000_000), ("q40", 10_000_000)])
+@pytest.mark.parametrize("mode,n", [("div", 20_000_000), ("exp", 20_000_000), ("q40", 10_000_000),
+                                    ("divt", 40_000_000)])
 def test_device_shortcuts_equal_canonical_ops(sim, mode, n):
-    """tg_div_rcp == IEEE a / b (weights over softmax denominators),
+    """tg_div_t == IEEE z / T (the temperature divide, every mode, with zeros,
+    infinities, NaN, denormals and huge logits among the inputs),
+    tg_div_rcp == IEEE a / b (weights over softmax denominators),
     tg_expf_nonpos == tg_expf on x <= 0 / -inf / NaN, and f64-summed
     tg_q40d == tg_q40, on the device header compiled for the host."""
     import subprocess

@@ -39,13 +39,12 @@ def test_accept_decisions_match_fp64(oracle, seed):
     u_acc = (g.integers(0, 1 << 24, size=(B, k)) / (1 << 24)).astype(np.float32)
     u_res = (g.integers(0, 1 << 24, size=B) / (1 << 24)).astype(np.float32)
     r = oracle.spec_verify_batch(target, draft, dtok, np.full(B, T), u_acc, u_res)
-    invT = np.float32(1) / T
     for b in range(B):
         n = r["n_acc"][b]
         assert 0 <= n <= k
         for j in range(n + (1 if n < k else 0)):
-            pt = softmax64(target[b, j] * invT)[dtok[b, j]]
-            pd = softmax64(draft[b, j] * invT)[dtok[b, j]]
+            pt = softmax64(target[b, j] / T)[dtok[b, j]]
+            pd = softmax64(draft[b, j] / T)[dtok[b, j]]
             ratio = pt / max(pd, 1e-10)
             if abs(u_acc[b, j] - ratio) <= 1e-5 * max(1.0, ratio):
                 break  # boundary case: either decision is allowed

@@ -103,6 +103,36 @@ __device__ __forceinline__ float tg_div_rcp(float a, float b, float rb) {
   return __builtin_fmaf(r, rb, q);
 }
 
+// z / T correctly rounded (the temperature divide of Serve.swift:1499 and
+// wasm/src/model.cpp:499), from the row's rT = RN(1 / T), by a mode fixed
+// once per row (tg_div_t_mode):
+//   TDIV_POW2  T a power of two: z rT is the same real number as z / T,
+//              so one multiply rounds it the same way;
+//   TDIV_FAST  T in [2^-20, 2^20]: q0 = RN(z rT) lies within 1.5 ulp of
+//              z / T; one residual correction q1 = q0 + (z - T q0) rT makes
+//              it faithful, and a second, with the residual z - T q1 exact
+//              by a fused multiply-add, rounds to RN(z / T) (Markstein's
+//              theorem).  The residuals stay exactly representable while
+//              |z| is in [2^-30, 2^30]; any other z (0, tiny, huge, inf,
+//              NaN) takes the IEEE division;
+//   TDIV_IEEE  any other T: the IEEE division.
+// Bit-equal to z / T: tests/cpu_sim/numerics.cpp, mode divt.
+constexpr int TDIV_POW2 = 0, TDIV_FAST = 1, TDIV_IEEE = 2;
+__device__ __forceinline__ int tg_div_t_mode(float T) {
+  if (T >= 0x1p-126f && (tg_f2u(T) & 0x7FFFFFu) == 0u) return TDIV_POW2;
+  return (T >= 0x1p-20f && T <= 0x1p20f) ? TDIV_FAST : TDIV_IEEE;
+}
+__device__ __forceinline__ float tg_div_t(float z, float T, float rT, int mode) {
+  if (mode == TDIV_POW2) return z * rT;
+  const float az = __builtin_fabsf(z);
+  if (mode == TDIV_FAST && az >= 0x1p-30f && az <= 0x1p30f) {
+    const float q0 = z * rT;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, T, z), rT, q0);
+    return __builtin_fmaf(__builtin_fmaf(-q1, T, z), rT, q1);
+  }
+  return z / T;
+}
+
 __device__ __forceinline__ float tg_weight(float y, float m) {
   return (y == m) ? 1.0f : tg_expf(y - m);
 }

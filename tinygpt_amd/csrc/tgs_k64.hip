@@ -127,7 +127,7 @@ __device__ __forceinline__ float values_plain(const Row& r, int t0, bool tail, c
     float m = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < EPV; e++) {
-      y[u * EPV + e] = elem_z<Tin>(raw[u], e, past) * r.invT;
+      y[u * EPV + e] = row_y(r, elem_z<Tin>(raw[u], e, past));
       m = fmaxf(m, y[u * EPV + e]);
     }
     vm[u] = m;
@@ -157,7 +157,7 @@ __device__ __forceinline__ float values_general(const Row& r, u64 hb, int t0, bo
       if (r.mrow) d |= ~(mw[u] >> (v & 31)) & GM;
     }
 #pragma unroll
-    for (int e = 0; e < EPV; e++) y[u * EPV + e] = elem_z<Tin>(raw[u], e, past) * r.invT;
+    for (int e = 0; e < EPV; e++) y[u * EPV + e] = row_y(r, elem_z<Tin>(raw[u], e, past));
     if (d) {
 #pragma unroll
       for (int e = 0; e < EPV; e++) y[u * EPV + e] = ((d >> e) & 1u) ? ninf : y[u * EPV + e];
@@ -274,10 +274,10 @@ __device__ __forceinline__ void each_cand(const Row& r, bool has_hist, const uin
     const int id = id_of<EPV>(t0, j);
     if (id >= r.v1) continue;
     const float z = Elem<Tin>::scalar(rowp, id);
-    float yy = z * r.invT;
+    float yy = row_y(r, z);
     if (has_hist && ((bitmap[2 * threadIdx.x + (j >> 5)] >> (j & 31)) & 1u)) {
       const int loc = id - t0;
-      yy = penalise(z, (int)((hcnt[loc >> 1] >> ((loc & 1) * 16)) & 0xFFFFu), r) * r.invT;
+      yy = row_y(r, penalise(z, (int)((hcnt[loc >> 1] >> ((loc & 1) * 16)) & 0xFFFFu), r));
     }
     if (yy >= tf && (!MASK || mask_allows(r, id))) f(comp_key(tg_key(yy), id));
   }
@@ -519,7 +519,7 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
     if (prod[q]) {
       const int id = hid[q], loc = id - v0;
       const int hc = (int)((hcnt[loc >> 1] >> ((loc & 1) * 16)) & 0xFFFFu);
-      const float yy = penalise(zq[q], hc, r) * r.invT;
+      const float yy = row_y(r, penalise(zq[q], hc, r));
       bool ok = yy > -__builtin_inff();
       if constexpr (MASK) ok = ok && (!r.mrow || ((mq[q] >> (id & 31)) & 1u));
       if (post) post[id] = ok ? yy : -__builtin_inff();

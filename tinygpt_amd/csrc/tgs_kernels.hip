@@ -164,7 +164,7 @@ __device__ __forceinline__ void full_stream(const SampleArgs& a, const Row& r, c
         if (cnt > 0) z = penalise(z, cnt, r);
       }
       float y;
-      const uint32_t key = elem_key(z, ((mw >> (id & 31)) & 1u) != 0, r.invT, &y);
+      const uint32_t key = elem_key(z, ((mw >> (id & 31)) & 1u) != 0, r, &y);
       if (id < a.V) f(id, key, y);
     }
   }
@@ -326,7 +326,7 @@ __device__ __forceinline__ void tile_keys(const Row& r, const uint32_t* bitmap, 
       const bool hist = (hb[u] >> ((id - r.v0) & 31)) & 1u;
       float y;
       const bool allowed = ((mw[u] >> (id & 31)) & 1u) && !hist;
-      key[u * EPV + e] = elem_key(Elem<Tin>::get(raw[u], e), allowed, r.invT, &y);
+      key[u * EPV + e] = elem_key(Elem<Tin>::get(raw[u], e), allowed, r, &y);
       if (post && id < r.v1 && !hist) post[id] = y;
     }
   }
@@ -342,7 +342,7 @@ __device__ __forceinline__ void history_pass(const SampleArgs& a, const Row& r, 
     const int v = e.x;
     const float z = penalise(Elem<Tin>::scalar(rowp, v), e.y, r);
     float y;
-    const uint32_t key = elem_key(z, mask_allows(r, v), r.invT, &y);
+    const uint32_t key = elem_key(z, mask_allows(r, v), r, &y);
     f(v, key, y);
   }
 }

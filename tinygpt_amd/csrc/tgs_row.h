@@ -68,7 +68,8 @@ __device__ __forceinline__ uint4 load_vec(const Tin* rowp, int v, int vend, bool
 struct Row {
   int b, c;
   int mode;  // 0 greedy, 1 candidate top-k, 2 full
-  float invT;
+  float T, rT;  // temperature (1 for greedy rows) and RN(1 / T)
+  int tdiv;     // tg_div_t mode of T
   int k;
   float top_p, rep, pres, freq, u;
   bool use_pen;
@@ -87,12 +88,16 @@ __device__ __forceinline__ bool row_setup_from(const SampleArgs& a, int b, int c
   const float T = p.temperature;
   if (__builtin_isnan(T)) return false;
   const bool greedy = (p.flags & TGS_FLAG_GREEDY) || T <= 0.0f;
-  r.invT = 1.0f;
+  r.T = 1.0f;
+  r.rT = 1.0f;
+  r.tdiv = TDIV_POW2;
   r.u = 0.0f;
   if (!greedy) {
     if (!__builtin_isfinite(T)) return false;
-    r.invT = 1.0f / T;
-    if (!__builtin_isfinite(r.invT)) return false;
+    r.T = T;
+    r.rT = 1.0f / T;
+    if (!__builtin_isfinite(r.rT)) return false;
+    r.tdiv = tg_div_t_mode(T);
     if (__builtin_isnan(p.top_p) || p.top_p <= 0.0f) return false;
     r.u = u;
     if (__builtin_isnan(r.u) || r.u < 0.0f || r.u >= 1.0f) return false;
@@ -198,9 +203,13 @@ __device__ __forceinline__ bool mask_allows(const Row& r, int v) {
   return r.mrow == nullptr || ((r.mrow[v >> 5] >> (v & 31)) & 1u);
 }
 
+// The canonical logit of a (penalised) logit z: z / T correctly rounded
+// (z itself on greedy rows, whose T is 1).
+__device__ __forceinline__ float row_y(const Row& r, float z) { return tg_div_t(z, r.T, r.rT, r.tdiv); }
+
 // Key of one element (0 when not allowed); *y_out gets the canonical logit.
-__device__ __forceinline__ uint32_t elem_key(float z, bool allowed, float invT, float* y_out) {
-  const float y = z * invT;
+__device__ __forceinline__ uint32_t elem_key(float z, bool allowed, const Row& r, float* y_out) {
+  const float y = row_y(r, z);
   const bool ok = allowed && (y > -__builtin_inff());
   *y_out = ok ? y : -__builtin_inff();
   return ok ? tg_key(y) : 0u;

@@ -72,24 +72,29 @@ __device__ __forceinline__ void load_block(const Tin* rowp, int blk, int V, bool
   for (int i = 0; i < Tile<Tin>::NV; i++) raw[i] = load_vec<Tin>(rowp, blk_id<Tin>(blk, i, 0), V, aligned);
 }
 
-// y = z * invT with NaN and -inf mapped to -inf (ids past V were loaded as NaN)
-__device__ __forceinline__ float scaled(float z, float invT) {
-  const float t = z * invT;
-  return (t > -__builtin_inff()) ? t : -__builtin_inff();
-}
-
-// Sequence temperature: greedy (T <= 0), the clamped T = max(T, 1e-5) and
-// its reciprocal.  NaN T is reported by the decide kernel.
+// Sequence temperature: greedy (T <= 0), the clamped T = max(T, 1e-5), its
+// reciprocal and the mode of the exact divide (greedy: T = 1).  NaN T is
+// reported by the decide kernel.
 struct SeqT {
   bool greedy;
-  float invT;
+  float T, rT;
+  int tdiv;
 };
 __device__ __forceinline__ SeqT seq_temp(float T) {
   SeqT s;
   s.greedy = !(T > 0.0f);
   const float Tc = T > 1e-5f ? T : 1e-5f;
-  s.invT = s.greedy ? 1.0f : 1.0f / Tc;
+  s.T = s.greedy ? 1.0f : Tc;
+  s.rT = 1.0f / s.T;
+  s.tdiv = tg_div_t_mode(s.T);
   return s;
+}
+
+// y = z / T (correctly rounded) with NaN and -inf mapped to -inf (ids past V
+// were loaded as NaN)
+__device__ __forceinline__ float scaled(float z, const SeqT& st) {
+  const float t = tg_div_t(z, st.T, st.rT, st.tdiv);
+  return (t > -__builtin_inff()) ? t : -__builtin_inff();
 }
 
 // ------------------------------------------------------------------ K1
@@ -102,13 +107,12 @@ __device__ __forceinline__ SeqT seq_temp(float T) {
 struct BlockRef {
   int b, r, blk;
   bool live, greedy;
-  float invT;
+  SeqT st;
 };
 __device__ __forceinline__ void block_ref_temp(const SpecArgs& a, BlockRef& x) {
   const float T = a.T[x.b];
-  const SeqT st = seq_temp(T);
-  x.greedy = st.greedy;
-  x.invT = st.invT;
+  x.st = seq_temp(T);
+  x.greedy = x.st.greedy;
 }
 __device__ __forceinline__ bool block_live(const SpecArgs& a, const BlockRef& x) {
   return !__builtin_isnan(a.T[x.b]) && !(x.greedy && x.r > a.k);
@@ -149,7 +153,7 @@ __device__ __forceinline__ void block_stats(const SpecArgs& a, const BlockRef& x
     for (int i = 0; i < TL::NV; i++)
 #pragma unroll
       for (int e = 0; e < TL::EPV; e++) {
-        const float y = scaled(Elem<Tin>::get(raw[i], e), 1.0f);
+        const float y = scaled(Elem<Tin>::get(raw[i], e), x.st);
         if (y > -__builtin_inff()) {
           const u64 c = comp_key(tg_key(y), blk_id<Tin>(x.blk, i, e));
           arg = c > arg ? c : arg;
@@ -167,7 +171,7 @@ __device__ __forceinline__ void block_stats(const SpecArgs& a, const BlockRef& x
   for (int i = 0; i < TL::NV; i++)
 #pragma unroll
     for (int e = 0; e < TL::EPV; e++) {
-      y[i * TL::EPV + e] = Elem<Tin>::get(raw[i], e) * x.invT;
+      y[i * TL::EPV + e] = tg_div_t(Elem<Tin>::get(raw[i], e), x.st.T, x.st.rT, x.st.tdiv);
       mx = fmaxf(mx, y[i * TL::EPV + e]);
     }
   mx = wave_maxf(mx);
@@ -298,7 +302,7 @@ __global__ __launch_bounds__(DT) void spec_decide_kernel(SpecArgs a) {
   }
   // validation (the CPU restatement's rules): T, draft ids, uniforms
   if (w == 0) {
-    bool bad = __builtin_isnan(T) || (!st.greedy && !(st.invT > 0.0f && __builtin_isfinite(st.invT)));
+    bool bad = __builtin_isnan(T) || (!st.greedy && !(st.rT > 0.0f && __builtin_isfinite(st.rT)));
     if (lane < k) {
       if (d < 0 || d >= a.V) bad = true;
       if (!st.greedy && (__builtin_isnan(ua) || ua < 0.0f || ua >= 1.0f)) bad = true;
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(DT) void spec_decide_kernel(SpecArgs a) {
   // every draft position at once (lane j), then the first rejection
   bool acc = true, empty = false;
   if (lane < k) {
-    const float yt = scaled(zt, st.invT), yd = scaled(zd, st.invT);
+    const float yt = scaled(zt, st), yd = scaled(zd, st);
     const float mt = sm[lane], St = sS[lane];
     const float md = sm[k + 1 + lane], Sd = sS[k + 1 + lane];
     if (!(St > 0.0f) || !(Sd > 0.0f)) {
@@ -408,21 +412,22 @@ template <typename Tin>
 struct DrawRow {
   const Tin* tr;
   const Tin* dr;
-  float invT, mt, St, md, Sd, rSt, rSd;
+  SeqT st;
+  float mt, St, md, Sd, rSt, rSd;
   int V;
   bool resid, fast;
   __device__ __forceinline__ double mass(float zt, float zd) const {
     if (fast) {
-      const float wt = tg_expf_nonpos(zt * invT - mt);
+      const float wt = tg_expf_nonpos(tg_div_t(zt, st.T, st.rT, st.tdiv) - mt);
       if (!resid) return tg_q40d(wt);
-      const float wd = tg_expf_nonpos(zd * invT - md);
+      const float wd = tg_expf_nonpos(tg_div_t(zd, st.T, st.rT, st.tdiv) - md);
       const float pa = tg_div_rcp(wt, St, rSt);
       const float pb = tg_div_rcp(wd, Sd, rSd);
       return tg_q40d(fmaxf(pa - pb, 0.0f));
     }
-    const float yt = scaled(zt, invT);
+    const float yt = scaled(zt, st);
     if (!resid) return tg_q40d(tg_weight(yt, mt));
-    const float yd = scaled(zd, invT);
+    const float yd = scaled(zd, st);
     const float pa = tg_weight(yt, mt) / St;
     const float pb = tg_weight(yd, md) / Sd;
     return tg_q40d(fmaxf(pa - pb, 0.0f));
@@ -432,7 +437,7 @@ struct DrawRow {
 template <typename Tin>
 __device__ __forceinline__ DrawRow<Tin> draw_row(const SpecArgs& a, int b, const SeqState& s, bool resid) {
   DrawRow<Tin> d;
-  d.invT = seq_temp(a.T[b]).invT;
+  d.st = seq_temp(a.T[b]);
   d.V = a.V;
   d.resid = resid;
   d.mt = s.mt;

@@ -127,8 +127,8 @@ __device__ __forceinline__ bool hist_bit(const uint32_t* hbits, int id) { return
 
 // Canonical logit of a (non-history) id from its raw logit: y = z / T when
 // allowed, else the composite 0.
-__device__ __forceinline__ u64 comp_of(float z, bool allowed, float invT, int id) {
-  const float y = z * invT;
+__device__ __forceinline__ u64 comp_of(float z, bool allowed, const Row& r, int id) {
+  const float y = row_y(r, z);
   return (allowed && y > -__builtin_inff()) ? comp_key(tg_key(y), id) : 0ull;
 }
 
@@ -671,7 +671,7 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
       const int i = threadIdx.x + j * BT;
       if (i < (int)ncb) {
         const bool hist = r.use_pen && hist_bit(hbits, (int)id[j]);
-        cand[i] = hist ? 0ull : comp_of(x[j], true, r.invT, (int)id[j]);
+        cand[i] = hist ? 0ull : comp_of(x[j], true, r, (int)id[j]);
       }
     }
     if (r.use_pen) {
@@ -680,7 +680,7 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
         if (h.x == -1) continue;
         const int hid = h.x;
         const float z = penalise(Elem<Tin>::scalar(rowp, hid), h.y, r);
-        const u64 c = comp_of(z, mask_allows(r, hid), r.invT, hid);
+        const u64 c = comp_of(z, mask_allows(r, hid), r, hid);
         if (c) {
           const unsigned sl = ncb + atomicAdd(&ts.ng, 1u);
           if (sl < (unsigned)CAPK) cand[sl] = c;
@@ -705,7 +705,7 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
           if (id >= V) continue;
           float z = Elem<Tin>::get(raw, e);
           if (r.use_pen && hist_bit(hbits, id)) z = penalise(z, hash_count(hash, a.TS, a.ts_shift, id), r);
-          const u64 c = comp_of(z, mask_allows(r, id), r.invT, id);
+          const u64 c = comp_of(z, mask_allows(r, id), r, id);
           if (c) f(c);
         }
       }
@@ -735,7 +735,7 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
         if (id >= V) continue;
         float z = Elem<Tin>::get(raw, e);
         if (r.use_pen && hist_bit(hbits, id)) z = penalise(z, hash_count(hash, a.TS, a.ts_shift, id), r);
-        const float y = z * r.invT;
+        const float y = row_y(r, z);
         post[id] = (mask_allows(r, id) && y > -__builtin_inff()) ? y : -__builtin_inff();
       }
     }

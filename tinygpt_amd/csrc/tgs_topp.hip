@@ -82,7 +82,7 @@ struct RowView {
       const int id = v + e;
       float z = Elem<Tin>::get(raw, e);
       if ((hw >> (id & 31)) & 1u) z = penalise(z, hash_count(hash, a.TS, a.ts_shift, id), r);
-      const float yy = z * r.invT;
+      const float yy = row_y(r, z);
       yv[e] = (((mw >> (id & 31)) & 1u) && yy > -__builtin_inff() && id < a.V) ? yy : -__builtin_inff();
     }
   }
