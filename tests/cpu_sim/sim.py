@@ -4,6 +4,7 @@ outputs as the GPU harness.  TEST INFRASTRUCTURE ONLY: a debugging aid for
 kernel memory errors, never part of the product path."""
 from __future__ import annotations
 
+import fcntl
 import os
 import subprocess
 import tempfile
@@ -15,7 +16,13 @@ BIN = os.environ.get("TGS_SIM_BIN", os.path.join(HERE, "build", "run_case"))
 
 
 def build():
-    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    # One build at a time across test worker processes; the Makefile writes
+    # each binary under a temporary name and renames it into place, so a
+    # worker still running the previous binary is not disturbed.
+    os.makedirs(os.path.join(HERE, "build"), exist_ok=True)
+    with open(os.path.join(HERE, "build", ".lock"), "w") as lk:
+        fcntl.flock(lk, fcntl.LOCK_EX)
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
 def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=None, kept_cap=64,

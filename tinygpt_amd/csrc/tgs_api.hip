@@ -92,21 +92,20 @@ void free_spec(tgs_ctx* h) {
   h->spec_nbs = 0;
 }
 
-// Chunks per row of the fused top_k <= 64 kernel: every chunk is one tile
-// of at most kK64Tile ids (so S >= V / kK64Tile; with V <= kMaxVocab that is
-// at most kMaxSplit, the most lists the last workgroup of a row merges);
-// beyond that about two workgroups per CU with chunks of at least 2048
-// ids.  TGS_SPLIT raises the split (tuning).
-constexpr int kK64Tile = tgs::K64_TILE;
-int choose_split_k64(int num_cu, int B, int V) {
-  const int smin = (V + kK64Tile - 1) / kK64Tile;
+// Chunks per row of the fused top_k <= 64 kernel: about one workgroup per CU
+// (chunks of at least 2048 ids), never fewer chunks than a workgroup's
+// capacity requires, at most K64_MAX_SPLIT.  TGS_SPLIT sets the split
+// (tuning, tests).
+constexpr int kMaxSplitK64 = tgs::K64_MAX_SPLIT;
+int choose_split_k64(int num_cu, int B, int V, int dt) {
+  const int ch = tgs::k64_chunk_ids(dt);
+  const int smin = (V + ch - 1) / ch;
   int S;
   const char* env = std::getenv("TGS_SPLIT");
   if (env && std::atoi(env) > 0) {
-    S = std::min(std::atoi(env), kMaxSplit);
+    S = std::min(std::atoi(env), kMaxSplitK64);
   } else {
-    const long long target = 2LL * num_cu;
-    S = (int)std::min<long long>(kMaxSplit, std::max<long long>(1, (target + B - 1) / B));
+    S = std::min(kMaxSplitK64, std::max(1, (num_cu + B - 1) / B));
     while (S > 1 && (V + S - 1) / S < 2048) S--;
   }
   return std::max(S, smin);
@@ -127,6 +126,11 @@ int choose_split(int num_cu, int ws_rows, int B, int V) {
   while (S > 1 && (long long)S * B > ws_rows) S >>= 1;
   return S;
 }
+
+// Static LDS of the fused kernel beyond its dynamic carve-up: the wave
+// lists of its merges (4 waves x 64 u64), its staging (4 waves x 64 vectors
+// and their indices), the radix-select scratch and a few words.
+constexpr size_t kK64Static = 4 * 64 * 8 + 4 * 64 * (16 + 4) + sizeof(tgs::BlockScratch) + 128;
 
 // What a sampling call launches with: the device's size, and the workspace
 // and mask table it uses (a handle's allocations, or the allocation-free
@@ -200,21 +204,21 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
   a.ts_shift = a.TS ? 32 - log2i(a.TS) : 0;
   if (mk <= 64 && mk < V && hist_cap <= tgs::K64_MAX_HIST) {
     a.full_rows = 0;
-    const int S = choose_split_k64(res.num_cu, B, V);
-    // whole tiles when the split allows them (their loads need no checks)
-    const int L = S == (V + kK64Tile - 1) / kK64Tile ? kK64Tile
-                                                     : std::min(kK64Tile, ((V + S - 1) / S + 63) / 64 * 64);
+    const int S = choose_split_k64(res.num_cu, B, V, dt);
+    const int epv = dt == TGS_BF16 ? 8 : 4;
+    const int L = ((V + S - 1) / S + epv - 1) / epv * epv;  // whole vectors: chunk starts stay aligned
     a.S = (V + L - 1) / L;
     a.L = L;
-    a.BW = tgs::K64_BITMAP_WORDS;
-    a.off_hash = 0;                             // 16-bit history count per id of a tile
-    a.off_bitmap = tgs::K64_TILE / 2 * 4;       // history bitmap of a tile
-    a.off_cand = a.off_bitmap + a.BW * 4;       // candidate staging (16-byte aligned)
+    // dynamic LDS: history hash, history bitmap of the chunk, candidate
+    // buffer (+16 pad entries for the ranking)
+    a.BW = (L + 31) / 32;
+    a.off_hash = 0;
+    a.off_bitmap = a.TS * 8;
+    a.off_cand = (a.off_bitmap + a.BW * 4 + 15) / 16 * 16;
     a.capt = tgs::K64_CAP;
     a.ws_stride = 64;
-    const size_t lds = (size_t)a.off_cand + (size_t)tgs::K64_CAND_ENTRIES * 8;
-    if (lds + sizeof(tgs::BlockScratch) + 4096 > res.lds_limit)
-      return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS");
+    const size_t lds = (size_t)a.off_cand + (size_t)(tgs::K64_CAP + 16) * 8;
+    if (lds + kK64Static > res.lds_limit) return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS");
     hipError_t e = tgs::launch_k64(a, dt, lds, stream);
     if (e != hipSuccess) return efail(err, TGS_EHIP, std::string("sample kernel launch: ") + hipGetErrorString(e));
     return TGS_OK;
@@ -281,7 +285,7 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
 constexpr int kNaRows = 256;    // rows per call
 constexpr int kNaWsRows = 512;  // general-path (row, chunk) lists
 constexpr int kNaHist = tgs::K64_MAX_HIST;
-constexpr size_t kNaListWords = (size_t)kNaRows * kMaxSplit * 64;
+constexpr size_t kNaListWords = (size_t)kNaRows * kMaxSplitK64 * 64;
 constexpr size_t kNaWsWords = (size_t)kNaWsRows * tgs::KMAX;
 constexpr size_t kNaCntU32 = (size_t)kNaRows * tgs::K64_CNT_STRIDE;
 constexpr size_t kNaWsCntI32 = (size_t)kNaWsRows * (tgs::KMAX / 64);
@@ -328,7 +332,7 @@ int noalloc_setup(int device, NoAllocDevice*& out) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
       d.lds_limit = (size_t)v;
     if (tgs::set_sample_lds_limit(d.lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
-    if (tgs::set_k64_lds_limit(d.lds_limit - sizeof(tgs::BlockScratch) - 4096) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_k64_lds_limit(d.lds_limit - kK64Static) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topp_lds_limit(d.lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topk_lds_limit(d.lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     // k64 lists "not written" (~0); everything after them zero
@@ -415,7 +419,7 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
     // rejects the attribute keeps its default (calls that need more fail
     // with TGS_ETOOBIG / TGS_EHIP instead)
     if (tgs::set_sample_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
-    if (tgs::set_k64_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch) - 4096) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_k64_lds_limit(h->lds_limit - kK64Static) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topp_lds_limit(h->lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topk_lds_limit(h->lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     e = hipDeviceSynchronize();

@@ -622,35 +622,52 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Bitonic sort of 64 values across the lanes of a wave (descending).
+// Bitonic sort of 64 values across the lanes of a wave (descending).  The
+// strides are template arguments, so every lane move is one fixed DPP or
+// permlane instruction (a loop over a runtime stride compiles to branches).
+template <int SIZE, int STRIDE, typename T>
+__device__ __forceinline__ T sort_stage(T x, int lane) {
+  if constexpr (STRIDE == 0) {
+    return x;
+  } else {
+    const T y = xor_lane<STRIDE>(x);
+    const bool lower = (lane & STRIDE) == 0;
+    const bool desc = (lane & SIZE) == 0;
+    x = (lower == desc) ? tmax(x, y) : tmin(x, y);
+    return sort_stage<SIZE, STRIDE / 2>(x, lane);
+  }
+}
+template <int SIZE, typename T>
+__device__ __forceinline__ T sort_sizes(T x, int lane) {
+  if constexpr (SIZE > 64) {
+    return x;
+  } else {
+    x = sort_stage<SIZE, SIZE / 2>(x, lane);
+    return sort_sizes<SIZE * 2>(x, lane);
+  }
+}
 template <typename T>
 __device__ __forceinline__ T wave_sort_desc(T x) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const T y = xor_lane_s(x, stride);
-      const bool lower = (lane & stride) == 0;
-      const bool desc = (lane & size) == 0;
-      x = (lower == desc) ? tmax(x, y) : tmin(x, y);
-    }
+  return sort_sizes<2>(x, lane_id());
+}
+
+// Half-cleaner steps of a bitonic merge (descending), strides STRIDE..1.
+template <int STRIDE, typename T>
+__device__ __forceinline__ T merge_stage(T c, int lane) {
+  if constexpr (STRIDE == 0) {
+    return c;
+  } else {
+    const T y = xor_lane<STRIDE>(c);
+    c = ((lane & STRIDE) == 0) ? tmax(c, y) : tmin(c, y);
+    return merge_stage<STRIDE / 2>(c, lane);
   }
-  return x;
 }
 
 // a and b sorted descending across lanes: the 64 largest of their union,
 // sorted descending (max with the reversed b is bitonic, then 6 merge steps).
 template <typename T>
 __device__ __forceinline__ T wave_merge_top64(T a, T b) {
-  const int lane = lane_id();
-  T c = tmax(a, rev_lanes(b));
-#pragma unroll
-  for (int stride = 32; stride > 0; stride >>= 1) {
-    const T y = xor_lane_s(c, stride);
-    c = ((lane & stride) == 0) ? tmax(c, y) : tmin(c, y);
-  }
-  return c;
+  return merge_stage<32>(tmax(a, rev_lanes(b)), lane_id());
 }
 
 }  // namespace tgs

@@ -1,49 +1,47 @@
 // tgs_k64.hip -- one fused kernel for batches whose rows are greedy or sample
 // with 1 <= top_k <= 64 (the launch's batch hint promises it).
 //
-// Workgroup (b, c) of K64_NT = 256 threads (4 waves) owns chunk c of row b:
-// S chunks per row, each one tile of at most 16384 ids (64 per thread:
-// sixteen 16-byte vectors of fp32 or eight of bf16).
-//
-// Loads.  At entry a thread requests everything it reads: four history ids,
-// the tile and (with a mask table) the mask word of each of its vectors; the
-// row's parameters come through the scalar cache.  In the vector variant
-// every load is issued unconditionally (addresses clamped into the chunk,
-// values past its end replaced afterwards), so the same number of loads is
-// in flight on every path and each use waits for exactly the loads it needs:
-// the history counts are built while the tile streams in, and the values of
-// a vector are computed as soon as it arrives.
-//
-// History.  The row's history ids that fall in the chunk are counted in LDS
-// (a 16-bit count per id of the tile, two per word) and marked in a bitmap
-// of the tile by owner thread.  The value pass leaves marked elements out
-// (-inf); the thread whose insertion of an id came first (its producer)
-// loads that id's logit once, penalises it and adds it to its wave's
-// candidates, so history ids cost one lane each, not a pass over the tile.
-//
-// Candidates.  Every wave sorts its threads' maxima (bitonic, in registers);
-// the k-th and ceil(k/4)-th entries of all waves give a threshold T with at
-// least k elements of the tile at or above it.  Each wave stages the vectors
-// whose maximum reaches T (placed by ballot prefix counts), tests their
-// elements one per lane, sorts its candidates in registers (64 at a time),
-// and wave 0 merges the four waves' top 64.  A wave with more candidates
-// than its staging holds (ties, skewed tiles) sends the workgroup down an
-// exact path: radix selection of the k-th composite, then ranking of the k
-// candidates at or above it.
+// Workgroup (b, c) of K64_NT threads owns chunk c of row b: S chunks per
+// row, each at most K64_NT * K64_NVT sixteen-byte vectors (thread t holding
+// chunk vectors t, t + K64_NT, ...).  Everything a thread reads is requested
+// at entry: the row's parameters, its history ids, its vectors and (with a
+// mask table) their mask words, so the whole chunk is in flight at once.
+// Under a full-chip stream the chunk's data lands in one burst near the end
+// of the stream, so the steps after it are kept short:
+//   1. Vector maxima and thread maxima of the raw logits (ids the mask
+//      forbids and ids past the chunk left out; history ids included).
+//   2. A bound: the larger of (the minimum over waves of the wave's
+//      ceil(k / waves)-th largest thread maximum) and (the maximum over
+//      waves of the wave's k-th largest), read from one wave sort each.  At
+//      least k distinct ids have a raw logit at or above it.  The collection
+//      threshold cz lies 16 representable values below it.
+//   3. Every vector whose maximum reaches cz is staged whole in its wave's
+//      LDS list.
+//   4. One staged vector per lane: the canonical logit y = z / T of each
+//      element (correctly rounded, tg_div_t), history ids left to their
+//      producers (the lane whose insertion created the id's LDS hash slot
+//      loads its logit at entry and adds its penalised value), the mask
+//      test, and a wave-aggregated append to the LDS candidate buffer that
+//      also counts the candidates strictly above yc = cz / T.
+//   5. An id left out is not a history id and has z < cz, so its y is at
+//      most yc: with at least k candidates strictly above yc the chunk's top
+//      k are among the candidates and are ranked into wave 0.  Otherwise
+//      (ties, penalties that move the top ids, skewed chunks) an exact radix
+//      selection runs over the chunk read again from memory.
 //
 // Rows split over S > 1 chunks.  Each workgroup counts itself in the row's
 // arrival counter at entry (a relaxed device atomic issued with the loads).
 // The workgroup that arrives last merges the row: every other workgroup of
-// the row has started by then and will store its chunk's sorted list with
-// agent-coherent stores (written through past the per-XCD L2s, which are not
-// coherent with each other) without waiting for anything, so the merging
-// workgroup polls those lists with agent-coherent loads until no entry holds
-// the empty marker, merges them with its own, finishes the row (masses,
-// top-p, draw) and resets the lists to the marker and the counter to zero
-// for the next call.  The wait is bounded: one that runs out (it cannot
-// while every workgroup runs) writes id -4 for the row.  No fence is issued:
-// on this part an agent-scope release or acquire fence writes back or
-// invalidates the whole L2 of the XCD.
+// the row has started by then and stores its sorted list with agent-coherent
+// stores (written through past the per-XCD L2s, which are not coherent with
+// each other) without waiting for anything.  The merging workgroup polls
+// those lists with agent-coherent loads, one list per wave, until no entry
+// holds the empty marker, merges them with its own (a tree of wave merges),
+// finishes the row (masses, top-p, draw) and resets the lists to the marker
+// and the counter to zero for the next call.  The wait is bounded: one that
+// runs out (it cannot while every workgroup runs) writes id -4 for the row.
+// No fence is issued: on this part an agent-scope release or acquire fence
+// writes back or invalidates the whole L2 of the XCD.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 #include "tgs_row.h"
@@ -51,191 +49,34 @@
 namespace tgs {
 namespace k64 {
 
-constexpr int BS = K64_NT;
-constexpr int NWB = BS / 64;
-constexpr int KM = 64;                   // largest top_k served
-constexpr int NHID = K64_MAX_HIST / BS;  // history ids per thread
-constexpr u64 EMPTY = ~0ull;             // list entry not written yet: above every composite
-constexpr int SPIN_LIMIT = 1 << 18;      // polls of one list before the wait gives up
-constexpr int KM_PRE = 2;                // lists per wave the merging workgroup requests early (S <= 8)
+constexpr int NVT = K64_NVT;         // 16-byte vectors per thread
+constexpr int P1 = NVT / 2;          // vectors behind the bound
+constexpr int KM = 64;               // largest top_k served
+constexpr int CAP = K64_CAP;         // candidate buffer entries
+constexpr u64 EMPTY = ~0ull;         // list entry not written yet: above every composite
+constexpr int SPIN_LIMIT = 1 << 18;  // polls of one list before the wait gives up
+constexpr uint32_t KEY_MIN = 0x00800000u;  // key of -FLT_MAX: below it only -inf and NaN
 
-// A tile gives every thread 64 elements: 16384 ids.
-template <typename Tin>
-struct TileK {
+template <typename Tin, int NTT>
+struct Geo {
   static constexpr int EPV = Elem<Tin>::EPV;
-  static constexpr int EPT = 64;
-  static constexpr int U = EPT / EPV;  // 16-byte vectors per thread
-  static constexpr int SIZE = BS * EPT;
-  static_assert(SIZE == K64_TILE, "tile size");
-};
-constexpr int BITMAP_WORDS = K64_BITMAP_WORDS;  // one bit per id of a tile
-constexpr int CNT_WORDS = K64_TILE / 2;         // 16-bit history counts, two per word
-static_assert(BITMAP_WORDS * 32 == K64_TILE, "bitmap covers a tile");
-
-// id of element j of this thread in the tile starting at t0
-template <int EPV>
-__device__ __forceinline__ int id_of(int t0, int j) {
-  return t0 + ((j / EPV) * BS + (int)threadIdx.x) * EPV + (j % EPV);
-}
-
-// The tile's 16-byte vectors.  VEC: the chunk holds whole vectors (rows
-// aligned, chunk ends multiples of the vector); a vector past the chunk end
-// is read at the chunk's last vector and replaced by NaN in the value pass.
-// Otherwise ids at or past v1 read as NaN here (checked loads).
-template <typename Tin, bool VEC, int U = TileK<Tin>::U>
-__device__ __forceinline__ void load_tile(const Tin* rowp, int t0, int v1, bool aligned, uint4 (&raw)[U]) {
-  constexpr int EPV = TileK<Tin>::EPV;
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
-    if constexpr (VEC) raw[u] = tg_load_nt(rowp + (v < v1 ? v : v1 - EPV));
-    else raw[u] = load_vec<Tin>(rowp, v, v1, aligned);
-  }
-}
-
-// Mask word of each vector (unconditional; rows without a mask read a valid
-// table row and ignore it).
-template <typename Tin, int U = TileK<Tin>::U>
-__device__ __forceinline__ void load_mask(const uint32_t* mrow, int t0, int v1, uint32_t (&mw)[U]) {
-  constexpr int EPV = TileK<Tin>::EPV;
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
-    mw[u] = mrow[(v < v1 ? v : v1 - 1) >> 5];
-  }
-}
-
-// Logit of element e of a vector; NaN for a vector past the chunk end.
-template <typename Tin>
-__device__ __forceinline__ float elem_z(const uint4& raw, int e, bool past) {
-  const float z = Elem<Tin>::get(raw, e);
-  return past ? __builtin_nanf("") : z;
-}
-
-// y = logit / T over a tile with no mask and no history ids.  NaN and -inf
-// (ids past the chunk end read as NaN) never pass a threshold test or raise
-// a maximum.  vm[u]: the maximum of vector u.  Returns the thread maximum.
-// tail: vectors past the chunk end were read at a clamped address.
-template <typename Tin, int U = TileK<Tin>::U>
-__device__ __forceinline__ float values_plain(const Row& r, int t0, bool tail, const uint4 (&raw)[U],
-                                              float (&y)[TileK<Tin>::EPT], float (&vm)[U]) {
-  constexpr int EPV = TileK<Tin>::EPV;
-  float mx = -__builtin_inff();
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    const bool past = tail && t0 + (u * BS + (int)threadIdx.x) * EPV >= r.v1;
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int e = 0; e < EPV; e++) {
-      y[u * EPV + e] = row_y(r, elem_z<Tin>(raw[u], e, past));
-      m = fmaxf(m, y[u * EPV + e]);
-    }
-    vm[u] = m;
-    mx = fmaxf(mx, m);
-  }
-  return mx;
-}
-
-// The same with the grammar mask and the history ids of the tile left out
-// (-inf; their penalised values join the candidates separately).  hb: this
-// thread's history elements, bit j for element j.
-template <typename Tin, bool MASK, int U = TileK<Tin>::U>
-__device__ __forceinline__ float values_general(const Row& r, u64 hb, int t0, bool tail, const uint4 (&raw)[U],
-                                                const uint32_t (&mw)[U], float (&y)[TileK<Tin>::EPT],
-                                                float (&vm)[U]) {
-  constexpr int EPV = TileK<Tin>::EPV;
-  constexpr uint32_t GM = (1u << EPV) - 1u;
-  const float ninf = -__builtin_inff();
-  const uint32_t hlo = (uint32_t)hb, hhi = (uint32_t)(hb >> 32);
-  float mx = ninf;
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int v = t0 + (u * BS + (int)threadIdx.x) * EPV;
-    const bool past = tail && v >= r.v1;
-    uint32_t d = ((u * EPV < 32 ? hlo : hhi) >> ((u * EPV) & 31)) & GM;
-    if constexpr (MASK) {
-      if (r.mrow) d |= ~(mw[u] >> (v & 31)) & GM;
-    }
-#pragma unroll
-    for (int e = 0; e < EPV; e++) y[u * EPV + e] = row_y(r, elem_z<Tin>(raw[u], e, past));
-    if (d) {
-#pragma unroll
-      for (int e = 0; e < EPV; e++) y[u * EPV + e] = ((d >> e) & 1u) ? ninf : y[u * EPV + e];
-    }
-    float m = ninf;
-#pragma unroll
-    for (int e = 0; e < EPV; e++) m = fmaxf(m, y[u * EPV + e]);
-    vm[u] = m;
-    mx = fmaxf(mx, m);
-  }
-  return mx;
-}
-
-// An order key T with at least k allowed elements of key >= T in the tile:
-// the larger of (max over waves of the wave's k-th largest thread maximum)
-// and (min over waves of the wave's ceil(k / waves)-th largest thread
-// maximum), read from each wave's sorted thread maxima.  mx: this thread's
-// maximum y.  Ends with a barrier.
-__device__ __forceinline__ uint32_t first_threshold(float mx, int k, uint32_t* thr_w) {
-  const uint32_t key = mx > -__builtin_inff() ? tg_key(mx) : 0u;
-  const uint32_t srt = wave_sort_desc(key);  // lane i: the (i+1)-th largest
-  const uint32_t tk = __builtin_amdgcn_readlane(srt, k - 1);
-  const uint32_t tj = __builtin_amdgcn_readlane(srt, (k + NWB - 1) / NWB - 1);
-  const int w = threadIdx.x >> 6;
-  if (lane_id() == 0) {
-    thr_w[w] = tk;
-    thr_w[NWB + w] = tj;
-  }
-  __syncthreads();
-  uint32_t hi = 0, lo = 0xFFFFFFFFu;
-#pragma unroll
-  for (int i = 0; i < NWB; i++) {
-    hi = thr_w[i] > hi ? thr_w[i] : hi;
-    lo = thr_w[NWB + i] < lo ? thr_w[NWB + i] : lo;
-  }
-  return hi > lo ? hi : lo;
-}
-
-// Smallest y whose key is at least the key part of composite threshold thr
-// (-FLT_MAX when that admits every allowed value).
-__device__ __forceinline__ float thr_value(u64 thr) {
-  const uint32_t tk = (uint32_t)(thr >> 32);
-  const uint32_t kmin = 0x00800000u;  // key of -FLT_MAX
-  return tk <= kmin ? -3.40282347e38f : tg_unkey(tk);
-}
-
-// Candidate buffer (LDS).  Common path, per wave: up to VCAP candidate
-// vectors (a vector whose maximum reaches the threshold value tf; tf is the
-// value of a threshold whose low, id part is 1, so y >= tf is the composite
-// test for any id) as EPV floats each plus the id of their first element,
-// and a list of up to LCAP candidate composites.  The exact path (a wave
-// with more candidate vectors or candidates than that) reuses the same
-// memory for up to CCAP compacted candidates (+ 16 pad entries for the rank
-// counting).
-constexpr int VCAP = 64;
-constexpr int LCAP = 256;
-constexpr int CCAP = K64_CAP;
-static_assert(CCAP + 16 <= K64_CAND_ENTRIES, "candidate buffer");
-
-template <typename Tin>
-struct Stage {
-  static constexpr int EPV = Elem<Tin>::EPV;
-  static constexpr int VALS = NWB * VCAP * EPV;  // floats
-  static constexpr int IDS = NWB * VCAP;         // ints
-  static constexpr int BYTES = VALS * 4 + IDS * 4 + NWB * LCAP * 8;
-  static_assert(BYTES <= K64_CAND_ENTRIES * 8, "stage fits the candidate buffer");
+  static constexpr int NW = NTT / 64;
+  static constexpr int CH = NTT * NVT * EPV;  // ids of a chunk at most
+  static constexpr int NHID = (K64_MAX_HIST + NTT - 1) / NTT;  // history ids per thread
+  static constexpr uint32_t GM = (1u << EPV) - 1u;
 };
 
-// cmp[0, n) holds unique composites (published by a barrier; room for 16
-// pad entries).  Writes the min(n, k) largest to top[rank] (rank 0 = the
-// largest).  The rank of an entry is the number of entries above it; P
-// adjacent threads (P a power of two, P * n <= BS where possible) each count
-// over one segment of the buffer with 16-byte broadcast reads and sum with
-// lane shuffles.  Ends with a barrier.
 struct alignas(16) u64x2 {
   u64 x, y;
 };
 
+// The min(n, k) largest of the unique composites cmp[0, n) (published by a
+// barrier; room for 16 pad entries past n) into top[rank], rank 0 the
+// largest.  The rank of an entry is the number of entries above it; P
+// adjacent threads (P a power of two, P n <= BS where possible) each count
+// over one segment of the buffer with 16-byte broadcast reads and sum with
+// lane moves.  Ends with a barrier.
+template <int BS>
 __device__ __forceinline__ void rank_into(u64* cmp, u64* top, int n, int k) {
   int P = 1;
   while (P < 8 && n * P * 2 <= BS) P <<= 1;
@@ -263,42 +104,88 @@ __device__ __forceinline__ void rank_into(u64* cmp, u64* top, int n, int k) {
   __syncthreads();
 }
 
-// Calls f(x) for every candidate composite x of this thread, re-reading the
-// tile (the exact path: a rolled loop keeps registers free).
-template <typename Tin, bool MASK, class F>
-__device__ __forceinline__ void each_cand(const Row& r, bool has_hist, const uint32_t* bitmap, const uint32_t* hcnt,
-                                          const Tin* rowp, int t0, float tf, F f) {
-  constexpr int EPV = TileK<Tin>::EPV;
-#pragma unroll 1
-  for (int j = 0; j < TileK<Tin>::EPT; j++) {
-    const int id = id_of<EPV>(t0, j);
-    if (id >= r.v1) continue;
-    const float z = Elem<Tin>::scalar(rowp, id);
-    float yy = row_y(r, z);
-    if (has_hist && ((bitmap[2 * threadIdx.x + (j >> 5)] >> (j & 31)) & 1u)) {
-      const int loc = id - t0;
-      yy = row_y(r, penalise(z, (int)((hcnt[loc >> 1] >> ((loc & 1) * 16)) & 0xFFFFu), r));
-    }
-    if (yy >= tf && (!MASK || mask_allows(r, id))) f(comp_key(tg_key(yy), id));
+// Tree merge of the waves' sorted top-64 lists (lane i = rank i): after it,
+// wave 0 holds the top 64 of their union, sorted.  Each slot is written once
+// (by its wave, at the level it sends), so one barrier per level suffices.
+// Called by all waves; ends with a barrier.
+template <int NW, typename T>
+__device__ __forceinline__ T merge_waves(T acc, T (*slots)[64]) {
+  const int w = threadIdx.x >> 6, lane = lane_id();
+#pragma unroll
+  for (int step = 1; step < NW; step <<= 1) {
+    if ((w & (2 * step - 1)) == step) slots[w][lane] = acc;
+    __syncthreads();
+    if ((w & (2 * step - 1)) == 0) acc = wave_merge_top64(acc, slots[w + step][lane]);
   }
+  __syncthreads();
+  return acc;
 }
 
-// Tree merge of the waves' sorted top-64 lists (lane i = rank i) held in
-// tops[w]: after it, wave 0 returns the top 64 of their union, sorted.
-// Called by all waves; ends with a barrier; only wave 0's result counts.
-__device__ __forceinline__ u64 merge_waves(u64 acc, u64 (*tops)[64]) {
+// The sorted top k of buf[0, n) (n <= CAP, unique composites) in wave 0's
+// lanes: ranking for short buffers, wave sorts of 64-entry slices merged
+// as a tree otherwise.  Ends with a barrier.
+template <int NTT>
+__device__ __forceinline__ u64 select_top(u64* buf, int n, int k, u64 (*slots)[64]) {
+  constexpr int NW = NTT / 64;
   const int w = threadIdx.x >> 6, lane = lane_id();
-  tops[w][lane] = acc;
-  __syncthreads();
-#pragma unroll
-  for (int step = 1; step < NWB; step <<= 1) {
-    if ((w & (2 * step - 1)) == 0 && w + step < NWB) {
-      acc = wave_merge_top64(acc, tops[w + step][lane]);
-      tops[w][lane] = acc;
-    }
+  if (n <= 256) {
+    u64* top = slots[NW - 1];
+    if (threadIdx.x < 64) top[threadIdx.x] = 0ull;
     __syncthreads();
+    rank_into<NTT>(buf, top, n, k);
+    return lane < k ? top[lane] : 0ull;
   }
-  return acc;
+  u64 acc = 0ull;
+  bool first = true;
+  for (int s0 = w * 64; s0 < n; s0 += NTT) {
+    u64 x = s0 + lane < n ? buf[s0 + lane] : 0ull;
+    x = wave_sort_desc(x);
+    acc = first ? x : wave_merge_top64(acc, x);
+    first = false;
+  }
+  acc = merge_waves<NW>(acc, slots);
+  return lane < k ? acc : 0ull;
+}
+
+// Wave-aggregated append of composite x (when ok) to the LDS buffer.
+__device__ __forceinline__ void append(bool ok, u64 x, u64* buf, unsigned* nbuf) {
+  const u64 bal = __ballot(ok);
+  if (bal == 0ull) return;
+  unsigned base = 0;
+  if (lane_id() == 0) base = atomicAdd(nbuf, (unsigned)__popcll(bal));
+  base = (unsigned)__shfl((int)base, 0, 64);
+  const unsigned sl = base + lanes_below(bal);
+  if (ok && sl < (unsigned)CAP) buf[sl] = x;
+}
+
+// Wave-aggregated append of up to N composites per lane (entry q when
+// ok[q]) to the LDS buffer, counting the appended entries whose key is above
+// kc: one LDS atomic per wave on a packed counter (appended entries in the
+// low 16 bits, entries above kc in the high 16), slots from a wave prefix
+// sum of the lanes' counts.
+template <int N>
+__device__ __forceinline__ void append_n(const u64 (&x)[N], const bool (&ok)[N], uint32_t kc, u64* buf,
+                                         unsigned* packed) {
+  unsigned cnt = 0, abv = 0;
+#pragma unroll
+  for (int q = 0; q < N; q++) {
+    cnt += ok[q] ? 1u : 0u;
+    abv += (ok[q] && (uint32_t)(x[q] >> 32) > kc) ? 1u : 0u;
+  }
+  const unsigned v = cnt | (abv << 16);
+  const unsigned incl = wave_incl_scan(v);
+  const unsigned tot = readlane_u32(incl, 63);
+  if (tot == 0u) return;
+  unsigned base = 0;
+  if (lane_id() == 0) base = atomicAdd(packed, tot);
+  base = readlane_u32(base, 0) & 0xFFFFu;
+  unsigned sl = base + ((incl - v) & 0xFFFFu);
+#pragma unroll
+  for (int q = 0; q < N; q++)
+    if (ok[q]) {
+      if (sl < (unsigned)CAP) buf[sl] = x[q];
+      sl++;
+    }
 }
 
 // Row finish by one wave; x: lane i holds the row's i-th kept composite
@@ -327,31 +214,104 @@ __device__ __forceinline__ void wave_finish_row(const SampleArgs& a, const Row& 
   }
 }
 
-template <typename Tin, bool VEC, bool MASK>
-__global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
-  using TL = TileK<Tin>;
+// Calls f(composite) for every allowed, non-history id of the chunk (and
+// each history composite of this thread), reading the chunk again from
+// memory in a rolled loop (the exact path keeps the registers free).
+template <typename Tin, int NTT, int NHID, class F>
+__device__ __forceinline__ void each_allowed(const SampleArgs& a, const Row& r, const Tin* rowp, int nvec, bool pen,
+                                             const uint32_t* bitmap, bool masked, const u64 (&hcomp)[NHID], F f) {
+  constexpr int EPV = Elem<Tin>::EPV;
+#pragma unroll 1
+  for (int j = threadIdx.x; j < nvec; j += NTT) {
+    const int vid = r.v0 + j * EPV;
+    const uint4 v = load_vec<Tin>(rowp, vid, r.v1, a.aligned);
+    const uint32_t o = (uint32_t)(j * EPV);
+    const uint32_t hw = pen ? bitmap[o >> 5] >> (o & 31) : 0u;
+    const uint32_t mwv = masked ? r.mrow[vid >> 5] >> (vid & 31) : 0xFFFFFFFFu;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) {
+      if (((hw >> e) & 1u) || !((mwv >> e) & 1u)) continue;
+      const float y = row_y(r, Elem<Tin>::get(v, e));  // ids past the chunk read as NaN
+      if (y > -__builtin_inff()) f(comp_key(tg_key(y), vid + e));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NHID; q++)
+    if (hcomp[q] != 0ull) f(hcomp[q]);
+}
+
+// The exact path: the k-th composite of the chunk by radix selection, the k
+// entries at or above it (composites are unique), ranked into wave 0.
+template <typename Tin, int NTT, bool MASK, int NHID>
+__device__ __forceinline__ u64 exact_top(const SampleArgs& a, const Row& r, const Tin* rowp, int nvec, bool pen,
+                                      const uint32_t* bitmap, bool masked, const u64 (&hcomp)[NHID], int k, u64* buf,
+                                      unsigned* nbuf, u64 (*slots)[64], BlockScratch& bs) {
+  auto en = [&](auto f) { each_allowed<Tin, NTT, NHID>(a, r, rowp, nvec, pen, bitmap, masked, hcomp, f); };
+  const u64 T = block_select_kth<u64, 64, NTT>(en, (unsigned)k, bs);
+  if (threadIdx.x == 0) *nbuf = 0;
+  __syncthreads();
+  en([&](u64 x) {
+    if (x >= T) buf[atomicAdd(nbuf, 1u)] = x;  // exactly k entries
+  });
+  __syncthreads();
+  const int n2 = (int)*nbuf;
+  return select_top<NTT>(buf, n2 < CAP ? n2 : CAP, k, slots);
+}
+
+// Debug output: the canonical logit of every non-history id of the chunk
+// (history ids are written by their producers), -inf where not allowed.
+template <typename Tin, int NTT>
+__device__ __forceinline__ void post_logits_chunk(const SampleArgs& a, const Row& r, const Tin* rowp, int nvec, bool pen,
+                                               const uint32_t* bitmap, bool masked) {
+  constexpr int EPV = Elem<Tin>::EPV;
+  float* post = a.dbg.post_logits + (long long)r.b * a.V;
+#pragma unroll 1
+  for (int j = threadIdx.x; j < nvec; j += NTT) {
+    const int vid = r.v0 + j * EPV;
+    const uint4 v = load_vec<Tin>(rowp, vid, r.v1, a.aligned);
+    const uint32_t o = (uint32_t)(j * EPV);
+    const uint32_t hw = pen ? bitmap[o >> 5] >> (o & 31) : 0u;
+    const uint32_t mwv = masked ? r.mrow[vid >> 5] >> (vid & 31) : 0xFFFFFFFFu;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) {
+      const int id = vid + e;
+      if (id >= r.v1 || ((hw >> e) & 1u)) continue;
+      const float y = row_y(r, Elem<Tin>::get(v, e));
+      post[id] = (((mwv >> e) & 1u) && y > -__builtin_inff()) ? y : -__builtin_inff();
+    }
+  }
+}
+
+template <typename Tin, int NTT, bool VEC, bool MASK>
+__global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
+  using G = Geo<Tin, NTT>;
+  constexpr int EPV = G::EPV, NW = G::NW, NHID = G::NHID;
+  constexpr uint32_t GM = G::GM;
+  constexpr int SCAP = 64;   // staged vectors per wave
   TGS_DYN_SMEM(smem);
-  __shared__ uint32_t thr_w[2 * NWB];
-  __shared__ u64 tops[NWB][64];
-  __shared__ u64 own[64];
-  __shared__ unsigned nbuf, nhist;
-  __shared__ int ovf, elect, tmo;
+  __shared__ u64 slots[NW][64];      // wave lists (merges, the ranked top k)
+  __shared__ uint4 svec[NW][SCAP];   // per wave: vectors whose maximum reaches the collection threshold
+  __shared__ int sidx[NW][SCAP];     // their vector index in the chunk
+  __shared__ uint32_t wkey[2][NW];   // per wave: its ceil(k / NW)-th and k-th largest thread maximum keys
+  __shared__ unsigned nbuf;          // candidates appended (low 16 bits), of them above yc (high 16)
+  __shared__ int elect, tmo, spill;
   __shared__ BlockScratch bs;
-  uint32_t* hcnt = (uint32_t*)(smem + a.off_hash);
+  int2* hash = (int2*)(smem + a.off_hash);
   uint32_t* bitmap = (uint32_t*)(smem + a.off_bitmap);
-  u64* cand = (u64*)(smem + a.off_cand);
+  u64* buf = (u64*)(smem + a.off_cand);
   const int w = threadIdx.x >> 6, lane = lane_id();
 
   const int b = blockIdx.x / a.S, c = blockIdx.x % a.S;
   if (b >= a.B) return;
-  const int v0 = c * a.L, v1 = min(a.V, v0 + a.L);
+  const int v0 = c * a.L, v1 = min(a.V, v0 + a.L);  // a.L is a multiple of EPV
+  const int nvec = (v1 - v0 + EPV - 1) / EPV;
+  const int nfull = nvec / NTT;  // vectors every thread holds
   const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
-  const bool full = v0 + TL::SIZE <= v1;
   unsigned* cnt = a.cnt + (long long)b * K64_CNT_STRIDE;
 
-  // everything read first, in one round trip, in the order it is needed (a
-  // wave's loads return in order): the row's parameters, its history length
-  // and ids, the arrival count, the tile
+  // ---- everything read first, in the order it is needed (a wave's loads
+  // return in order): the row's parameters, its history length and ids, the
+  // arrival count, the chunk, the mask words
   const tgs_row_params p = a.params[b];
   const float ub = a.u[b];
   const int hlr = *(a.hist_len ? a.hist_len + b : (const int*)a.params);
@@ -361,14 +321,23 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
   int hid[NHID];
 #pragma unroll
   for (int q = 0; q < NHID; q++) {
-    const int j = (int)threadIdx.x + q * BS;
+    const int j = (int)threadIdx.x + q * NTT;
     hid[q] = hp[j < hlast ? j : hlast];
   }
   unsigned arrived = 0;
   if (a.S > 1 && threadIdx.x == 0)
     arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  uint4 raw[TL::U];
-  load_tile<Tin, VEC>(rowp, v0, v1, a.aligned, raw);
+  uint4 raw[NVT];
+#pragma unroll
+  for (int i = 0; i < NVT; i++) {
+    const int j = (int)threadIdx.x + i * NTT;
+    if (i * NTT < nvec) {  // whole-workgroup test: vectors wholly past the chunk are not read
+      if constexpr (VEC) raw[i] = tg_load_nt(rowp + v0 + (j < nvec ? j : nvec - 1) * EPV);
+      else raw[i] = load_vec<Tin>(rowp, v0 + j * EPV, v1, a.aligned);
+    } else {
+      raw[i] = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);  // NaN: never counted
+    }
+  }
   const int hl = a.hist_len ? hlr : a.hist_cap;
 
   Row r;
@@ -386,234 +355,251 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
   const int k = r.mode == 0 ? 1 : r.k;
   r.v0 = v0;
   r.v1 = v1;
-  float* post = a.dbg.post_logits ? a.dbg.post_logits + (long long)b * a.V : nullptr;
-  uint32_t mw[TL::U];
-  if constexpr (MASK) load_mask<Tin>(r.mrow ? r.mrow : a.mask_table, v0, v1, mw);
+  const bool masked = MASK && r.mrow != nullptr;
+  uint32_t mw[MASK ? NVT : 1];
+  if constexpr (MASK) {
+    const uint32_t* mrow = r.mrow ? r.mrow : a.mask_table;
+#pragma unroll
+    for (int i = 0; i < NVT; i++) {
+      const int j = (int)threadIdx.x + i * NTT;
+      mw[i] = (i * NTT < nvec) ? mrow[(v0 + (j < nvec ? j : nvec - 1) * EPV) >> 5] : 0u;
+    }
+  }
 
+  // ---- history: each id of the chunk counted in the LDS hash (its
+  // producer is the lane that created its slot) and marked in the bitmap
   if (threadIdx.x == 0) {
     nbuf = 0;
-    nhist = 0;
-    ovf = 0;
     tmo = 0;
+    spill = 0;
+    elect = a.S > 1 && arrived == (unsigned)(a.S - 1);
   }
-  // history: count of every id of the tile, and per thread a 64-bit mask of
-  // its elements that are history ids (two words per thread; bitmap[2t + h]);
-  // the first insertion of each id makes its thread the id's producer
-  bool prod[NHID];
+  const bool pen = r.use_pen;
+  const int bmw = (v1 - v0 + 31) >> 5;
+  int hslot[NHID];
 #pragma unroll
-  for (int q = 0; q < NHID; q++) prod[q] = false;
-  if (r.use_pen) {
-#pragma unroll
-    for (int i = 0; i < CNT_WORDS / 4 / BS; i++) ((uint4*)hcnt)[threadIdx.x + i * BS] = make_uint4(0u, 0u, 0u, 0u);
-    for (int i = threadIdx.x; i < BITMAP_WORDS; i += BS) bitmap[i] = 0u;
+  for (int q = 0; q < NHID; q++) hslot[q] = -1;
+  if (pen) {
+    for (int i = threadIdx.x; i < a.TS; i += NTT) hash[i] = make_int2(-1, 0);
+    for (int i = threadIdx.x; i < bmw; i += NTT) bitmap[i] = 0u;
     __syncthreads();
-    unsigned mine = 0;
+    const unsigned tmask = (unsigned)a.TS - 1u;
 #pragma unroll
     for (int q = 0; q < NHID; q++) {
       const int id = hid[q];
-      if ((int)threadIdx.x + q * BS < r.H && id >= v0 && id < v1) {
-        const int loc = id - v0;                              // < TileK::SIZE
-        const unsigned old = atomicAdd(&hcnt[loc >> 1], 1u << ((loc & 1) * 16));
-        prod[q] = ((old >> ((loc & 1) * 16)) & 0xFFFFu) == 0u;  // first occurrence: this id's producer
-        const int u = loc / (BS * TL::EPV), rr = loc % (BS * TL::EPV);
-        const int t = rr / TL::EPV, el = u * TL::EPV + rr % TL::EPV;  // owner thread, its element
-        atomicOr(&bitmap[2 * t + (el >> 5)], 1u << (el & 31));
-        mine++;
+      if ((int)threadIdx.x + q * NTT < r.H && id >= v0 && id < v1) {
+        unsigned h = hash_slot(id, a.ts_shift);
+        for (;;) {  // the table has at least twice as many slots as history entries
+          const int old = atomicCAS(&hash[h].x, -1, id);
+          if (old == -1 || old == id) {
+            atomicAdd(&hash[h].y, 1);
+            if (old == -1) hslot[q] = (int)h;
+            break;
+          }
+          h = (h + 1) & tmask;
+        }
+        atomicOr(&bitmap[(id - v0) >> 5], 1u << ((id - v0) & 31));
       }
     }
-    if (mine) atomicAdd(&nhist, mine);
   }
   __syncthreads();
-  const bool has_hist = r.use_pen && nhist > 0;
-  u64 hb = 0;
-  if (has_hist) hb = ((u64)bitmap[2 * threadIdx.x + 1] << 32) | bitmap[2 * threadIdx.x];
-  // producers' logits (and mask words): one load per history id of this
-  // thread, issued behind the tile and first needed after the threshold;
-  // the loads are unconditional (others read id v0) to keep the count fixed
+  // producers' logits (and mask words): one load per history id of the
+  // chunk, first needed after the bound
   float zq[NHID];
   uint32_t mq[NHID];
 #pragma unroll
   for (int q = 0; q < NHID; q++) {
-    const int id = prod[q] ? hid[q] : v0;
-    zq[q] = Elem<Tin>::scalar(rowp, id);
-    if constexpr (MASK) mq[q] = (r.mrow ? r.mrow : a.mask_table)[id >> 5];
+    zq[q] = 0.0f;
+    mq[q] = 0xFFFFFFFFu;
+    if (hslot[q] >= 0) {
+      zq[q] = Elem<Tin>::scalar(rowp, hid[q]);
+      if (masked) mq[q] = r.mrow[hid[q] >> 5];
+    }
   }
 
-  // values, per-vector maxima, thread maximum
-  float y[TL::EPT];
-  float vm[TL::U];
-  const bool tail = VEC && !full;
-  bool gen = has_hist;
-  if constexpr (MASK) gen = gen || r.mrow != nullptr;
-  const float mx = gen ? values_general<Tin, MASK>(r, hb, v0, tail, raw, mw, y, vm)
-                       : values_plain<Tin>(r, v0, tail, raw, y, vm);
-  if (post) {
+  // ---- 1. vector maxima and thread maximum of the raw logits (history ids
+  // included: a bound from them is checked by counting below); ids the mask
+  // forbids and vectors past the chunk are left out
+  float vm[NVT];
+  float tm = -__builtin_inff();
 #pragma unroll
-    for (int j = 0; j < TL::EPT; j++) {
-      const int id = id_of<TL::EPV>(v0, j);
-      if (id < v1) post[id] = y[j] > -__builtin_inff() ? y[j] : -__builtin_inff();
+  for (int i = 0; i < NVT; i++) {
+    float m;
+    if constexpr (MASK) {
+      const uint32_t x = masked ? ~(mw[i] >> ((v0 + ((int)threadIdx.x + i * NTT) * EPV) & 31)) & GM : 0u;
+      m = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < EPV; e++) m = ((x >> e) & 1u) ? m : fmaxf(m, Elem<Tin>::get(raw[i], e));
+    } else {
+      m = Elem<Tin>::get(raw[i], 0);
+#pragma unroll
+      for (int e = 1; e < EPV; e++) m = fmaxf(m, Elem<Tin>::get(raw[i], e));
     }
+    if (i == nfull) m = ((int)threadIdx.x + i * NTT < nvec) ? m : -__builtin_inff();  // the partial vector round
+    vm[i] = m;
+    tm = fmaxf(tm, m);
   }
-  // candidates are >= thr; every allowed composite is far above the id part
-  if (threadIdx.x == 0) elect = a.S > 1 && arrived == (unsigned)(a.S - 1);  // published by the next barrier
-  const u64 thr = ((u64)first_threshold(mx, k, thr_w) << 32) | 1ull;
-  // the merging workgroup requests the other chunks' lists now, so that
-  // their load overlaps its own candidate work; entries still empty are
-  // polled again at the merge
-  u64 pre[KM_PRE];
-  const bool elected = elect != 0;
-  u64* lists = a.lists + (long long)b * a.S * KM;
-#pragma unroll
-  for (int q = 0; q < KM_PRE; q++) {
-    const int cc = w + q * NWB;
-    pre[q] = (elected && cc < a.S && cc != c)
-                 ? __hip_atomic_load(lists + (long long)cc * KM + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                 : EMPTY;
-  }
-  const float tf = thr_value(thr);
 
-  // Every element >= tf, wave by wave.  A vector whose maximum reaches tf
-  // is staged whole (lanes placed by a ballot prefix count); the staged
-  // elements are then tested one per lane and listed with the wave's history
-  // candidates; the list is sorted in registers and the four waves' top 64
-  // are merged.
-  using ST = Stage<Tin>;
-  float* svals = (float*)cand + w * VCAP * TL::EPV;
-  int* sids = (int*)((float*)cand + ST::VALS) + w * VCAP;
-  u64* wl = (u64*)((int*)((float*)cand + ST::VALS) + ST::IDS) + w * LCAP;
-  unsigned nv = 0;  // candidate vectors of the wave
-#pragma unroll
-  for (int u = 0; u < TL::U; u++) {
-    const bool pv = vm[u] >= tf;
-    const u64 bal = __ballot(pv);
-    if (bal) {
-      const unsigned sl = nv + lanes_below(bal);
-      if (pv && sl < (unsigned)VCAP) {
-        uint4* dst = (uint4*)(svals + sl * TL::EPV);
-#pragma unroll
-        for (int q = 0; q < TL::EPV / 4; q++)
-          dst[q] = make_uint4(tg_f2u(y[u * TL::EPV + 4 * q]), tg_f2u(y[u * TL::EPV + 4 * q + 1]),
-                              tg_f2u(y[u * TL::EPV + 4 * q + 2]), tg_f2u(y[u * TL::EPV + 4 * q + 3]));
-        sids[sl] = id_of<TL::EPV>(v0, u * TL::EPV);
-      }
-      nv += (unsigned)__popcll(bal);
+  // ---- 2. the bound: at least k thread maxima (distinct ids) are >= it:
+  // the larger of (min over waves of the wave's ceil(k / NW)-th largest)
+  // and (max over waves of the wave's k-th largest), both read from one sort
+  {
+    const uint32_t tk = tm > -__builtin_inff() ? tg_key(tm) : 0u;
+    const uint32_t srt = wave_sort_desc(tk);  // lane i: the (i+1)-th largest
+    const uint32_t v1k = readlane_u32(srt, (k + NW - 1) / NW - 1);
+    const uint32_t v2k = readlane_u32(srt, k - 1);
+    if (lane == 0) {
+      wkey[0][w] = v1k;
+      wkey[1][w] = v2k;
     }
   }
-  wave_lds_sync();
-  const unsigned nel = (nv < (unsigned)VCAP ? nv : (unsigned)VCAP) * TL::EPV;
-  unsigned nl = 0;  // list entries of the wave
-  for (unsigned e0 = 0; e0 < nel; e0 += 64) {
-    const unsigned e = e0 + (unsigned)lane;
-    const float yy = e < nel ? svals[e] : -__builtin_inff();
-    const bool pc = yy >= tf;
-    const u64 bal = __ballot(pc);
-    const unsigned sl = nl + lanes_below(bal);
-    if (pc && sl < (unsigned)LCAP) wl[sl] = comp_key(tg_key(yy), sids[e / TL::EPV] + (int)(e % TL::EPV));
-    nl += (unsigned)__popcll(bal);
-  }
-  // history candidates: the penalised logit of each history id of the
-  // chunk, computed by its producer (counts are final since the barrier)
-#pragma unroll
-  for (int q = 0; q < NHID; q++) {
-    u64 x = 0ull;
-    if (prod[q]) {
-      const int id = hid[q], loc = id - v0;
-      const int hc = (int)((hcnt[loc >> 1] >> ((loc & 1) * 16)) & 0xFFFFu);
-      const float yy = row_y(r, penalise(zq[q], hc, r));
-      bool ok = yy > -__builtin_inff();
-      if constexpr (MASK) ok = ok && (!r.mrow || ((mq[q] >> (id & 31)) & 1u));
-      if (post) post[id] = ok ? yy : -__builtin_inff();
-      if (ok) x = comp_key(tg_key(yy), id);
-    }
-    const bool pc = x >= thr;
-    const u64 bal = __ballot(pc);
-    const unsigned sl = nl + lanes_below(bal);
-    if (pc && sl < (unsigned)LCAP) wl[sl] = x;
-    nl += (unsigned)__popcll(bal);
-  }
-  wave_lds_sync();
-  const bool wovf = nv > (unsigned)VCAP || nl > (unsigned)LCAP;
-  // the wave's top 64: its list sorted 64 at a time, merged
-  u64 xs = 0ull;
-  if (!wovf) {
-#pragma unroll 1
-    for (unsigned c0 = 0; c0 < nl; c0 += 64) {
-      u64 x = c0 + (unsigned)lane < nl ? wl[c0 + lane] : 0ull;
-      x = wave_sort_desc(x);
-      xs = c0 == 0 ? x : wave_merge_top64(xs, x);
-    }
-  }
-  if (wovf && lane == 0) ovf = 1;
-  tops[w][lane] = xs;
   __syncthreads();
-  u64 acc = 0ull;  // wave 0: the chunk's top 64 candidates, sorted
-  if (!ovf) {
-    if (w == 0) {
-      acc = xs;
+  uint32_t bkey;
+  {
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
 #pragma unroll
-      for (int i = 1; i < NWB; i++) acc = wave_merge_top64(acc, tops[i][lane]);
+    for (int i = 0; i < NW; i++) {
+      lo = wkey[0][i] < lo ? wkey[0][i] : lo;
+      hi = wkey[1][i] > hi ? wkey[1][i] : hi;
     }
-  } else {
-    // the exact k-th composite among all candidates, then exactly the k
-    // candidates >= it, ranked
-    u64* cmp = cand;
-    auto en = [&](auto f) { each_cand<Tin, MASK>(r, has_hist, bitmap, hcnt, rowp, v0, tf, f); };
-    const u64 T = block_select_kth<u64, 64, BS>(en, (unsigned)k, bs);
-    __syncthreads();
-    int c2 = 0;
-    en([&](u64 x) { c2 += x >= T ? 1 : 0; });
-    unsigned p2 = c2 ? atomicAdd(&nbuf, (unsigned)c2) : 0u;
-    en([&](u64 x) {
-      if (x >= T) cmp[p2++] = x;
-    });
-    __syncthreads();
-    const int nc = (int)nbuf;
-    rank_into(cmp, tops[0], nc, k);
-    const int n = nc < k ? nc : k;
-    acc = lane < n ? tops[0][lane] : 0ull;
+    bkey = lo > hi ? lo : hi;
   }
+  // the collection threshold: 16 representable values below the bound, so
+  // that the ids that set the bound land strictly above its canonical value
+  const bool all = bkey < KEY_MIN + 32u;  // no usable bound: collect every allowed id
+  const float cz = all ? -__builtin_inff() : tg_unkey(bkey - 16u);
+  const float yc = all ? -__builtin_inff() : row_y(r, cz);
+  const uint32_t kc = tg_key(yc);
 
+  // ---- 3. collection: every vector whose maximum reaches cz is staged
+  // whole (its bits and its chunk index) in its wave's list
+  unsigned ns = 0;  // staged vectors of the wave (uniform)
+#pragma unroll
+  for (int i = 0; i < NVT; i++) {
+    const bool pass = vm[i] >= cz && vm[i] > -__builtin_inff();  // (cz may be -inf)
+    const u64 bal = __ballot(pass);
+    if (bal != 0ull) {
+      const unsigned sl = ns + lanes_below(bal);
+      if (pass && sl < (unsigned)SCAP) {
+        svec[w][sl] = raw[i];
+        sidx[w][sl] = (int)threadIdx.x + i * NTT;
+      }
+      ns += (unsigned)__popcll(bal);
+    }
+  }
+  if (ns > (unsigned)SCAP && lane == 0) spill = 1;
+  wave_lds_sync();
+
+  // ---- 4. the staged vectors (one per lane) and the history ids: exact
+  // canonical logits, history ids left to their producers, into the
+  // candidate buffer; the high half of the packed counter counts candidates
+  // strictly above yc
+  {
+    const unsigned nst = ns < (unsigned)SCAP ? ns : (unsigned)SCAP;
+    for (unsigned s0 = 0; s0 < nst; s0 += 64) {
+      const unsigned si = s0 + (unsigned)lane;
+      u64 x[EPV];
+      bool ok[EPV];
+      uint4 v = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);
+      int j = 0;
+      if (si < nst) {
+        v = svec[w][si];
+        j = sidx[w][si];
+      }
+      const int o = j * EPV;
+      const uint32_t hw = (pen && si < nst) ? bitmap[o >> 5] >> (o & 31) : 0u;
+      uint32_t xm = 0u;
+      if constexpr (MASK) xm = (masked && si < nst) ? ~(r.mrow[(v0 + o) >> 5] >> ((v0 + o) & 31)) : 0u;
+#pragma unroll
+      for (int e = 0; e < EPV; e++) {
+        const float z = Elem<Tin>::get(v, e);
+        const float y = row_y(r, z);
+        ok[e] = si < nst && z >= cz && !((hw >> e) & 1u) && !((xm >> e) & 1u) && y > -__builtin_inff() &&
+                j < nvec;
+        x[e] = comp_key(tg_key(y), v0 + o + e);
+      }
+      append_n<EPV>(x, ok, kc, buf, &nbuf);
+    }
+  }
+  u64 hcomp[NHID];
+  {
+    bool hok[NHID];
+#pragma unroll
+    for (int q = 0; q < NHID; q++) {
+      u64 x = 0ull;
+      if (hslot[q] >= 0) {
+        const int id = hid[q];
+        const float y = row_y(r, penalise(zq[q], hash[hslot[q]].y, r));
+        const bool ok = y > -__builtin_inff() && (!masked || ((mq[q] >> (id & 31)) & 1u));
+        if (ok) x = comp_key(tg_key(y), id);
+        if (a.dbg.post_logits) a.dbg.post_logits[(long long)b * a.V + id] = ok ? y : -__builtin_inff();
+      }
+      hcomp[q] = x;
+      hok[q] = x != 0ull && (uint32_t)(x >> 32) >= kc;
+    }
+    append_n<NHID>(hcomp, hok, kc, buf, &nbuf);
+  }
+  __syncthreads();
+
+  // ---- 5. the chunk's sorted top k: from the candidates when they hold at
+  // least k entries strictly above yc (then no id left out can be among the
+  // top k) or every allowed id; otherwise the exact path
+  u64 acc;
+  const int nb = (int)(nbuf & 0xFFFFu), nab = (int)(nbuf >> 16);
+  if (!spill && nb <= CAP && (all || nab >= k)) {
+    acc = select_top<NTT>(buf, nb, k, slots);
+  } else {
+    // exact path (rare: ties, skewed chunks, penalties that move the top
+    // ids): the k-th composite of the chunk by radix selection over the
+    // chunk read again (L2 / MALL hits), then the k entries at or above it
+    acc = exact_top<Tin, NTT, MASK>(a, r, rowp, nvec, pen, bitmap, masked, hcomp, k, buf, &nbuf, slots, bs);
+  }
+  if (a.dbg.post_logits) post_logits_chunk<Tin, NTT>(a, r, rowp, nvec, pen, bitmap, masked);
+
+  // ---- 6. the row
   if (a.S == 1) {
     if (w == 0) {
       const int n = __popcll(__ballot(acc != 0ull));
-      const int nk = n < k ? n : k;
-      wave_finish_row(a, r, lane < nk ? acc : 0ull, nk);
+      wave_finish_row(a, r, acc, n < k ? n : k);
     }
     return;
   }
-  if (!elected) {
+  u64* lists = a.lists + (long long)b * a.S * KM;
+  if (!elect) {
     // publish the chunk's list for the row's merging workgroup
     if (w == 0) __hip_atomic_store(lists + (long long)c * KM + lane, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-
-  // the row's last arrival: merge the S sorted, zero-padded lists
+  // the row's last arrival: one list per wave (own list from wave 0's
+  // registers through LDS), polled in parallel, then a tree of merges
+  u64* own = slots[NW - 1];
   if (w == 0) own[lane] = acc;
   __syncthreads();
   u64 racc = 0ull;
   bool first = true;
-  for (int cc = w; cc < a.S; cc += NWB) {
+  for (int cc = w; cc < a.S; cc += NW) {
     u64 x;
     if (cc == c) {
       x = own[lane];
     } else {
       const u64* lp = lists + (long long)cc * KM + lane;
-      const int q = (cc - w) / NWB;
-      x = q < KM_PRE ? pre[q] : __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      x = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       int spins = 0;
       while (__ballot(x == EMPTY) != 0ull) {
         if (++spins > SPIN_LIMIT) {
           if (lane == 0) tmo = 1;
           break;
         }
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(1);
         x = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+      if (x == EMPTY) x = 0ull;
     }
     racc = first ? x : wave_merge_top64(racc, x);
     first = false;
   }
-  racc = merge_waves(racc, tops);
+  __syncthreads();  // own[] (a slot of the merge tree) read by its wave
+  racc = merge_waves<NW>(racc, slots);
   if (w == 0) {
     if (tmo) {
       if (lane == 0) {
@@ -622,45 +608,54 @@ __global__ __launch_bounds__(BS) void k64_kernel(SampleArgs a) {
       }
     } else {
       const int nr = __popcll(__ballot(racc != 0ull));
-      const int nk = nr < k ? nr : k;
-      wave_finish_row(a, r, lane < nk ? racc : 0ull, nk);
+      wave_finish_row(a, r, lane < k ? racc : 0ull, nr < k ? nr : k);
     }
   }
   // ready for the next call: lists empty, counter zero
-  for (int cc = w; cc < a.S; cc += NWB)
+  for (int cc = w; cc < a.S; cc += NW)
     if (cc != c) __hip_atomic_store(lists + (long long)cc * KM + lane, EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename Tin>
-hipError_t launch_t(const SampleArgs& a, size_t lds, hipStream_t st) {
-  const dim3 g(a.B * a.S), blk(K64_NT);
+template <typename Tin, int NTT>
+hipError_t launch_n(const SampleArgs& a, size_t lds, hipStream_t st) {
+  const dim3 g(a.B * a.S), blk(NTT);
   const bool vec = a.whole_vec != 0, mask = a.mask_table != nullptr && a.n_states > 0;
-  if (vec && mask) hipLaunchKernelGGL((k64_kernel<Tin, true, true>), g, blk, lds, st, a);
-  else if (vec) hipLaunchKernelGGL((k64_kernel<Tin, true, false>), g, blk, lds, st, a);
-  else if (mask) hipLaunchKernelGGL((k64_kernel<Tin, false, true>), g, blk, lds, st, a);
-  else hipLaunchKernelGGL((k64_kernel<Tin, false, false>), g, blk, lds, st, a);
+  if (vec && mask) hipLaunchKernelGGL((k64_kernel<Tin, NTT, true, true>), g, blk, lds, st, a);
+  else if (vec) hipLaunchKernelGGL((k64_kernel<Tin, NTT, true, false>), g, blk, lds, st, a);
+  else if (mask) hipLaunchKernelGGL((k64_kernel<Tin, NTT, false, true>), g, blk, lds, st, a);
+  else hipLaunchKernelGGL((k64_kernel<Tin, NTT, false, false>), g, blk, lds, st, a);
   return hipGetLastError();
 }
 
-}  // namespace k64
-
-hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
-  return dtype == 1 ? k64::launch_t<uint16_t>(a, lds, st) : k64::launch_t<float>(a, lds, st);
-}
-
-hipError_t set_k64_lds_limit(size_t bytes) {
+template <typename Tin, int NTT>
+hipError_t set_lds(size_t bytes) {
   const void* fns[] = {
-      (const void*)k64::k64_kernel<float, true, true>,     (const void*)k64::k64_kernel<float, true, false>,
-      (const void*)k64::k64_kernel<float, false, true>,    (const void*)k64::k64_kernel<float, false, false>,
-      (const void*)k64::k64_kernel<uint16_t, true, true>,  (const void*)k64::k64_kernel<uint16_t, true, false>,
-      (const void*)k64::k64_kernel<uint16_t, false, true>, (const void*)k64::k64_kernel<uint16_t, false, false>,
+      (const void*)k64_kernel<Tin, NTT, true, true>,
+      (const void*)k64_kernel<Tin, NTT, true, false>,
+      (const void*)k64_kernel<Tin, NTT, false, true>,
+      (const void*)k64_kernel<Tin, NTT, false, false>,
   };
   hipError_t e = hipSuccess;
   for (const void* f : fns) {
     hipError_t e2 = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e2 != hipSuccess) e = e2;
   }
+  return e;
+}
+
+}  // namespace k64
+
+int k64_chunk_ids(int dtype) { return K64_NT * K64_NVT * (dtype == 1 ? 8 : 4); }
+
+hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
+  return dtype == 1 ? k64::launch_n<uint16_t, K64_NT>(a, lds, st) : k64::launch_n<float, K64_NT>(a, lds, st);
+}
+
+hipError_t set_k64_lds_limit(size_t bytes) {
+  hipError_t e = hipSuccess, e2;
+  if ((e2 = k64::set_lds<float, K64_NT>(bytes)) != hipSuccess) e = e2;
+  if ((e2 = k64::set_lds<uint16_t, K64_NT>(bytes)) != hipSuccess) e = e2;
   return e;
 }
 

@@ -8,16 +8,16 @@
 
 namespace tgs {
 
-// Fused top_k <= 64 kernel: block size, tile (ids per chunk at most),
-// longest history it takes, exact-path candidate capacity, candidate buffer
-// entries (u64), bitmap words of a tile, and the stride (in unsigned words)
-// between the per-row arrival counters (one 128-byte line each).
+// Fused top_k <= 64 kernel: threads per workgroup, 16-byte vectors per
+// thread (a chunk is at most K64_NT x K64_NVT vectors), longest history it
+// takes, candidate buffer entries (u64; 16 more are reserved for ranking
+// pads), chunks per row at most, and the stride (in unsigned words) between
+// the per-row arrival counters (one 128-byte line each).
 constexpr int K64_NT = 256;
-constexpr int K64_TILE = 16384;
+constexpr int K64_NVT = 16;
 constexpr int K64_MAX_HIST = 1024;
-constexpr int K64_CAP = 1024;
-constexpr int K64_CAND_ENTRIES = 2176;  // per-wave candidate staging (bf16 size); the exact path reuses it
-constexpr int K64_BITMAP_WORDS = K64_TILE / 32;
+constexpr int K64_CAP = 2048;
+constexpr int K64_MAX_SPLIT = 16;
 constexpr int K64_CNT_STRIDE = 32;
 
 // Top-p kernel (rows without a top-k): threads per workgroup and the most
@@ -139,7 +139,9 @@ constexpr int SPEC_GROUPS = 4;  // 16-byte vector groups per block of 1024 ids (
 // order on st.
 hipError_t launch_sample(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
 hipError_t set_sample_lds_limit(size_t bytes);
-// The fused kernel for batches of greedy rows and rows with top_k <= 64.
+// The fused kernel for batches of greedy rows and rows with top_k <= 64:
+// K64_NT threads per workgroup, chunks of at most k64_chunk_ids(dtype) ids.
+int k64_chunk_ids(int dtype);
 hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
 hipError_t set_k64_lds_limit(size_t bytes);
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
