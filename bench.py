@@ -9,6 +9,8 @@ same generator set (tinygpt_amd/workloads.py):
 
   c1  B=1, V=256 byte-level sampling (latency-bound)
   c2  B=64, V=128256 fp32, full chain (headline)
+  c2m C2 plus the grammar mask stage (1024-state table of C3's statistics):
+      the north star's full penalty + mask + top-k/top-p + draw chain
   c3  B=128, V=32000 fp32, grammar mask table of 4096 states, greedy + top-p
   c4  B=1024, V=151936 bf16, per-row top-k/top-p/T/repetition
   c5  B=32 sequences, k=8 draft tokens, V=128256 speculative verification
@@ -19,12 +21,20 @@ same generator set (tinygpt_amd/workloads.py):
 
 Inputs are resident in HBM before timing; distinct input sets rotate so the
 256 MB Infinity Cache cannot serve repeats (at least 512 MB in rotation
-where a set is large).  The calls are captured in a HIP graph (one call per
-set) and replayed; the timed region is bracketed by synchronisations and HIP
-events on the launch stream.
+where a set is large).  The calls are captured in HIP graphs (one call per
+set; a second graph holds the remainder when --steps is not a multiple of
+the rotation) and replayed so that exactly --steps calls are timed; the
+timed region is bracketed by synchronisations and HIP events on the launch
+stream.  Then 256 eager calls, each between two HIP events, give the per-call
+p10 / p50 / p90.
 
-Prints one JSON line with the roofline of the call and the CPU oracle timed
-on this host over a bounded sample.
+Prints one JSON line with the roofline of the call, the CPU oracle timed on
+this host over a bounded sample, and the parity report of the sampled
+outputs against the oracle on the same inputs: id agreement, kept-set and
+top-p count agreement, the largest relative error of the reported
+probabilities against fp64 softmax of the canonical logits, and the draw /
+top-p boundary cases (u or p within 1e-6 of a CDF step) with the
+disagreements outside them.
 
 `--calibrate-copy MIB` instead runs a plain device-to-device copy of MIB MiB
 a few times: profiling it with the FETCH_SIZE / WRITE_SIZE counters gives the
@@ -51,7 +61,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "lp", "mask"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c2m", "c3", "c4", "c5", "lp", "mask"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
@@ -69,7 +79,24 @@ def oracle_mod():
 
 
 def cpu_threads():
-    return max(1, min(16, os.cpu_count() or 1))
+    """Threads of the CPU baseline: every core this process may run on, at
+    most 16 (a one-GPU box's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def timed_loop(fn, n_sets, seconds):
@@ -108,6 +135,20 @@ class Sampling:
             self.sets = [W.config2(B=self.B, V=self.V, H=self.H, seed_offset=i * 1000) for i in range(self.rot)]
             self.config = {"workload": "c2_llama3_bpe", "B": 64, "V": 128256, "history": 512, "top_k": 50,
                            "top_p": 0.9, "temperature": 0.7, "presence": 0.5, "frequency": 0.3}
+            self.dtype = "f32"
+        elif name == "c2m":
+            self.rot, self.B, self.V, self.H = 16, 64, 128256, 512
+            g = W.rng(20)
+            table = W.mask_table_loguniform(g, 1024, self.V)
+            self.sets = []
+            for i in range(self.rot):
+                s = W.config2(B=self.B, V=self.V, H=self.H, seed_offset=i * 1000)
+                s["mask_table"] = table
+                s["params"]["mask_state"] = g.integers(0, table.shape[0], size=self.B).astype(np.int32)
+                self.sets.append(s)
+            self.config = {"workload": "c2m_full_chain_masked", "B": 64, "V": 128256, "history": 512, "top_k": 50,
+                           "top_p": 0.9, "temperature": 0.7, "presence": 0.5, "frequency": 0.3,
+                           "mask_states": 1024, "mask_density": "log-uniform [0.1%, 30%]"}
             self.dtype = "f32"
         elif name == "c3":
             self.rot, self.B, self.V, self.H = 16, 128, 32000, 0
@@ -153,8 +194,7 @@ class Sampling:
                 out=torch.empty(self.B, dtype=torch.int32, device=dev),
             ))
         self.hints = [tg.batch_hint(s["params"], self.V) for s in self.sets]
-        self.alg_bytes = W.algorithmic_bytes_per_row(
-            "c3" if name == "c3" else name, self.V, self.H, dtype_bytes=2 if name == "c4" else 4) * self.B
+        self.alg_bytes = W.algorithmic_bytes_per_row(name, self.V, self.H, dtype_bytes=2 if name == "c4" else 4) * self.B
         self.units_per_step = self.B
         self.unit = "rows/s"
         self.metric = METRIC if name == "c2" else f"sampled rows/sec, workload {self.config['workload']}"
@@ -166,6 +206,77 @@ class Sampling:
 
     def gpu_outputs(self):
         return {i: self.d[i]["out"].cpu().numpy() for i in range(self.rot)}
+
+    def parity_report(self, pyoracle, nthreads, n_sets=4, max_rows=128):
+        """The first n_sets sets (at most max_rows rows each), sampled once more
+        with the diagnostic outputs, against the oracle on the same rows:
+        ids; the top-k / top-p sizes, masses and cut ids; the kept sets and
+        reported probabilities of rows that report a kept list (greedy rows
+        and rows with 1 <= top_k <= 1024); the largest relative error of
+        those probabilities against fp64 softmax of the oracle's canonical
+        logits over the top-p survivors; the boundary cases."""
+        import torch
+
+        import tinygpt_amd as tg
+
+        dev = "cuda:0"
+        kc = 64 if self.name in ("c1", "c2", "c2m") else 1024
+        R = min(self.B, max_rows)
+        rep = dict(rows=0, ids_equal=0, topk_topp_equal=0, kept_rows=0, kept_equal=0, prob_rows=0,
+                   probs_bit_equal_oracle=0, max_rel_prob_err_fp64=0.0, draw_boundary=0, topp_boundary=0,
+                   id_disagreements_outside_boundary=0)
+        for i in range(min(n_sets, self.rot)):
+            x, s = self.d[i], self.sets[i]
+            dbg = dict(kept_ids=torch.full((self.B, kc), -7, dtype=torch.int32, device=dev),
+                       kept_probs=torch.full((self.B, kc), -7.0, dtype=torch.float32, device=dev),
+                       counts=torch.full((self.B, 2), -7, dtype=torch.int32, device=dev),
+                       mass=torch.zeros((self.B, 2), dtype=torch.int64, device=dev),
+                       cut_ids=torch.full((self.B,), -7, dtype=torch.int32, device=dev))
+            out = torch.empty(self.B, dtype=torch.int32, device=dev)
+            self.sampler.sample(x["logits"], x["params"], x["u"], hist=x["hist"], hist_len=x["hist_len"], out=out,
+                                hint=self.hints[i], debug=dbg)
+            torch.cuda.synchronize()
+            gp = {k: v.cpu().numpy() for k, v in dbg.items()}
+            gp["mass"] = gp["mass"].view(np.uint64)
+            gid = out.cpu().numpy()
+            cut = lambda a: None if a is None else a[:R]
+            o = pyoracle.sample_batch(s["logits"][:R], s["params"][:R], s["u"][:R], hist=cut(s.get("hist")),
+                                      hist_len=cut(s.get("hist_len")), mask_table=s.get("mask_table"),
+                                      kept_cap=kc, want_post=True, nthreads=nthreads)
+            res = o["res"]
+            p = s["params"][:R]
+            greedy = ((p["flags"] & 1) != 0) | (p["temperature"] <= 0)
+            listed = greedy | ((p["top_k"] >= 1) & (p["top_k"] <= 1024) & (p["top_k"] < self.V))
+            for b in range(R):
+                rep["rows"] += 1
+                same = gid[b] == o["ids"][b]
+                rep["ids_equal"] += int(same)
+                bnd = bool(res["draw_boundary"][b] or res["topp_boundary"][b])
+                rep["draw_boundary"] += int(res["draw_boundary"][b])
+                rep["topp_boundary"] += int(res["topp_boundary"][b])
+                rep["id_disagreements_outside_boundary"] += int(not same and not bnd)
+                rep["topk_topp_equal"] += int(gp["counts"][b, 0] == res["n_topk"][b] and gp["counts"][b, 1] == res["n_topp"][b]
+                                              and gp["mass"][b, 0] == res["mass_k"][b]
+                                              and gp["mass"][b, 1] == res["mass_p"][b]
+                                              and gp["cut_ids"][b] == res["cut_id"][b])
+                if not listed[b] or o["ids"][b] < 0:
+                    continue
+                n = min(kc, int(res["n_topk"][b]))
+                rep["kept_rows"] += 1
+                rep["kept_equal"] += int(np.array_equal(gp["kept_ids"][b, :n], o["kept_ids"][b, :n]))
+                m = min(kc, int(res["n_topp"][b]))
+                if greedy[b] or m < 1:
+                    continue
+                rep["prob_rows"] += 1
+                rep["probs_bit_equal_oracle"] += int(np.array_equal(gp["kept_probs"][b, :m], o["kept_probs"][b, :m]))
+                y = o["post"][b][o["kept_ids"][b, :m]].astype(np.float64)
+                e = np.exp(y - y.max())
+                pr = e / e.sum()
+                err = float(np.max(np.abs(gp["kept_probs"][b, :m].astype(np.float64) - pr) / pr))
+                rep["max_rel_prob_err_fp64"] = max(rep["max_rel_prob_err_fp64"], err)
+        rep["sets"] = min(n_sets, self.rot)
+        rep["rows_per_set"] = R
+        return rep
 
     def cpu_call(self, pyoracle, nthreads):
         def fn(i):
@@ -214,6 +325,35 @@ class SpecVerify:
 
     def tokens_per_step(self):
         return float(np.mean([(self.d[i]["n_acc"].cpu().numpy() + 1).sum() for i in range(self.rot)]))
+
+    def parity_report(self, pyoracle, nthreads):
+        """Accept / reject decisions and emitted tokens of every set against
+        the oracle, with the boundary cases (an accept ratio or a draw
+        within 1e-6 of its threshold)."""
+        rep = dict(sequences=0, n_acc_equal=0, tokens_equal=0, accept_boundary=0, draw_boundary=0,
+                   disagreements_outside_boundary=0)
+        for i in range(self.rot):
+            s = self.sets[i]
+            self.launch(i, self.torch_stream())
+            g = self.gpu_outputs()[i]
+            o = pyoracle.spec_verify_batch(s["target"], s["draft"], s["dtok"], s["T"], s["u_acc"], s["u_res"],
+                                           nthreads=nthreads)
+            for b in range(self.B):
+                rep["sequences"] += 1
+                na = g[b, 0] == o["n_acc"][b]
+                tok = np.array_equal(g[b, 1:], o["out"][b])
+                rep["n_acc_equal"] += int(na)
+                rep["tokens_equal"] += int(tok)
+                ab, db = int(o["info"]["accept_boundary"][b]), int(o["info"]["draw_boundary"][b])
+                rep["accept_boundary"] += ab
+                rep["draw_boundary"] += db
+                rep["disagreements_outside_boundary"] += int(not (na and tok) and not (ab or db))
+        return rep
+
+    def torch_stream(self):
+        import torch
+
+        return torch.cuda.current_stream().cuda_stream
 
     def cpu_call(self, pyoracle, nthreads):
         def fn(i):
@@ -368,11 +508,13 @@ def cpu_baseline(wl, seconds):
         rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), 1, seconds)
         outs = {wl.rot - 1: outs[0]}
         return dict(value=round(rate, 2), unit=wl.unit, cores=1, kind="port",
+                    host_cpu_count=os.cpu_count(), host_cpu_model=cpu_model(),
                     sample=f"{units} rows (4 states of the last set, V={wl.V}, numpy vectorised byte replay) "
                            f"on 1 thread"), outs
     if isinstance(wl, TokenLogprobs):  # numpy, one thread
         rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), wl.rot, seconds)
         return dict(value=round(rate, 2), unit=wl.unit, cores=1, kind="port",
+                    host_cpu_count=os.cpu_count(), host_cpu_model=cpu_model(),
                     sample=f"{units} positions of lp_scoring (the first {wl.SAMPLE} rows of each of {wl.rot} "
                            f"seeded sets, float64 numpy log-softmax) on 1 thread"), outs
     return dict(
@@ -380,6 +522,8 @@ def cpu_baseline(wl, seconds):
         sample=f"{units_n} rows of {wl.config['workload']} (batches of {wl.B} cycling over {wl.rot} seeded sets) "
                f"on {nthr} threads; 1 thread: {round(rate_1, 2)} {wl.unit} over {units_1} rows",
         single_thread_value=round(rate_1, 2),
+        host_cpu_count=os.cpu_count(), host_cpu_model=cpu_model(),
+        threads_note="every core this process may run on, at most 16 (a one-GPU box's share of the host)",
     ), outs
 
 
@@ -405,7 +549,8 @@ TRAFFIC_FILES = {"c2": "k64_kernel_c2_traffic.json", "c3": "c3_grammar_traffic.j
                  "c4": "c4_large_batch_traffic.json", "c5": "c5_spec_verify_traffic.json"}
 TRAFFIC_FILES["lp"] = "lp_scoring_traffic.json"
 TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
-KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c3": "topp_kernel<float, true>",
+KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c2m": "k64_kernel<float> (mask variant)",
+           "c3": "topp_kernel<float, true>",
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
            "lp": "lp::chunk_kernel<float>", "mask": "maskb::prep_image + maskb::build_lds (one call)"}
@@ -444,27 +589,36 @@ def main():
             wl.launch(i, stream.cuda_stream)
     torch.cuda.synchronize()
 
-    graph = None
-    if not args.eager:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream, capture_error_mode="thread_local"):
-            for i in range(ROT):
+    steps = max(1, args.steps)
+    reps, rem = divmod(steps, ROT)
+
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+            for i in range(n):
                 wl.launch(i, stream.cuda_stream)
         torch.cuda.synchronize()
-        for _ in range(3):
-            graph.replay()
+        return g
+
+    graph = graph_rem = None
+    if not args.eager:
+        graph = capture(ROT) if reps else None
+        graph_rem = capture(rem) if rem else None
+        for g in (graph, graph_rem):
+            if g is not None:
+                g.replay()
         torch.cuda.synchronize()
 
-    reps = max(1, (args.steps + ROT - 1) // ROT)
-    steps = reps * ROT if graph is not None else args.steps
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         ev0.record(stream)
-        if graph is not None:
+        if not args.eager:
             for _ in range(reps):
                 graph.replay()
+            if graph_rem is not None:
+                graph_rem.replay()
         else:
             for i in range(steps):
                 wl.launch(i, stream.cuda_stream)
@@ -473,10 +627,27 @@ def main():
     ms_total = ev0.elapsed_time(ev1)
     ms_per_step = ms_total / steps
 
+    # per-call distribution: eager calls, each between two events
+    n_calls = 256
+    e_start = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
+    e_end = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
+    with torch.cuda.stream(stream):
+        for i in range(n_calls):
+            e_start[i].record(stream)
+            wl.launch(i, stream.cuda_stream)
+            e_end[i].record(stream)
+    torch.cuda.synchronize()
+    per_call = np.array([a.elapsed_time(b) * 1e3 for a, b in zip(e_start, e_end)])
+    per_call_us = {"p10": round(float(np.percentile(per_call, 10)), 2),
+                   "p50": round(float(np.percentile(per_call, 50)), 2),
+                   "p90": round(float(np.percentile(per_call, 90)), 2), "calls": n_calls,
+                   "mode": "eager launches, HIP events around each call on the launch stream"}
+
     # parity of the timed outputs against the oracle (same inputs)
     gpu_out = wl.gpu_outputs()
     cpu = None
     agreement = None
+    parity = None
     if not args.no_cpu:
         cpu, cpu_out = cpu_baseline(wl, args.cpu_seconds)
         if isinstance(wl, TokenLogprobs):
@@ -485,6 +656,8 @@ def main():
             agreement = float(np.mean([np.mean(gpu_out[i] == cpu_out[i]) for i in cpu_out]))
         if agreement != 1.0:
             print("WARNING: GPU outputs differ from the oracle", file=sys.stderr)
+        if hasattr(wl, "parity_report"):
+            parity = wl.parity_report(oracle_mod(), cpu_threads())
 
     achieved = wl.alg_bytes / (ms_per_step * 1e-3) / 1e9
     units_per_s = wl.units_per_step / (ms_per_step * 1e-3)
@@ -517,6 +690,8 @@ def main():
                      "alg_bytes_per_launch": wl.alg_bytes, "kernel": KERNELS[args.workload]},
         "cpu_baseline": cpu,
         "id_agreement": agreement,
+        "parity": parity,
+        "per_call_us": per_call_us,
     }
     if isinstance(wl, SpecVerify):
         line["tokens_per_s"] = round(wl.tokens_per_step() / (ms_per_step * 1e-3), 1)

@@ -88,6 +88,8 @@ def lib() -> C.CDLL:
         L.tgo_expf.argtypes = [C.c_float]
         L.tgo_weight.restype = C.c_float
         L.tgo_weight.argtypes = [C.c_float, C.c_float]
+        L.tgo_weight_wide.restype = C.c_float
+        L.tgo_weight_wide.argtypes = [C.c_float, C.c_float]
         L.tgo_q40.restype = C.c_uint64
         L.tgo_q40.argtypes = [C.c_float]
         L.tgo_u64_to_f32.restype = C.c_float
@@ -201,6 +203,12 @@ def spec_verify_batch(target, draft, dtok, T, u_acc, u_res, nthreads=1):
 def expf(x):
     f = lib().tgo_expf
     return np.array([f(float(v)) for v in np.asarray(x, dtype=np.float32).ravel()], dtype=np.float32)
+
+
+def weight_wide(x):
+    """tgo_weight_wide(x, 0) over an array of x <= 0."""
+    f = lib().tgo_weight_wide
+    return np.array([f(float(v), 0.0) for v in np.asarray(x, dtype=np.float32).ravel()], dtype=np.float32)
 
 
 def spec_row_stats(y):

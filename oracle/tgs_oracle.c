@@ -87,6 +87,39 @@ float tgo_weight(float y, float m) { return (y == m) ? 1.0f : tgo_expf(y - m); }
 
 uint64_t tgo_q40(float e) { return (uint64_t)(e * 0x1p40f); }
 
+/* Weight for reported probabilities only: tgo_weight's formula continued
+ * below -32 down to y - m = -86 (2^n, n >= -124, a normal scale) instead of
+ * 0; equal to tgo_weight wherever y - m >= -32. */
+float tgo_weight_wide(float y, float m) {
+  if (y == m) return 1.0f;
+  const float x = y - m;
+  if (!(x >= -86.0f)) return 0.0f;
+  const float log2e = 0x1.715476p+0f;
+  const float ln2_hi = 0x1.62ep-1f;
+  const float ln2_lo = 0x1.0bfbe8p-15f;
+  const float shifter = 12582912.0f;
+  float t = x * log2e;
+  float n = (t + shifter) - shifter;
+  float r = fmaf(n, -ln2_hi, x);
+  r = fmaf(n, -ln2_lo, r);
+  float p = 0x1.a01a02p-13f;
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+/* Reported probability of a kept id: its wide weight over the top-p mass S'
+ * (2^-40 units).  S' differs from the exact sum of the weights by at most
+ * one unit per kept id (plus the weights below 2^-40 it leaves out) and is
+ * at least 2^40, so the ratio carries only the float roundings of the
+ * weight, of f32(S') and of the quotient. */
+float tgo_kept_prob(float y, float m, float fs) { return (tgo_weight_wide(y, m) * 0x1p40f) / fs; }
+
 float tgo_u64_to_f32(uint64_t x) {
   if (x < (1ull << 24)) return (float)(uint32_t)x;
   int lz = __builtin_clzll(x);
@@ -321,13 +354,10 @@ static int sample_row_impl(const float* x, int V, const int32_t* hist, int H, co
   res.mass_p = Sp;
   if (kept_ids)
     for (long i = 0; i < kk && i < kept_cap; i++) kept_ids[i] = comp_id(s->keys[i]);
-  if (kept_probs) {
+  if (kept_probs) { /* float weights over the top-p mass (not the floored integer masses) */
     float fs = tgo_u64_to_f32(Sp);
-    uint64_t prev = 0;
-    for (long i = 0; i <= istar && i < kept_cap; i++) {
-      kept_probs[i] = tgo_u64_to_f32(s->cdf[i] - prev) / fs;
-      prev = s->cdf[i];
-    }
+    for (long i = 0; i <= istar && i < kept_cap; i++)
+      kept_probs[i] = tgo_kept_prob(comp_y(s->keys[i]), m, fs);
   }
   *r = res;
   return 0;

@@ -62,6 +62,8 @@ typedef struct {
 /* ---- canonical numerics (exposed so tests can pin them) ---------------- */
 float tgo_expf(float x);            /* e^x for x in [-32, 88]; 0 below -32   */
 float tgo_weight(float y, float m); /* y == m ? 1 : tgo_expf(y - m)          */
+float tgo_weight_wide(float y, float m);           /* as tgo_weight, down to y - m = -86 (reported probabilities) */
+float tgo_kept_prob(float y, float m, float fs);   /* reported probability: wide weight 2^40 / fs */
 uint64_t tgo_q40(float e);          /* floor(e * 2^40), e in [0, 1]          */
 float tgo_u64_to_f32(uint64_t x);   /* round-to-nearest-even conversion      */
 uint32_t tgo_key(float f);          /* order-preserving key, -0 -> +0        */

@@ -31,6 +31,27 @@ def test_expf_accuracy(oracle):
     assert err.max() <= 1.0, err.max()
 
 
+def test_weight_wide_accuracy(oracle):
+    """The reported-probability weight: within one ulp of fp64 exp down to
+    -86 (normal results only), equal to the mass weight where both are
+    defined, 0 below -86."""
+    g = np.random.default_rng(3)
+    x = np.concatenate([np.linspace(-86, 0, 100001, dtype=np.float32),
+                        (-g.random(50000) * 86).astype(np.float32),
+                        np.float32([-85.99999, -86.0, -32.0, -32.000004, -0.0])])
+    e = oracle.weight_wide(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert (np.abs(e - ref) / ulp).max() <= 1.0
+    assert np.all(e >= np.finfo(np.float32).tiny)  # normal results
+    xs = x[x >= -32]
+    np.testing.assert_array_equal(oracle.weight_wide(xs), oracle.expf(xs))
+    L = oracle.lib()
+    assert L.tgo_weight_wide(-86.5, 0.0) == 0.0
+    assert L.tgo_weight_wide(float("-inf"), 0.0) == 0.0
+    assert L.tgo_weight_wide(2.0, 2.0) == 1.0
+
+
 def test_expf_special_values(oracle):
     L = oracle.lib()
     assert L.tgo_expf(0.0) == 1.0

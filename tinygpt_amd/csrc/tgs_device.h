@@ -139,6 +139,35 @@ __device__ __forceinline__ float tg_weight(float y, float m) {
 
 __device__ __forceinline__ u64 tg_q40(float e) { return (u64)(e * 0x1p40f); }
 
+// Weight of a kept id for its reported probability only (masses and draws
+// never use it): tg_weight's formula continued below -32 down to
+// y - m = -86 instead of returning 0 there (2^n with n >= -124 is still a
+// normal scale and p 2^n a normal result), so that ids far below the
+// maximum keep their relative accuracy.  Equal to tg_weight wherever
+// y - m >= -32.
+__device__ __forceinline__ float tg_weight_wide(float y, float m) {
+  if (y == m) return 1.0f;
+  const float x = y - m;
+  if (!(x >= -86.0f)) return 0.0f;
+  const float log2e = 0x1.715476p+0f;
+  const float ln2_hi = 0x1.62ep-1f;
+  const float ln2_lo = 0x1.0bfbe8p-15f;
+  const float shifter = 12582912.0f;
+  float t = x * log2e;
+  float n = (t + shifter) - shifter;
+  float r = __builtin_fmaf(n, -ln2_hi, x);
+  r = __builtin_fmaf(n, -ln2_lo, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
 __device__ __forceinline__ float tg_u64_to_f32(u64 x) {
   if (x < (1ull << 24)) return (float)(uint32_t)x;
   int lz = __clzll((long long)x);

@@ -105,7 +105,7 @@ __device__ __forceinline__ void finalize_topk(const SampleArgs& a, const Row& r,
     const float fs = tg_u64_to_f32(Sp);
     for (int i = threadIdx.x; i < a.dbg.kept_cap; i += NT) {
       float pv = 0.0f;
-      if (i <= istar) pv = tg_u64_to_f32(C[i] - (i ? C[i - 1] : 0ull)) / fs;
+      if (i <= istar) pv = kept_prob(comp_y(cand[i]), m, fs);
       kp[i] = pv;
     }
   }

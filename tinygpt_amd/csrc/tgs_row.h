@@ -223,6 +223,15 @@ __device__ __forceinline__ void write_row_diag(const SampleArgs& a, int b, int n
   if (a.dbg.cut_ids) a.dbg.cut_ids[b] = cut;
 }
 
+// Reported probability of a kept id: its float weight (tg_weight_wide) over
+// the top-p mass (fs = f32(S'), 2^-40 units).  S' differs from the exact sum
+// of the weights by at most one unit per kept id (plus the weights below
+// 2^-40 it leaves out) and is at least 2^40, so the ratio carries only float
+// roundings, not the floor of the integer masses.
+__device__ __forceinline__ float kept_prob(float y, float m, float fs) {
+  return (tg_weight_wide(y, m) * 0x1p40f) / fs;
+}
+
 // Called by one whole wave: x is this lane's entry of the kept list sorted
 // by (logit desc, id asc) (lane i = rank i), n in [1, 64] valid entries.
 __device__ __forceinline__ void wave_finalize(const SampleArgs& a, const Row& r, u64 x, int n) {
@@ -258,7 +267,7 @@ __device__ __forceinline__ void wave_finalize(const SampleArgs& a, const Row& r,
   if (a.dbg.kept_probs) {
     float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
     const float fs = tg_u64_to_f32(Sp);
-    for (int i = lane; i < a.dbg.kept_cap; i += 64) kp[i] = (i <= istar) ? tg_u64_to_f32(q) / fs : 0.0f;
+    for (int i = lane; i < a.dbg.kept_cap; i += 64) kp[i] = (i <= istar) ? kept_prob(y, m, fs) : 0.0f;
   }
 }
 

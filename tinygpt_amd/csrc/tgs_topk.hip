@@ -518,7 +518,7 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
       float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
       const float fs = tg_u64_to_f32(Sp);
       for (int i = threadIdx.x; i < a.dbg.kept_cap; i += BT)
-        kp[i] = i <= (int)istar ? tg_u64_to_f32(bucket::mass_c(cand[i], m)) / fs : 0.0f;
+        kp[i] = i <= (int)istar ? kept_prob(comp_y(cand[i]), m, fs) : 0.0f;
     }
   }
 }

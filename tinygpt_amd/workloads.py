@@ -74,16 +74,36 @@ def config2(B: int = 64, V: int = 128256, H: int = 512, seed_offset: int = 0):
                 hist_len=np.full(B, H, np.int32), u=u, mask_table=None, V=V)
 
 
-def config3(B: int = 128, V: int = 32000, n_states: int = 4096, seed_offset: int = 0):
-    g = rng(3 + seed_offset)
-    logits = normal_f32(g, (B, V), 2.5)
+def mask_table_loguniform(g: np.random.Generator, n_states: int, V: int, lo: float = 0.001, hi: float = 0.30):
+    """Per-state vocab bitmasks (V/32 words) whose allowed-token density is
+    log-uniform in [lo, hi], at least one token per state."""
     words = (V + 31) // 32
     table = np.zeros((n_states, words), dtype=np.uint32)
-    dens = np.exp(g.uniform(np.log(0.001), np.log(0.30), size=n_states))
+    dens = np.exp(g.uniform(np.log(lo), np.log(hi), size=n_states))
     for s in range(n_states):
         n = max(1, int(round(dens[s] * V)))
         ids = g.choice(V, size=n, replace=False)
         np.bitwise_or.at(table[s], ids >> 5, (np.uint32(1) << (ids & 31).astype(np.uint32)))
+    return table
+
+
+def config2_masked(B: int = 64, V: int = 128256, H: int = 512, n_states: int = 1024, seed_offset: int = 0):
+    """C2 with the grammar mask stage: the north star's full chain (penalties,
+    mask, temperature, top-k 50, top-p 0.9, draw).  The mask table follows
+    C3's automaton statistics (density log-uniform in [0.1%, 30%], at least
+    one token per state) at V = 128256; each row draws a uniform state."""
+    c = config2(B=B, V=V, H=H, seed_offset=seed_offset)
+    g = rng(20 + seed_offset)
+    c["mask_table"] = mask_table_loguniform(g, n_states, V)
+    c["params"]["mask_state"] = g.integers(0, n_states, size=B).astype(np.int32)
+    c["name"] = "c2m_full_chain_masked"
+    return c
+
+
+def config3(B: int = 128, V: int = 32000, n_states: int = 4096, seed_offset: int = 0):
+    g = rng(3 + seed_offset)
+    logits = normal_f32(g, (B, V), 2.5)
+    table = mask_table_loguniform(g, n_states, V)
     states = g.integers(0, n_states, size=B).astype(np.int32)
     half = B // 2
     params = make_params(B, temperature=1.0, top_k=0, top_p=0.95, mask_state=states)
@@ -151,4 +171,6 @@ def algorithmic_bytes_per_row(name: str, V: int, H: int = 0, k: int = 8, dtype_b
         return 4 * V + V // 8
     if name.startswith("c5"):
         return (2 * k + 1) * V * dtype_bytes
+    if name.startswith("c2m"):  # logits, history ids, the row's mask bits
+        return dtype_bytes * V + 4 * H + V // 8
     return dtype_bytes * V + 4 * H
