@@ -134,7 +134,9 @@ const char* tgs_last_error(tgs_handle h);
 /* Grammar mask table: n_states rows of ceil(vocab/32) uint32 words; bit v
  * of row s (word v>>5, bit v&31) is 1 <=> token v is allowed in state s.
  * _set replaces the table (synchronous upload); _update overwrites n rows
- * (states[i] < current n_states). */
+ * (states[i] < current n_states, all checked before anything is written;
+ * the last of repeated states wins): one upload of every row, then (states
+ * not consecutive) one scatter launch; synchronous. */
 int tgs_mask_table_set(tgs_handle h, const uint32_t* host_words, int n_states, int vocab);
 int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32_t* host_words,
                           int n);

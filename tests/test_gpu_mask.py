@@ -109,3 +109,56 @@ def test_mask_build_rejects_bad_arguments(sampler):
     assert call(n_tokens=100) != 0  # more tokens than the table's vocabulary
     assert call(n=0) == 0
     torch.cuda.synchronize()
+
+
+def _read_rows(sampler, rows, V):
+    import torch
+
+    import tinygpt_amd as tg
+
+    dev = "cuda:0"
+    params = tg.make_params(len(rows), temperature=0.0, mask_state=list(rows))
+    post = torch.empty(len(rows), V, dtype=torch.float32, device=dev)
+    sampler.sample(torch.zeros(len(rows), V, device=dev), tg.params_to_device(params, dev),
+                   torch.zeros(len(rows), device=dev), vocab=V, debug={"post_logits": post})
+    torch.cuda.synchronize()
+    bits = (post == 0).cpu().numpy()
+    return np.packbits(bits, axis=1, bitorder="little").view(np.uint8)
+
+
+def test_mask_table_update_batches(sampler):
+    """tgs_mask_table_update: a consecutive run (one copy), scattered states
+    with a repeat (one upload, one scatter launch: the last repeat wins),
+    rows left alone keep their bits, and a bad state changes nothing."""
+    V, n = 1000, 64
+    words = (V + 31) // 32
+    g = np.random.default_rng(77)
+    table = g.integers(0, 2**32, size=(n, words), dtype=np.uint64).astype(np.uint32)
+    table[:, -1] &= np.uint32((1 << (V % 32)) - 1)
+    sampler.set_mask_table(table, V)
+    expect = table.copy()
+
+    def check(what):
+        got = _read_rows(sampler, range(n), V)
+        want = np.unpackbits(expect.view(np.uint8), axis=1, bitorder="little")[:, :V]
+        want = np.packbits(want, axis=1, bitorder="little")
+        np.testing.assert_array_equal(got, want, err_msg=what)
+
+    new = g.integers(0, 2**32, size=(5, words), dtype=np.uint64).astype(np.uint32)
+    new[:, -1] &= np.uint32((1 << (V % 32)) - 1)
+    H.log("mask update: consecutive run 10..14")
+    sampler.update_mask_rows(np.arange(10, 15), new)
+    expect[10:15] = new
+    check("consecutive run")
+    states = np.array([3, 40, 7, 40, 63], np.int32)
+    new = g.integers(0, 2**32, size=(5, words), dtype=np.uint64).astype(np.uint32)
+    new[:, -1] &= np.uint32((1 << (V % 32)) - 1)
+    H.log("mask update: scattered states with a repeat")
+    sampler.update_mask_rows(states, new)
+    for i, s in enumerate(states):
+        expect[s] = new[i]
+    check("scattered")
+    H.log("mask update: a state out of range")
+    with pytest.raises(Exception):
+        sampler.update_mask_rows(np.array([1, n], np.int32), new[:2])
+    check("rejected update")

@@ -16,6 +16,8 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "tgs_device.h"
 #include "tgs_kernels.h"
@@ -32,6 +34,8 @@ struct tgs_ctx {
   unsigned long long* k64_lists = nullptr;  // fused kernel chunk lists, [max_batch * kMaxSplit][64]
   uint32_t* mask_table = nullptr;
   int n_states = 0, mask_vocab = 0, mask_words = 0;
+  void* mask_stage = nullptr;  // tgs_mask_table_update staging (grown on demand)
+  size_t mask_stage_bytes = 0;
   float* spec_blk_m = nullptr;             // speculative workspace (tgs_reserve_spec)
   unsigned long long* spec_blk_q = nullptr;
   unsigned long long* spec_blk_w = nullptr;
@@ -440,6 +444,7 @@ void tgs_destroy(tgs_handle h) {
   if (h->k64_cnt) (void)hipFree(h->k64_cnt);
   if (h->k64_lists) (void)hipFree(h->k64_lists);
   if (h->mask_table) (void)hipFree(h->mask_table);
+  if (h->mask_stage) (void)hipFree(h->mask_stage);
   free_spec(h);
   delete h;
 }
@@ -479,15 +484,57 @@ int tgs_mask_table_set(tgs_handle h, const uint32_t* host_words, int n_states, i
 int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32_t* host_words, int n) {
   if (!h) return TGS_EINVAL;
   if (n < 0 || (n > 0 && (!host_states || !host_words))) return fail(h, TGS_EINVAL, "mask update: bad arguments");
-  DeviceGuard g(h->device);
-  for (int i = 0; i < n; i++) {
+  for (int i = 0; i < n; i++)
     if (host_states[i] < 0 || host_states[i] >= h->n_states) return fail(h, TGS_EINVAL, "mask update: state out of range");
-    hipError_t e = hipMemcpy(h->mask_table + (size_t)host_states[i] * h->mask_words,
-                             host_words + (size_t)i * h->mask_words, sizeof(uint32_t) * h->mask_words,
+  if (n == 0) return TGS_OK;
+  DeviceGuard g(h->device);
+  const size_t row_bytes = sizeof(uint32_t) * (size_t)h->mask_words;
+  // consecutive states: one copy straight into the table
+  bool run = true;
+  for (int i = 1; i < n && run; i++) run = host_states[i] == host_states[0] + i;
+  if (run) {
+    hipError_t e = hipMemcpy(h->mask_table + (size_t)host_states[0] * h->mask_words, host_words, row_bytes * n,
                              hipMemcpyHostToDevice);
-    if (e != hipSuccess) return hip_fail(h, e, "mask update upload");
+    return e == hipSuccess ? TGS_OK : hip_fail(h, e, "mask update upload");
   }
-  return TGS_OK;
+  // otherwise one upload of the rows (the last of repeated states wins) and
+  // their destinations, then one scatter launch
+  std::vector<int> last(n);
+  {
+    std::unordered_map<int, int> pos;
+    for (int i = 0; i < n; i++) pos[host_states[i]] = i;
+    int m = 0;
+    for (int i = 0; i < n; i++)
+      if (pos[host_states[i]] == i) last[m++] = i;
+    last.resize(m);
+  }
+  const int m = (int)last.size();
+  const size_t head = ((sizeof(int) * 2 * (size_t)m) + 255) / 256 * 256;
+  const size_t need = head + row_bytes * n;
+  if (need > h->mask_stage_bytes) {
+    if (h->mask_stage) {
+      (void)hipDeviceSynchronize();
+      (void)hipFree(h->mask_stage);
+      h->mask_stage = nullptr;
+      h->mask_stage_bytes = 0;
+    }
+    if (hipMalloc(&h->mask_stage, need) != hipSuccess) return fail(h, TGS_ENOMEM, "mask update staging");
+    h->mask_stage_bytes = need;
+  }
+  std::vector<char> up(need);
+  int* packed = (int*)up.data();
+  for (int r = 0; r < m; r++) {
+    packed[r] = host_states[last[r]];
+    packed[m + r] = last[r];
+  }
+  std::memcpy(up.data() + head, host_words, row_bytes * n);
+  char* stage = (char*)h->mask_stage;
+  hipError_t e = hipMemcpy(stage, up.data(), need, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(h, e, "mask update upload");
+  e = tgs::launch_mask_scatter((const int*)stage, (const uint32_t*)(stage + head), m, h->mask_words, h->mask_table,
+                               nullptr);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  return e == hipSuccess ? TGS_OK : hip_fail(h, e, "mask update scatter");
 }
 
 int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, int64_t row_stride,

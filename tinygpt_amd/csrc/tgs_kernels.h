@@ -86,6 +86,10 @@ struct MaskBuildArgs {
   int n_rows, words;         // its rows and words per row
 };
 hipError_t launch_mask_build(const MaskBuildArgs& a, hipStream_t st);
+// Rows packed[i] of table (rows of `words` words) from rows packed[n + i] of
+// src, i < n (distinct destinations).
+hipError_t launch_mask_scatter(const int* packed, const uint32_t* src, int n, int words, uint32_t* table,
+                               hipStream_t st);
 // The 16-bit table with the dead state, reject and stay columns, and the LDS
 // image (512 bytes of class offsets, then the table, in whole 16 bytes).
 __host__ __device__ inline size_t mask_lds_table_bytes(int n_dfa, int n_cls) {

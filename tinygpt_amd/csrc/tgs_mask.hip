@@ -280,7 +280,26 @@ __global__ __launch_bounds__(MT) void build_global(MaskBuildArgs a) {
   }
 }
 
+// Mask-table rows from a staging upload: packed [n dst rows][n src rows]
+// ints, then the source rows' words; workgroup (x, y) copies one stretch
+// of MT words of rows y, y + gridDim.y, ...
+__global__ __launch_bounds__(MT) void scatter_rows(const int* packed, const uint32_t* src, int n, int words,
+                                                   uint32_t* table) {
+  const int w = blockIdx.x * MT + (int)threadIdx.x;
+  if (w >= words) return;
+  for (int r = blockIdx.y; r < n; r += gridDim.y)
+    table[(size_t)packed[r] * words + w] = src[(size_t)packed[n + r] * words + w];
+}
+
 }  // namespace maskb
+
+hipError_t launch_mask_scatter(const int* packed, const uint32_t* src, int n, int words, uint32_t* table,
+                               hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const dim3 g((words + maskb::MT - 1) / maskb::MT, n < 65535 ? n : 65535);
+  hipLaunchKernelGGL(maskb::scatter_rows, g, dim3(maskb::MT), 0, st, packed, src, n, words, table);
+  return hipGetLastError();
+}
 
 hipError_t launch_mask_build(const MaskBuildArgs& a, hipStream_t st) {
   if (a.lds) {
