@@ -250,6 +250,29 @@ def test_mask_rows_from_dfa(sim, oracle):
         np.testing.assert_array_equal(post[i] == 0.0, allowed)
 
 
+
+def test_mask_rows_many_tool_tag_states(sim, oracle):
+    """80 states of the tool-tag DFA (five workgroup rows of the LDS kernel,
+    MASK_SPW_LDS = 16 states each, two of the global kernel, MASK_SPW = 64)
+    through the class table in LDS and the 256-column table in global
+    memory (the GPU test takes all 434)."""
+    from tinygpt_amd import grammar as G
+
+    g = np.random.default_rng(81)
+    d = G.compile_gbnf(G.PACE_TOOL_TAGS)
+    pieces = [b"[", b"]", b"POINT", b":", b"none", b",", b"CLICK", b"TYPE", b"up", b" ", b"-", b"12", b"x", b"A"]
+    toks = [b""] + [b"".join(g.choice(pieces) for _ in range(g.integers(1, 4))) for _ in range(40)]
+    V = len(toks)
+    off, data = G.token_csr(toks)
+    states = np.arange(80, dtype=np.int32)
+    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states, eos=5)
+    bits = np.unpackbits(want.view(np.uint8), axis=1, bitorder="little")[:, :V].astype(bool)
+    bc, ct = d.byte_classes()
+    for byte_class, trans in ((bc, ct), (np.arange(256, dtype=np.uint8), d.trans)):
+        post = sim.run_maskbuild(byte_class, trans, d.complete.astype(np.uint8), off, data, states, states,
+                                 n_rows=len(states), eos=5)
+        np.testing.assert_array_equal(post == 0.0, bits)
+
 def _spec_case(seed, B, k, V, T, bf16=False):
     from tinygpt_amd import workloads as W
 

@@ -72,6 +72,38 @@ def test_tool_tag_rows_built_on_device(sampler, oracle):
     H.log("case mask build: ok")
 
 
+
+def test_every_tool_tag_state_both_tables(sampler, oracle):
+    """Rows for all states of the tool-tag DFA (many workgroup rows of both
+    kernels) through the class table in LDS and the 256-column table read
+    from global memory, bit-exact against the DFA replay oracle."""
+    import torch
+
+    from tinygpt_amd import grammar as G
+
+    g = np.random.default_rng(22)
+    V = 6000
+    d = G.compile_gbnf(G.PACE_TOOL_TAGS)
+    toks = _vocab(g, V)
+    off, data = G.token_csr(toks)
+    n = d.n
+    states = np.arange(n, dtype=np.int32)
+    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states, eos=7)
+    bits = np.packbits(np.unpackbits(want.view(np.uint8), axis=1, bitorder="little")[:, :V], axis=1,
+                       bitorder="little")
+    dev = "cuda:0"
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    bc, ct = d.byte_classes()
+    comp = T(d.complete.astype(np.uint8))
+    for name, byte_class, trans in (("lds", bc, ct), ("global", np.arange(256, dtype=np.uint8), d.trans)):
+        H.log(f"case mask build all states: {name} table, {n} states, V={V}")
+        sampler.set_mask_table(np.zeros((n, (V + 31) // 32), np.uint32), V)
+        sampler.mask_rows_from_dfa(T(byte_class), T(trans), comp, T(off), T(data), T(states), T(states), eos=7)
+        for r0 in range(0, n, 512):
+            rows = list(range(r0, min(n, r0 + 512)))
+            np.testing.assert_array_equal(_read_rows(sampler, rows, V), bits[r0:r0 + len(rows)],
+                                          err_msg=f"{name} rows {r0}..")
+
 @pytest.mark.gpu
 def test_mask_build_rejects_bad_arguments(sampler):
     """Argument errors are reported on the host, before any launch."""

@@ -4,8 +4,9 @@ The product is libtgs_sampler.so (C ABI in include/tgs_sampler.h): gfx950
 HIP kernels for penalties, temperature, the grammar mask, top-k, top-p, the
 categorical draw and speculative verification.  This package holds the
 kernels' sources (csrc/), the in-tree build, a ctypes binding (`Sampler`,
-`sample_noalloc`), the host grammar compiler that fills mask-table rows
-(`grammar`), and the synthetic workloads of the benchmark configurations
+`sample_noalloc`), the host grammar compilers whose automata fill
+mask-table rows on the device (`grammar` for GBNF, `json_schema` for JSON
+schemas), and the synthetic workloads of the benchmark configurations
 (`workloads`).
 """
 from ._lib import (  # noqa: F401

@@ -22,8 +22,9 @@
 // reject and stay columns, so every invalid move lands in the dead state and
 // a walk is a chain of branch-free LDS reads.  Otherwise the walk reads the
 // table from global memory (L2).
-// Malformed input cannot read out of bounds: a class or next state outside
-// the table rejects, rows outside the table are skipped.
+// A class or next state outside the table rejects and rows outside the
+// table are skipped.  Token offsets are trusted: each token's bytes must
+// lie inside the byte buffer (tinygpt_amd.grammar.token_csr builds them so).
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 

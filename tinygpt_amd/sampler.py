@@ -240,6 +240,17 @@ class Sampler:
         [V + 1], tok_bytes uint8, states / rows int32 [n] (device tensors).
         The table must exist (set_mask_table)."""
         torch = _torch()
+        dev = torch.device("cuda", self.device) if isinstance(self.device, int) else torch.device(self.device)
+        want = (("byte_class", byte_class, torch.uint8), ("trans", trans, torch.int32), ("complete", complete, torch.uint8),
+                ("tok_off", tok_off, torch.int32), ("tok_bytes", tok_bytes, torch.uint8),
+                ("states", states, torch.int32), ("rows", rows, torch.int32))
+        for name, t, dt in want:
+            if t.dtype != dt or not t.is_contiguous() or t.device != dev:
+                raise ValueError(f"mask_rows_from_dfa: {name} must be a contiguous {dt} tensor on {dev}")
+        if trans.dim() != 2 or byte_class.numel() != 256 or complete.numel() != trans.shape[0]:
+            raise ValueError("mask_rows_from_dfa: byte_class [256], trans [n_dfa, n_cls], complete [n_dfa]")
+        if states.numel() != rows.numel() or tok_off.numel() < 1:
+            raise ValueError("mask_rows_from_dfa: states and rows of one length, tok_off [V + 1]")
         n_dfa, n_cls = trans.shape
         V = tok_off.numel() - 1
         n = states.numel()
