@@ -548,6 +548,7 @@ def calibrate_copy(torch, mib, reps=8):
 TRAFFIC_FILES = {"c2": "k64_kernel_c2_traffic.json", "c3": "c3_grammar_traffic.json",
                  "c4": "c4_large_batch_traffic.json", "c5": "c5_spec_verify_traffic.json"}
 TRAFFIC_FILES["lp"] = "lp_scoring_traffic.json"
+TRAFFIC_FILES["c2m"] = "k64_kernel_c2m_traffic.json"
 TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
 KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c2m": "k64_kernel<float> (mask variant)",
            "c3": "topp_kernel<float, true>",
