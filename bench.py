@@ -18,6 +18,10 @@ same generator set (tinygpt_amd/workloads.py):
       (tgs_token_logprobs; a row outside the sampling chain)
   mask  grammar mask rows built on the device (tgs_mask_rows_from_dfa): 64
       new tool-tag FSM states per call over a 151,936-token byte vocabulary
+  json  JSON-schema grammar rows: 64 new snapshots of the reference's
+      pace-fm-response-v11 schema per call, local DFA on the host and rows on
+      the device (tinygpt_amd.json_schema), V=151,936; timed eagerly (host work
+      inside each call)
 
 Inputs are resident in HBM before timing; distinct input sets rotate so the
 256 MB Infinity Cache cannot serve repeats (at least 512 MB in rotation
@@ -61,7 +65,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c2m", "c3", "c4", "c5", "lp", "mask"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c2m", "c3", "c4", "c5", "lp", "mask", "json"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
@@ -497,11 +501,106 @@ class MaskRows:
         return fn
 
 
+def json_vocab(V, seed=33):
+    """synthetic_vocab with JSON pieces in its last ids: structural runs,
+    the schema's keys and enum values, escapes and numbers."""
+    pieces = ['{"', '"}', '":"', '","', '":', '",', '},', '[{', '}]', '[]', '{}', '""', '":{"', '":[', 'true',
+              'false', 'null', '\\n', '\\"', '\\u00', '0', '1', '12', '-1', '0.5', 'spokenText', '"spokenText":"',
+              'intent', '"intent":"', 'action', 'answer', 'dictate', 'edit', 'out_of_scope', 'clarify',
+              'confirm_destructive', 'payload', '"payload":{', 'name', 'args', 'calls', 'text', 'reference', '"}}']
+    extra = [p.encode() for p in pieces]
+    return synthetic_vocab(V - len(extra), seed) + extra
+
+
+class JsonRows:
+    """json: JsonSchemaConstraint.rows_for over 64 snapshots per call (each
+    call builds all of them: the constraint forgets its rows first)."""
+
+    SCHEMA = "pace-fm-response-v11"
+
+    def __init__(self, name, torch, tg, W):
+        from tinygpt_amd import json_schema as J
+
+        self.name = name
+        self.rot, self.B, self.V = 4, 64, 151936
+        self.toks = json_vocab(self.V)
+        text = open(os.path.join(ROOT, "tests", "golden", "grammars", self.SCHEMA + ".schema.json")).read()
+        self.schema_text = text
+        self.sampler = tg.Sampler(device=0, max_batch=self.B, max_vocab=self.V, max_hist=1)
+        words = (self.V + 31) // 32
+        self.sampler.set_mask_table(np.zeros((self.B, words), np.uint32), self.V)
+        self.c = J.JsonSchemaConstraint(self.sampler, J.schema_from_json(text), self.toks, eos=self.V - 1,
+                                        n_rows=self.B)
+        g = np.random.default_rng(11)
+        self.sets, self.prefixes = [], []
+        while len(self.sets) < self.rot:
+            snaps, pre = [], []
+            while len(snaps) < self.B:
+                s, data = self.c.start(), bytearray()
+                for step in range(int(g.integers(2, 200))):  # a random walk of printable bytes
+                    ok = [(b, n) for b in range(0x20, 0x7F) if (n := J.JsonSchemaFSM.accept_byte(s, b)) is not None]
+                    if not ok:
+                        break
+                    b, s = ok[int(g.integers(0, len(ok)))]
+                    data.append(b)
+                snaps.append(s)
+                pre.append(bytes(data))
+            self.sets.append(snaps)
+            self.prefixes.append(pre)
+        off, data = __import__("tinygpt_amd.grammar", fromlist=["token_csr"]).token_csr(self.toks)
+        self.alg_bytes = int(off.nbytes + data.nbytes + self.B * words * 4)
+        self.units_per_step = self.B
+        self.unit = "rows/s"
+        self.metric = "JSON-schema mask rows built/sec (pace-fm-response-v11, V=151936), workload json_rows"
+        self.config = {"workload": "json_rows", "B": self.B, "V": self.V, "schema": self.SCHEMA,
+                       "bound_note": "host local DFA (Python) + dependent LDS lookups on the device, not HBM"}
+        self.dtype = "u8"
+
+    def launch(self, i, stream):
+        self.c.reset()
+        self.c.rows_for(self.sets[i % self.rot], stream=stream)
+
+    def gpu_outputs(self):
+        import torch
+
+        import tinygpt_amd as tg
+
+        dev = "cuda:0"
+        i = self.rot - 1
+        self.launch(i, torch.cuda.current_stream().cuda_stream)
+        rows = self.c.rows_for(self.sets[i][:4])
+        params = tg.make_params(4, temperature=0.0, mask_state=rows.tolist())
+        post = torch.empty(4, self.V, dtype=torch.float32, device=dev)
+        self.sampler.sample(torch.zeros(4, self.V, device=dev), tg.params_to_device(params, dev),
+                            torch.zeros(4, device=dev), vocab=self.V, debug={"post_logits": post})
+        torch.cuda.synchronize()
+        return {i: (post == 0).cpu().numpy()}
+
+    def cpu_call(self, pyoracle, nthreads):
+        import json_fsm
+
+        def fn(i):
+            out = []
+            for pre in self.prefixes[self.rot - 1][:4]:
+                f = json_fsm.FSM(json_fsm.from_json(self.schema_text))
+                assert f.accept_bytes(pre)
+                out.append(json_fsm.masker_row(f, self.toks, eos=self.V - 1))
+            return np.array(out, dtype=bool), 4
+        return fn
+
+
 def cpu_baseline(wl, seconds):
     """The oracle (C restatement of the reference sampler) on this host:
     units/s with all host threads (up to 16) and with one thread."""
     pyoracle = oracle_mod()
     nthr = cpu_threads()
+    if isinstance(wl, JsonRows):  # the reference's clone-and-replay masker, one thread
+        rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), 1, seconds)
+        outs = {wl.rot - 1: outs[0]}
+        return dict(value=round(rate, 3), unit=wl.unit, cores=1, kind="port",
+                    host_cpu_count=os.cpu_count(), host_cpu_model=cpu_model(),
+                    sample=f"{units} rows (4 snapshots of the last set, V={wl.V}, the oracle's per-token "
+                           f"clone-and-replay of LogitsMasker.mask in Python) on 1 thread"), outs
     rate_n, units_n, outs = timed_loop(wl.cpu_call(pyoracle, nthr), wl.rot, seconds * 0.6)
     rate_1, units_1, _ = timed_loop(wl.cpu_call(pyoracle, 1), wl.rot, seconds * 0.4)
     if isinstance(wl, MaskRows):  # vectorised numpy DFA replay, one thread
@@ -549,12 +648,14 @@ TRAFFIC_FILES = {"c2": "k64_kernel_c2_traffic.json", "c3": "c3_grammar_traffic.j
                  "c4": "c4_large_batch_traffic.json", "c5": "c5_spec_verify_traffic.json"}
 TRAFFIC_FILES["lp"] = "lp_scoring_traffic.json"
 TRAFFIC_FILES["c2m"] = "k64_kernel_c2m_traffic.json"
+TRAFFIC_FILES["json"] = "json_rows_traffic.json"
 TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
 KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c2m": "k64_kernel<float> (mask variant)",
            "c3": "topp_kernel<float, true>",
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
-           "lp": "lp::chunk_kernel<float>", "mask": "maskb::prep_image + maskb::build_lds (one call)"}
+           "lp": "lp::chunk_kernel<float>", "mask": "maskb::prep_image + maskb::build_lds (one call)",
+           "json": "host local DFA + maskb kernels (one call)"}
 
 
 def main():
@@ -579,6 +680,9 @@ def main():
         wl = TokenLogprobs(args.workload, torch, tg, W)
     elif args.workload == "mask":
         wl = MaskRows(args.workload, torch, tg, W)
+    elif args.workload == "json":
+        wl = JsonRows(args.workload, torch, tg, W)
+        args.eager = True  # the host builds each call's automaton: no graph
     else:
         wl = Sampling(args.workload, torch, tg, W)
     torch.cuda.synchronize()
@@ -586,11 +690,13 @@ def main():
     ROT = wl.rot
 
     with torch.cuda.stream(stream):
-        for i in range(args.warmup):
+        for i in range(min(args.warmup, 4) if isinstance(wl, JsonRows) else args.warmup):
             wl.launch(i, stream.cuda_stream)
     torch.cuda.synchronize()
 
     steps = max(1, args.steps)
+    if isinstance(wl, JsonRows):
+        steps = min(steps, 64)  # about 0.1 s of host work per call
     reps, rem = divmod(steps, ROT)
 
     def capture(n):
@@ -629,7 +735,7 @@ def main():
     ms_per_step = ms_total / steps
 
     # per-call distribution: eager calls, each between two events
-    n_calls = 256
+    n_calls = 16 if isinstance(wl, JsonRows) else 256
     e_start = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
     e_end = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
     with torch.cuda.stream(stream):

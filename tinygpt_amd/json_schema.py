@@ -688,6 +688,10 @@ class JsonSchemaConstraint:
     def start(self):
         return self.fsm.start
 
+    def reset(self):
+        """Forget every interned snapshot (its rows are free for new ones)."""
+        self.rows = {}
+
     def rows_for(self, snaps, stream=None):
         """Table row of each snapshot (int32 numpy [n]); rows not yet built
         are built on the device (stream order)."""
