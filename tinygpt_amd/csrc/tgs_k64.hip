@@ -327,6 +327,19 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   unsigned arrived = 0;
   if (a.S > 1 && threadIdx.x == 0)
     arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the mask words depend on the parameters: requested before the chunk so
+  // that they do not queue behind it (a state out of range reads the first
+  // row, and the row is rejected below)
+  uint32_t mw[MASK ? NVT : 1];
+  if constexpr (MASK) {
+    const uint32_t* mrow = a.mask_table;
+    if (p.mask_state >= 0 && p.mask_state < a.n_states) mrow += (long long)p.mask_state * a.mask_words;
+#pragma unroll
+    for (int i = 0; i < NVT; i++) {
+      const int j = (int)threadIdx.x + i * NTT;
+      mw[i] = (i * NTT < nvec) ? mrow[(v0 + (j < nvec ? j : nvec - 1) * EPV) >> 5] : 0u;
+    }
+  }
   uint4 raw[NVT];
 #pragma unroll
   for (int i = 0; i < NVT; i++) {
@@ -356,15 +369,6 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   r.v0 = v0;
   r.v1 = v1;
   const bool masked = MASK && r.mrow != nullptr;
-  uint32_t mw[MASK ? NVT : 1];
-  if constexpr (MASK) {
-    const uint32_t* mrow = r.mrow ? r.mrow : a.mask_table;
-#pragma unroll
-    for (int i = 0; i < NVT; i++) {
-      const int j = (int)threadIdx.x + i * NTT;
-      mw[i] = (i * NTT < nvec) ? mrow[(v0 + (j < nvec ? j : nvec - 1) * EPV) >> 5] : 0u;
-    }
-  }
 
   // ---- history: each id of the chunk counted in the LDS hash (its
   // producer is the lane that created its slot) and marked in the bitmap
