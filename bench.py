@@ -18,6 +18,10 @@ same generator set (tinygpt_amd/workloads.py):
       (tgs_token_logprobs; a row outside the sampling chain)
   mask  grammar mask rows built on the device (tgs_mask_rows_from_dfa): 64
       new tool-tag FSM states per call over a 151,936-token byte vocabulary
+  jsondec  JSON-schema constrained decoding, 64 sequences under the v11 schema:
+      per step the batch's mask rows (new ones built on the device), one
+      sampling call over the masked logits, and the commit of the sampled
+      tokens; timed eagerly (host work inside each step)
   json  JSON-schema grammar rows: 64 new snapshots of the reference's
       pace-fm-response-v11 schema per call, local DFA on the host and rows on
       the device (tinygpt_amd.json_schema), V=151,936; timed eagerly (host work
@@ -65,7 +69,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c2m", "c3", "c4", "c5", "lp", "mask", "json"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c2m", "c3", "c4", "c5", "lp", "mask", "json", "jsondec"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
@@ -503,12 +507,14 @@ class MaskRows:
 
 def json_vocab(V, seed=33):
     """synthetic_vocab with JSON pieces in its last ids: structural runs,
-    the schema's keys and enum values, escapes and numbers."""
+    the schema's keys and enum values, escapes, numbers and every printable
+    ASCII byte (a real tokenizer's byte fallback: any document can be
+    spelled)."""
     pieces = ['{"', '"}', '":"', '","', '":', '",', '},', '[{', '}]', '[]', '{}', '""', '":{"', '":[', 'true',
               'false', 'null', '\\n', '\\"', '\\u00', '0', '1', '12', '-1', '0.5', 'spokenText', '"spokenText":"',
               'intent', '"intent":"', 'action', 'answer', 'dictate', 'edit', 'out_of_scope', 'clarify',
               'confirm_destructive', 'payload', '"payload":{', 'name', 'args', 'calls', 'text', 'reference', '"}}']
-    extra = [p.encode() for p in pieces]
+    extra = [p.encode() for p in pieces] + [bytes([c]) for c in range(0x20, 0x7F)]  # every printable byte
     return synthetic_vocab(V - len(extra), seed) + extra
 
 
@@ -589,11 +595,120 @@ class JsonRows:
         return fn
 
 
+class JsonDecode:
+    """jsondec: one constrained decoding step of 64 sequences per call:
+    JsonSchemaConstraint.rows_for, tgs_sample over the masked logits
+    (T = 1, top-p 0.95), commit of the 64 ids (a sequence that completes
+    samples EOS once and starts a new document)."""
+
+    SCHEMA = "pace-fm-response-v11"
+
+    def __init__(self, name, torch, tg, W):
+        from tinygpt_amd import json_schema as J
+
+        dev = "cuda:0"
+        self.J, self.tg, self.torch = J, tg, torch
+        self.name = name
+        self.rot, self.B, self.V = 4, 64, 151936
+        self.toks = json_vocab(self.V)
+        self.eos = 0  # the empty token: never allowed but as EOS
+        text = open(os.path.join(ROOT, "tests", "golden", "grammars", self.SCHEMA + ".schema.json")).read()
+        self.schema_text = text
+        self.sampler = tg.Sampler(device=0, max_batch=self.B, max_vocab=self.V, max_hist=1)
+        n_rows = 4096
+        self.sampler.set_mask_table(np.zeros((n_rows, (self.V + 31) // 32), np.uint32), self.V)
+        self.c = J.JsonSchemaConstraint(self.sampler, J.schema_from_json(text), self.toks, eos=self.eos,
+                                        n_rows=n_rows)
+        g = np.random.default_rng(12)
+        # closing pieces likelier, so documents finish; tokens that are not UTF-8 never sampled
+        bias = np.zeros(self.V, np.float32)
+        for i, t in enumerate(self.toks):
+            try:
+                t.decode("utf-8")
+            except UnicodeDecodeError:
+                bias[i] = -np.inf
+                continue
+            if b'"' in t or b"}" in t:
+                bias[i] = 3.0
+        self.d_logits = [torch.from_numpy(W.normal_f32(g, (self.B, self.V), 3.0) + bias).to(dev)
+                         for _ in range(self.rot)]
+        self.d_u = [torch.from_numpy(W.uniforms(g, self.B)).to(dev) for _ in range(self.rot)]
+        self.params = tg.make_params(self.B, temperature=1.0, top_p=0.95)
+        self.out = torch.empty(self.B, dtype=torch.int32, device=dev)
+        self.snaps = [self.c.start()] * self.B
+        self.docs = [bytearray() for _ in range(self.B)]
+        self.completed = 0
+        self.stuck = 0  # documents no token could continue (id -1, nothing allowed)
+        self.checks = []  # (prefix, id) pairs kept for the parity check
+        self.alg_bytes = self.B * self.V * 4
+        self.units_per_step = self.B
+        self.unit = "tokens/s"
+        self.metric = "JSON-schema constrained decode tokens/sec (64 sequences, pace-fm-response-v11, V=151936)"
+        self.config = {"workload": "jsondec", "B": self.B, "V": self.V, "schema": self.SCHEMA, "temperature": 1.0,
+                       "top_p": 0.95, "bound_note": "host automaton and row interning per step; the sampling call "
+                                                    "is the C3-style masked top-p kernel"}
+        self.dtype = "f32"
+
+    def launch(self, i, stream):
+        tg = self.tg
+        try:
+            rows = self.c.rows_for(self.snaps, stream=stream)
+        except RuntimeError:  # the constraint's rows are used up: start over
+            self.c.reset()
+            rows = self.c.rows_for(self.snaps, stream=stream)
+        self.params["mask_state"] = rows
+        pd = tg.params_to_device(self.params, "cuda:0")
+        self.sampler.sample(self.d_logits[i % self.rot], pd, self.d_u[i % self.rot], out=self.out, stream=stream,
+                            hint=tg.batch_hint(self.params, self.V))
+        ids = self.out.cpu().numpy()
+        for b in range(self.B):
+            t = int(ids[b])
+            if t < 0:  # no token of this vocabulary continues the document: start a new one
+                self.snaps[b], self.docs[b] = self.c.start(), bytearray()
+                self.stuck += 1
+                continue
+            if len(self.checks) < 8 and b < 2:
+                self.checks.append((bytes(self.docs[b]), t))
+            if self.J.JsonSchemaFSM.is_complete(self.snaps[b]):
+                if t != self.eos:
+                    raise RuntimeError(f"a complete sequence sampled {t}, not EOS")
+                self.snaps[b], self.docs[b] = self.c.start(), bytearray()
+                self.completed += 1
+                continue
+            n = self.c.commit(self.snaps[b], t)
+            if n is None:
+                raise RuntimeError(f"sampled token {t} rejected by the automaton")
+            self.snaps[b] = n
+            self.docs[b] += self.toks[t]
+
+    def gpu_outputs(self):
+        return {0: np.array([t for _, t in self.checks], np.int64)}
+
+    def cpu_call(self, pyoracle, nthreads):
+        import json_fsm
+
+        def fn(i):
+            ok = []
+            for pre, t in self.checks:
+                f = json_fsm.FSM(json_fsm.from_json(self.schema_text))
+                assert f.accept_bytes(pre)
+                row = json_fsm.masker_row(f, self.toks, eos=self.eos)
+                ok.append(t if row[t] else -1)  # the sampled id when the reference's masker allows it
+            return np.array(ok, np.int64), len(self.checks)
+        return fn
+
+
 def cpu_baseline(wl, seconds):
     """The oracle (C restatement of the reference sampler) on this host:
     units/s with all host threads (up to 16) and with one thread."""
     pyoracle = oracle_mod()
     nthr = cpu_threads()
+    if isinstance(wl, JsonDecode):  # the reference's masker on the checked steps, one thread
+        rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), 1, seconds)
+        return dict(value=round(rate, 3), unit="masked rows/s", cores=1, kind="port",
+                    host_cpu_count=os.cpu_count(), host_cpu_model=cpu_model(),
+                    sample=f"{units} rows: the oracle's clone-and-replay of LogitsMasker.mask over V={wl.V} for "
+                           f"sampled steps of two sequences, 1 thread (the reference's masking cost per token)"), outs
     if isinstance(wl, JsonRows):  # the reference's clone-and-replay masker, one thread
         rate, units, outs = timed_loop(wl.cpu_call(pyoracle, 1), 1, seconds)
         outs = {wl.rot - 1: outs[0]}
@@ -655,7 +770,8 @@ KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c2m": "k64_ker
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
            "lp": "lp::chunk_kernel<float>", "mask": "maskb::prep_image + maskb::build_lds (one call)",
-           "json": "host local DFA + maskb kernels (one call)"}
+           "json": "host local DFA + maskb kernels (one call)",
+           "jsondec": "host automaton + mask rows + topp_kernel per step"}
 
 
 def main():
@@ -683,6 +799,9 @@ def main():
     elif args.workload == "json":
         wl = JsonRows(args.workload, torch, tg, W)
         args.eager = True  # the host builds each call's automaton: no graph
+    elif args.workload == "jsondec":
+        wl = JsonDecode(args.workload, torch, tg, W)
+        args.eager = True
     else:
         wl = Sampling(args.workload, torch, tg, W)
     torch.cuda.synchronize()
@@ -690,13 +809,13 @@ def main():
     ROT = wl.rot
 
     with torch.cuda.stream(stream):
-        for i in range(min(args.warmup, 4) if isinstance(wl, JsonRows) else args.warmup):
+        for i in range(min(args.warmup, 4) if isinstance(wl, (JsonRows, JsonDecode)) else args.warmup):
             wl.launch(i, stream.cuda_stream)
     torch.cuda.synchronize()
 
     steps = max(1, args.steps)
-    if isinstance(wl, JsonRows):
-        steps = min(steps, 64)  # about 0.1 s of host work per call
+    if isinstance(wl, (JsonRows, JsonDecode)):
+        steps = min(steps, 64 if isinstance(wl, JsonRows) else 200)  # host work in every call
     reps, rem = divmod(steps, ROT)
 
     def capture(n):
@@ -735,7 +854,7 @@ def main():
     ms_per_step = ms_total / steps
 
     # per-call distribution: eager calls, each between two events
-    n_calls = 16 if isinstance(wl, JsonRows) else 256
+    n_calls = 16 if isinstance(wl, (JsonRows, JsonDecode)) else 256
     e_start = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
     e_end = [torch.cuda.Event(enable_timing=True) for _ in range(n_calls)]
     with torch.cuda.stream(stream):
@@ -802,6 +921,10 @@ def main():
     }
     if isinstance(wl, SpecVerify):
         line["tokens_per_s"] = round(wl.tokens_per_step() / (ms_per_step * 1e-3), 1)
+    if isinstance(wl, JsonDecode):
+        line["documents_completed"] = wl.completed
+        line["documents_stuck"] = wl.stuck
+        line["mask_rows_built"] = wl.c.built
     print(json.dumps(line), flush=True)
 
 

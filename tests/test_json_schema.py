@@ -298,3 +298,41 @@ def test_canonical_keys_merge_equivalent_snapshots():
     f = J.JsonSchemaFSM(node)
     assert k(b'{"zz') == k(b'{"qq') != k(b'{"a')
     assert k(b'{"zz":1') == k(b'{"qq":1') != k(b'{"ab":1')
+
+
+@pytest.mark.parametrize("si", range(len(SCHEMAS)))
+def test_row_keys_share_only_equal_rows(si):
+    """Snapshots that share a row key (an open string's count kept only as
+    far as a token can see it) get equal rows; along a long string the keys
+    collapse to a few."""
+    text = SCHEMAS[si]
+    toks = U.json_vocab(n_random=300)
+    trie = J.TokenTrie(toks)
+    fsm = J.JsonSchemaFSM(J.schema_from_json(text))
+    g = np.random.default_rng(700 + si)
+    snaps = []
+    for _ in range(4):
+        _, sn = U.random_document(fsm, g, max_steps=300, partial=True)
+        snaps += sn
+    d = J.local_dfa(snaps, trie)
+    by_key = {}
+    for s, root in zip(snaps, d.roots):
+        row = U.dfa_row(d, root, toks, eos=3)
+        k = J.row_key(s, trie.max_len)
+        if k in by_key:
+            np.testing.assert_array_equal(by_key[k], row)
+        else:
+            by_key[k] = row
+    assert len(by_key) <= len(set(J.canonical_key(s) for s in snaps))
+
+
+def test_row_keys_collapse_a_long_string():
+    f = J.JsonSchemaFSM(J.schema_from_json(U.fixture_text("pace-fm-response-v11")))
+    s = J.JsonSchemaFSM.accept_bytes(f.start, b'{"spokenText":"')
+    keys = set()
+    for _ in range(400):  # counts 0 .. 399 of maxLength 400
+        keys.add(J.row_key(s, 24))
+        s = J.JsonSchemaFSM.accept_byte(s, ord("a"))
+    assert J.JsonSchemaFSM.accept_byte(s, ord("a")) is None  # a 401st character is refused
+    # count 0 (one more needed before the quote), counts 1..375 (room beyond any token), then 376..399
+    assert len(keys) == 26

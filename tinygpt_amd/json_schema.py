@@ -488,6 +488,23 @@ def _is_free(snap):
     return _canon_frame(top, snap[-2] if len(snap) > 1 else None)[6] == _OTHER
 
 
+def row_key(snap, max_len: int):
+    """Key under which snapshots get the same mask row: the canonical key,
+    except that an open free string's character count is kept only as far as
+    a token of at most max_len bytes can see it (how many characters the
+    string still needs before it may close, and how many it may still take,
+    each capped at max_len + 1)."""
+    key = canonical_key(snap)
+    top = key[-1]
+    if top[0] == "S" and isinstance(top[6], int):
+        _, st, digits, enum, mn, mx, cnt, is_key = top
+        cap = max_len + 1
+        need = min(max((mn or 0) - cnt, 0), cap)
+        room = cap if mx is None else min(mx - cnt, cap)
+        key = key[:-1] + (("S", st, digits, enum, None, None, ("need", need, "room", room), is_key),)
+    return key
+
+
 def _byte_groups(snap):
     """Groups of bytes with the same canonical successor from snap (each
     group evaluated once), as (representative, bytes) pairs; bytes outside
@@ -660,8 +677,9 @@ def local_dfa(snaps, trie: TokenTrie, max_states: int = 200000) -> LocalDfa:
 class JsonSchemaConstraint:
     """Per-sequence JSON-schema constraint over a sampler's mask table.
 
-    Snapshots are interned as table rows (canonical keys; rows [row0,
-    row0 + n_rows) of the table are this constraint's); `rows_for` returns
+    Snapshots are interned as table rows (row keys: snapshots that no token
+    can tell apart share a row; rows [row0, row0 + n_rows) of the table are
+    this constraint's); `rows_for` returns
     the row of each sequence's snapshot and builds the new ones on the
     device in one tgs_mask_rows_from_dfa call; `commit` replays the sampled
     token's bytes (LogitsMasker.commit, ConstrainedGen.swift:827-830)."""
@@ -700,7 +718,7 @@ class JsonSchemaConstraint:
         out = np.empty(len(snaps), dtype=np.int32)
         new = []
         for i, s in enumerate(snaps):
-            key = canonical_key(s)
+            key = row_key(s, self.trie.max_len)
             r = self.rows.get(key)
             if r is None:
                 if len(self.rows) >= self.n_rows:
