@@ -337,16 +337,21 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
 #pragma unroll
     for (int i = 0; i < NVT; i++) {
       const int j = (int)threadIdx.x + i * NTT;
-      mw[i] = (i * NTT < nvec) ? mrow[(v0 + (j < nvec ? j : nvec - 1) * EPV) >> 5] : 0u;
+      mw[i] = mrow[(v0 + (j < nvec ? j : nvec - 1) * EPV) >> 5];
     }
   }
+  // Whole vectors: one unconditional load each (a vector past the chunk
+  // reads its last one again and is left out in step 1).  With no branch
+  // among the loads the compiler waits exactly for the history ids and the
+  // arrival count, so the history hash is built while the chunk streams in.
   uint4 raw[NVT];
 #pragma unroll
   for (int i = 0; i < NVT; i++) {
     const int j = (int)threadIdx.x + i * NTT;
-    if (i * NTT < nvec) {  // whole-workgroup test: vectors wholly past the chunk are not read
-      if constexpr (VEC) raw[i] = tg_load_nt(rowp + v0 + (j < nvec ? j : nvec - 1) * EPV);
-      else raw[i] = load_vec<Tin>(rowp, v0 + j * EPV, v1, a.aligned);
+    if constexpr (VEC) {
+      raw[i] = tg_load_nt(rowp + v0 + (j < nvec ? j : nvec - 1) * EPV);
+    } else if (i * NTT < nvec) {  // whole-workgroup test: vectors wholly past the chunk are not read
+      raw[i] = load_vec<Tin>(rowp, v0 + j * EPV, v1, a.aligned);
     } else {
       raw[i] = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);  // NaN: never counted
     }
@@ -439,7 +444,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
 #pragma unroll
       for (int e = 1; e < EPV; e++) m = fmaxf(m, Elem<Tin>::get(raw[i], e));
     }
-    if (i == nfull) m = ((int)threadIdx.x + i * NTT < nvec) ? m : -__builtin_inff();  // the partial vector round
+    if (i >= nfull) m = ((int)threadIdx.x + i * NTT < nvec) ? m : -__builtin_inff();  // vectors past the chunk
     vm[i] = m;
     tm = fmaxf(tm, m);
   }

@@ -179,6 +179,39 @@ __device__ __forceinline__ void hash_build(const SampleArgs& a, const Row& r, in
   __syncthreads();
 }
 
+// The history entries of this thread, read before the row's logits so that
+// building the hash does not wait for them (a wave's loads return in
+// order): entry threadIdx.x + q * BS in hid[q] (clamped reads; entries at
+// or past the row's history length are ignored by hash_build_pre).
+template <int BS, int NPRE>
+__device__ __forceinline__ void hist_prefetch(const SampleArgs& a, int b, int (&hid)[NPRE]) {
+  const bool hv = a.hist && a.hist_cap > 0;
+  const int* hp = hv ? a.hist + (long long)b * a.hist_cap : (const int*)a.params;
+  const int hlast = hv ? a.hist_cap - 1 : 0;
+#pragma unroll
+  for (int q = 0; q < NPRE; q++) {
+    const int j = (int)threadIdx.x + q * BS;
+    hid[q] = hp[j < hlast ? j : hlast];
+  }
+}
+
+// hash_build over the entries hist_prefetch read (r.H <= NPRE * BS).
+template <int BS, int NPRE>
+__device__ __forceinline__ void hash_build_pre(const SampleArgs& a, const Row& r, const int (&hid)[NPRE],
+                                               int2* hash, uint32_t* bitmap, int BW) {
+  for (int i = threadIdx.x; i < a.TS; i += BS) hash[i] = make_int2(-1, 0);
+  for (int i = threadIdx.x; i < BW; i += BS) bitmap[i] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < NPRE; q++) {
+    const int id = hid[q];
+    if ((int)threadIdx.x + q * BS >= r.H || id < r.v0 || id >= r.v1 || id >= a.V) continue;
+    hash_insert(hash, a.TS, a.ts_shift, id);
+    if (BW) atomicOr(&bitmap[(id - r.v0) >> 5], 1u << ((id - r.v0) & 31));
+  }
+  __syncthreads();
+}
+
 __device__ __forceinline__ int hash_count(const int2* hash, int TS, int shift, int id) {
   const unsigned tmask = (unsigned)TS - 1u;
   unsigned h = hash_slot(id, shift);

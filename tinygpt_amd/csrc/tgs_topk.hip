@@ -88,15 +88,18 @@ struct Regs {
   uint4 raw[NVR];  // the row, packed as loaded
   __device__ __forceinline__ static int vec_id(int j) { return ((int)threadIdx.x + j * BT) * EPV; }
   // every vector, from addresses clamped into the row (the row is 16-byte
-  // aligned and a whole number of vectors); vectors past the end become
-  // all-ones words: NaN in every element, below every logit as a signed
-  // integer and never at or above a bound
+  // aligned and a whole number of vectors)
   __device__ __forceinline__ void load(const Tin* rowp, int V) {
 #pragma unroll
     for (int j = 0; j < NVR; j++) {
       const int v = vec_id(j);
       raw[j] = *(const uint4*)(rowp + (v < V ? v : V - EPV));
     }
+  }
+  // vectors past the end become all-ones words: NaN in every element, below
+  // every logit as a signed integer and never at or above a bound.  Apart
+  // from load, so that the work between them does not wait for the row.
+  __device__ __forceinline__ void past_end(int V) {
 #pragma unroll
     for (int j = 0; j < NVR; j++)
       if (vec_id(j) >= V) raw[j] = make_uint4(~0u, ~0u, ~0u, ~0u);
@@ -525,7 +528,7 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
 
 template <typename Tin, int NVR, bool MASK>
 __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned char* smem, Scratch& ts,
-                                         BlockScratch& bs) {
+                                         BlockScratch& bs, Regs<Tin, NVR>& g, const int (&hpre)[1]) {
   using RG = Regs<Tin, NVR>;
   constexpr int EPV = RG::EPV;
   constexpr int NEL = NVR * EPV;       // ids per thread
@@ -545,19 +548,18 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
   const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
   const int k = r.mode == 0 ? 1 : r.k;
 
-  // load: every vector of the row, once
-  RG g;
-  g.load(rowp, V);
+  // the row's vectors (g) and history entries (hpre) were requested at entry
   // history: id -> count hash and the row's bitmap; distinct ids
   r.v0 = 0;
   r.v1 = V;
   unsigned nh = 0;
   if (r.use_pen) {
-    hash_build<BT>(a, r, hash, hbits, bw);
+    hash_build_pre<BT, 1>(a, r, hpre, hash, hbits, bw);
     unsigned c = 0;
     for (int i = threadIdx.x; i < a.TS; i += BT) c += hash[i].x != -1;
     nh = bsum(c, ts.red32);
   }
+  g.past_end(V);
   if (MASK && r.mrow != nullptr) g.apply_mask(r, V);
 
   // bound
@@ -751,8 +753,18 @@ __global__ __launch_bounds__(BT) void topk_kernel(SampleArgs a) {
   __shared__ BlockScratch bs;
   const int b = blockIdx.x;
   if (b >= a.B) return;
+  // everything requested first, in the order it is needed (a wave's loads
+  // return in order): the row's parameters (scalar loads), its history
+  // entries (one per thread: the history is at most KMAX ids), its vectors
+  const tgs_row_params p = a.params[b];
+  const float ub = a.u[b];
+  const int hl = a.hist_len ? a.hist_len[b] : a.hist_cap;
+  int hid[1];
+  hist_prefetch<BT, 1>(a, b, hid);
+  Regs<Tin, NVR> g;
+  g.load((const Tin*)a.logits + (long long)b * a.row_stride, a.V);
   Row r;
-  const bool valid = row_setup(a, b, 0, r);
+  const bool valid = row_setup_from(a, b, 0, p, ub, hl, r);
   if (!valid || outside_hint(a, r) || r.mode == 2) {
     if (threadIdx.x == 0) {
       a.out[b] = valid ? -3 : -2;  // -3: row outside the launch hint
@@ -760,7 +772,7 @@ __global__ __launch_bounds__(BT) void topk_kernel(SampleArgs a) {
     }
     return;
   }
-  topk_row<Tin, NVR, MASK>(a, r, smem, ts, bs);
+  topk_row<Tin, NVR, MASK>(a, r, smem, ts, bs, g, hid);
 }
 
 template <typename Tin, int NVR>

@@ -87,24 +87,61 @@ struct RowView {
     }
   }
 
-  // the row's vectors of this thread (issued before the row's parameters are
-  // read, so the two latencies overlap)
+  // the row's vectors of this thread.  Rows of whole aligned vectors read
+  // every vector with one unconditional load (a vector past the row end
+  // reads the last one again; vec_y drops its ids), so no load waits for an
+  // earlier one: a divergent fallback beside the loads makes the compiler
+  // wait for the loads already issued before reusing their registers.
   __device__ __forceinline__ static void fetch(const SampleArgs& a, const Tin* p, uint4 (&raw)[NV]) {
     if constexpr (RES) {
+      if (a.aligned && a.V >= EPV && a.V % EPV == 0) {
+        const int last = a.V / EPV - 1;
 #pragma unroll
-      for (int j = 0; j < NV; j++) raw[j] = load_vec<Tin>(p, (threadIdx.x + j * BT) * EPV, a.V, a.aligned);
+        for (int j = 0; j < NV; j++) {
+          const int vi = (int)threadIdx.x + j * BT;
+          raw[j] = tg_load_nt(p + (vi < last ? vi : last) * EPV);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NV; j++) raw[j] = load_vec<Tin>(p, (threadIdx.x + j * BT) * EPV, a.V, a.aligned);
+      }
+    }
+  }
+
+  // y of the register-resident vectors, specialised on what is uniform over
+  // the row (penalties present, a power-of-two temperature) so that the
+  // per-element code carries no branch for the cases the row does not have;
+  // every mask word is requested before the first element is evaluated
+  template <bool PEN, bool POW2>
+  __device__ __forceinline__ void load_t(const uint4 (&raw)[NV]) {
+    uint32_t mw[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int v = ((int)threadIdx.x + j * BT) * EPV;
+      mw[j] = v >= a.V ? 0u : r.mrow ? r.mrow[v >> 5] : 0xFFFFFFFFu;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int v = ((int)threadIdx.x + j * BT) * EPV;
+      const uint32_t hw = (PEN && v < a.V) ? hbits[v >> 5] : 0u;
+#pragma unroll
+      for (int e = 0; e < EPV; e++) {
+        const int id = v + e;
+        float z = Elem<Tin>::get(raw[j], e);
+        if constexpr (PEN) {
+          if ((hw >> (id & 31)) & 1u) z = penalise(z, hash_count(hash, a.TS, a.ts_shift, id), r);
+        }
+        const float yy = POW2 ? z * r.rT : row_y(r, z);
+        y[j * EPV + e] = (((mw[j] >> (id & 31)) & 1u) && yy > -__builtin_inff() && id < a.V) ? yy : -__builtin_inff();
+      }
     }
   }
 
   __device__ __forceinline__ void load(const uint4 (&raw)[NV]) {
     if constexpr (RES) {
-#pragma unroll
-      for (int j = 0; j < NV; j++) {
-        float yv[EPV];
-        vec_y((threadIdx.x + j * BT) * EPV, raw[j], yv);
-#pragma unroll
-        for (int e = 0; e < EPV; e++) y[j * EPV + e] = yv[e];
-      }
+      if (r.use_pen) load_t<true, false>(raw);
+      else if (r.tdiv == TDIV_POW2) load_t<false, true>(raw);
+      else load_t<false, false>(raw);
     }
   }
 
@@ -435,10 +472,15 @@ __global__ __launch_bounds__(BT) void topp_kernel(SampleArgs a) {
   __shared__ BlockScratch bs;
   const int b = blockIdx.x;
   if (b >= a.B) return;
+  // the row's parameters (scalar loads) requested before its vectors, so
+  // that they arrive first and the mask words can be requested early
+  const tgs_row_params p = a.params[b];
+  const float ub = a.u[b];
+  const int hl = a.hist_len ? a.hist_len[b] : a.hist_cap;
   uint4 raw[RowView<Tin, RES>::NV];
   RowView<Tin, RES>::fetch(a, (const Tin*)a.logits + (long long)b * a.row_stride, raw);
   Row r;
-  const bool valid = row_setup(a, b, 0, r);
+  const bool valid = row_setup_from(a, b, 0, p, ub, hl, r);
   const bool mine = valid && (r.mode == 2 ? !(r.k >= 1 && r.k < a.V) : (r.mode == 0 && a.topp_all));
   if (!mine) {
     // other kernels' rows; in a launch that serves the whole batch, invalid
