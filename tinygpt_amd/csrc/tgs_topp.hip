@@ -19,8 +19,12 @@
 //           draw;
 //   pass 3  gather that bucket's ids (composites) into LDS, rank them (a
 //           wave sort for at most 64), scan their masses in rank order and
-//           pick the element.  The draw's bucket reuses the ranked list
-//           when it is the cut's bucket; otherwise one more gather.
+//           pick the element.  The draw's bucket is known before the cut is
+//           resolved whenever every S' the cut can leave draws from one
+//           bucket (nearly always: S' lies in the cut's bucket); then one
+//           gather collects both buckets and two waves rank them side by
+//           side.  Otherwise the cut is resolved first and the draw's
+//           bucket gathered after it.
 //
 // A row of at most 32768 ids is held in registers (32 per thread) after one
 // read; a longer row is streamed again from L2 / MALL by every pass.
@@ -48,9 +52,10 @@ struct Scratch {
   u64 red64b[WT];
   unsigned red32[WT];
   unsigned ng;    // gathered ids
-  unsigned ncomp; // allowed ids packed
+  unsigned ng2;   // gathered ids of the draw's bucket (list B)
   int sel[2];     // buckets of the cut and of the draw
   int first;      // first rank meeting a mass target
+  int first2;     // the same for the draw, in the one-gather tail
 };
 
 // The row's canonical logits: y after penalties and temperature, -inf where
@@ -240,12 +245,50 @@ __device__ __forceinline__ T block_reduce_max(T x, T* red) {
 struct Tail {
   unsigned* CI;  // NB + 1 inclusive counts
   u64* MI;       // NB + 1 inclusive masses
-  u64 *L, *R, *Q;
+  u64 *L, *R, *Q;     // list A: CAPG gathered, ranked, inclusive masses
+  u64 *L2, *R2, *Q2;  // list B: the same for at most 64 ids
   Packed* E;     // a.topp_cap packed allowed ids
   float m;
   int rb = -1;   // ranked bucket (-1: none)
   unsigned rn = 0;
 };
+
+// One wave ranks L[0, n) (n <= 64) into R (descending) and Q (inclusive
+// masses under m); no barrier.
+__device__ __forceinline__ void wave_rank64(const u64* L, unsigned n, float m, u64* R, u64* Q) {
+  const int lane = lane_id();
+  u64 x = lane < (int)n ? L[lane] : 0ull;
+  x = wave_sort_desc(x);
+  const u64 q = lane < (int)n ? bucket::mass_c(x, m) : 0ull;
+  const u64 ci = wave_incl_scan(q);
+  if (lane < (int)n) {
+    R[lane] = x;
+    Q[lane] = ci;
+  }
+}
+
+// The buckets whose inclusive masses first reach t1 and t2 (both in
+// [1, MI[NB - 1]]), in one pass and one barrier.
+__device__ __forceinline__ void find_mass2(const u64* MI, u64 t1, u64 t2, int* s1, int* s2) {
+  constexpr int PER = NB / BT;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int t = threadIdx.x * PER + i;
+    const u64 lo = t ? MI[t - 1] : 0ull, hi = MI[t];
+    if (hi >= t1 && lo < t1) *s1 = t;
+    if (hi >= t2 && lo < t2) *s2 = t;
+  }
+  __syncthreads();
+}
+
+// First rank of a ranked list whose inclusive mass reaches target (>= 1, at
+// most Q[n - 1]); one barrier, so each call needs a slot of its own.
+__device__ __forceinline__ int first_rank_once(const u64* Q, unsigned n, u64 target, int* slot) {
+  const int i = threadIdx.x;
+  if (i < (int)n && Q[i] >= target && (i == 0 || Q[i - 1] < target)) *slot = i;
+  __syncthreads();
+  return *slot;
+}
 
 // The element of bucket bq whose within-bucket inclusive prefix first
 // reaches target (>= 1): its composite, the mass ahead of it in the bucket
@@ -310,34 +353,81 @@ __device__ __forceinline__ void topp_rest(const SampleArgs& a, const Row& r, con
   const u64 S = tl.MI[NB - 1];
 
   // the cut (top-p): element i* with inclusive prefix >= P
-  u64 cutc = 0, Sp = S;
+  u64 cutc = 0, Sp = S, P = 0;
   unsigned ntopp = nv;
-  bool cut_last = false;
+  bool cut_last = false, cut_search = false;
   if (r.top_p < 1.0f) {
     const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
-    const u64 P = mul_shr24(S, pq);
+    P = mul_shr24(S, pq);
     if (P == 0) {
       cutc = Mc;
       Sp = tg_q40(1.0f);
       ntopp = 1;
     } else {
-      const int bp = bucket::find_mass<BT>(tl.MI, P, &ts.sel[0]);
+      cut_search = true;
+    }
+  } else {
+    cut_last = true;
+  }
+  // the draw: first element with inclusive prefix > t = floor(S' u24 / 2^24).
+  // While the cut is open, S' lies in [P, MI[bp]] (the cut's inclusive
+  // prefix reaches P and ends inside bucket bp), so t lies in [tlo, thi];
+  // when bucket bt holds every target in [tlo + 1, thi + 1], the cut's and
+  // the draw's buckets are gathered in one pass and ranked side by side.
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
+  const u64 tlo = mul_shr24(cut_search ? P : Sp, uq);
+  if (threadIdx.x == 0) {
+    ts.ng = 0;
+    ts.ng2 = 0;
+  }
+  find_mass2(tl.MI, cut_search ? P : tlo + 1, tlo + 1, &ts.sel[0], &ts.sel[1]);
+  const int bp = ts.sel[0], btl = ts.sel[1];
+  const int ba = cut_search ? bp : btl;               // list A: the cut's bucket (else the draw's)
+  const int bb = (cut_search && btl != bp) ? btl : -1;  // list B: the draw's bucket when it differs
+  const unsigned na = tl.CI[ba] - bucket::count_before(tl.CI, ba);
+  const unsigned nb2 = bb >= 0 ? tl.CI[bb] - bucket::count_before(tl.CI, bb) : 0u;
+  bool one = na <= (unsigned)CAPG && nb2 <= 64u;
+  if (cut_search) one = one && tl.MI[btl] >= mul_shr24(tl.MI[bp], uq) + 1;
+  u64 pick;
+  if (one) {
+    if (threadIdx.x == 0 && (na & 1)) tl.L[na] = 0ull;  // pad below every composite
+    rv.each([&](int id, float y) {
+      const int q = bucket::of(y, m);
+      if (q == ba) tl.L[atomicAdd(&ts.ng, 1u)] = comp_key(tg_key(y), id);
+      else if (q == bb) tl.L2[atomicAdd(&ts.ng2, 1u)] = comp_key(tg_key(y), id);
+    });
+    __syncthreads();
+    if (bb >= 0 && (threadIdx.x >> 6) == 1) wave_rank64(tl.L2, nb2, m, tl.R2, tl.Q2);
+    if (na > 64u) {
+      bucket::rank_list<BT>(tl.L, na, m, tl.R, tl.Q, ts.red64b);  // ends with a barrier
+    } else {
+      if ((threadIdx.x >> 6) == 0) wave_rank64(tl.L, na, m, tl.R, tl.Q);
+      __syncthreads();
+    }
+    if (cut_search) {
+      const int i = first_rank_once(tl.Q, na, P - bucket::mass_before(tl.MI, bp), &ts.first);
+      cutc = tl.R[i];
+      Sp = bucket::mass_before(tl.MI, bp) + (i > 0 ? tl.Q[i - 1] : 0ull) + bucket::mass_c(cutc, m);
+      ntopp = bucket::count_before(tl.CI, bp) + (unsigned)i + 1u;
+    }
+    const u64 t = mul_shr24(Sp, uq);
+    const u64 tb = t + 1 - bucket::mass_before(tl.MI, btl);
+    if (bb >= 0) pick = tl.R2[first_rank_once(tl.Q2, nb2, tb, &ts.first2)];
+    else pick = tl.R[first_rank_once(tl.Q, na, tb, &ts.first2)];
+  } else {
+    if (cut_search) {
       u64 before;
       unsigned rank;
       cutc = resolve_mass(rv, tl, bp, P - bucket::mass_before(tl.MI, bp), &before, &rank, ts, bs);
       Sp = bucket::mass_before(tl.MI, bp) + before + bucket::mass_c(cutc, m);
       ntopp = bucket::count_before(tl.CI, bp) + rank + 1;
     }
-  } else {
-    cut_last = true;
+    const u64 t = mul_shr24(Sp, uq);
+    const int bt = bucket::find_mass<BT>(tl.MI, t + 1, &ts.sel[1]);
+    u64 before;
+    unsigned rank;
+    pick = resolve_mass(rv, tl, bt, t + 1 - bucket::mass_before(tl.MI, bt), &before, &rank, ts, bs);
   }
-  // the draw: first element with inclusive prefix > t
-  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
-  const u64 t = mul_shr24(Sp, uq);
-  const int bt = bucket::find_mass<BT>(tl.MI, t + 1, &ts.sel[1]);
-  u64 before;
-  unsigned rank;
-  const u64 pick = resolve_mass(rv, tl, bt, t + 1 - bucket::mass_before(tl.MI, bt), &before, &rank, ts, bs);
   // diagnostics: with top-p disabled the cut is the smallest allowed composite
   if (cut_last && a.dbg.cut_ids) {
     u64 x = 0;
@@ -370,7 +460,10 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
   tl.Q = tl.R + CAPG;                                       // CAPG
   tl.CI = (unsigned*)(tl.Q + CAPG);                         // NB + 1 (+ pad)
   tl.MI = (u64*)(tl.CI + NB + 4);                           // NB + 1
-  tl.E = (Packed*)(tl.MI + NB + 1);                         // a.topp_cap
+  tl.L2 = tl.MI + NB + 1;                                   // 64 (+ pad)
+  tl.R2 = tl.L2 + 66;                                       // 64
+  tl.Q2 = tl.R2 + 64;                                       // 64
+  tl.E = (Packed*)(tl.Q2 + 64);                             // a.topp_cap
   r.v0 = 0;
   r.v1 = a.V;
   if (r.use_pen) hash_build<BT>(a, r, hash, hbits, bw);
@@ -415,18 +508,19 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
     tl.MI[i] = 0ull;
   }
   const unsigned nown = nvl;  // this thread's allowed ids
+  const unsigned wincl = wave_incl_scan(nown);  // lane 63: the wave's allowed ids
   mcl = wave_max(mcl);
-  nvl = wave_sum(nvl);
-  if (lane_id() == 0) {
+  if (lane_id() == 63) {
     ts.red64[threadIdx.x >> 6] = mcl;
-    ts.red32[threadIdx.x >> 6] = nvl;
+    ts.red32[threadIdx.x >> 6] = wincl;
   }
   __syncthreads();
   u64 Mc = 0;
-  unsigned nv = 0;
+  unsigned nv = 0, wbase = 0;  // wbase: allowed ids of the waves before this one
 #pragma unroll
   for (int i = 0; i < WT; i++) {
     Mc = ts.red64[i] > Mc ? ts.red64[i] : Mc;
+    wbase += i < (int)(threadIdx.x >> 6) ? ts.red32[i] : 0u;
     nv += ts.red32[i];
   }
   if (nv == 0 || r.mode == 0) {
@@ -450,12 +544,9 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
       // few allowed ids (a grammar mask): they alone, packed into LDS, feed
       // every later pass (the exact exp and the bucket gathers run on
       // allowed ids only)
-      if (threadIdx.x == 0) ts.ncomp = 0;
-      __syncthreads();
-      const unsigned wincl = wave_incl_scan(nown);
-      unsigned wbase = 0;
-      if (lane_id() == 63 && wincl) wbase = atomicAdd(&ts.ncomp, wincl);
-      unsigned off = __shfl(wbase, 63, 64) + wincl - nown;
+      // (in wave order: a thread's slots follow the allowed ids of the
+      // waves and lanes before it)
+      unsigned off = wbase + wincl - nown;
       rv.each([&](int id, float y) { tl.E[off++] = Packed{y, id}; });
       __syncthreads();
       topp_rest(a, r, CompactView{tl.E, (int)nv}, tl, Mc, nv, ts, bs);
@@ -499,7 +590,7 @@ __global__ __launch_bounds__(BT) void topp_kernel(SampleArgs a) {
 size_t topp_lds_bytes(int V, int TS) {
   const int bw = TS > 0 ? (V + 31) / 32 : 0;
   return (size_t)((bw * 4 + 15) / 16) * 16 + (size_t)TS * 8 + (size_t)(3 * TOPP_CAP + 2) * 8 +
-         (size_t)(bucket::NB + 4) * 4 + (size_t)(bucket::NB + 1) * 8;
+         (size_t)(bucket::NB + 4) * 4 + (size_t)(bucket::NB + 1) * 8 + (size_t)(66 + 64 + 64) * 8;
 }
 
 int topp_pack_cap(int V, int TS, size_t lds_avail) {
