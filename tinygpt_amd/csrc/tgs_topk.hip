@@ -60,6 +60,7 @@ struct Scratch {
   unsigned red32[WT];
   unsigned nc;    // candidates written
   unsigned ng;    // bucket members gathered
+  unsigned na;    // collection: candidates appended
   unsigned need;  // bound: slots still needed below the histogram range
   int dsel;       // bound: histogram bin of the k'-th slot
   int sel[3];     // tail: buckets of the k-th, of the cut and of the draw
@@ -531,8 +532,6 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
                                          BlockScratch& bs, Regs<Tin, NVR>& g, const int (&hpre)[1]) {
   using RG = Regs<Tin, NVR>;
   constexpr int EPV = RG::EPV;
-  constexpr int NEL = NVR * EPV;       // ids per thread
-  constexpr int NW = (NEL + 31) / 32;  // candidate mask words per thread
   const int b = r.b;
   const int V = a.V;
   const int bw = a.TS > 0 ? (V + 31) / 32 : 0;
@@ -574,62 +573,61 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
   const float thz = tkey > kneg + 16u ? tg_unkey(tkey - 16u) : -__builtin_inff();
   const float thf = fmaxf(thz, -3.40282347e38f);  // -inf never qualifies
 
-  // collect: one bit per id at or above the bound (element el = j * EPV + e
-  // of this thread is bit 31 - (el & 31) of word el >> 5)
-  uint32_t mb[NW];
+  // collect: the vectors holding an id at or above the bound (bit j of vb:
+  // this thread's vector j), from packed maxima of the patterns held in
+  // registers; the per-id test runs afterwards on those vectors only, read
+  // again from memory.  bf16 x >= thf exactly on the 16-bit patterns: for
+  // thf > 0 a signed compare with ceil(thf bits / 2^16); otherwise (sign
+  // set, or +0) an unsigned compare with the truncated pattern (every
+  // non-negative pattern lies below it).  Masked-out ids and ids past the
+  // row end hold the all-ones pattern and never pass.
+  const uint32_t tb = tg_f2u(thf);
+  const bool pos = !(tb >> 31) && tb != 0u;
+  const int ts16 = (int)((tb + 0xFFFFu) >> 16);
+  const uint32_t tu16 = tb == 0u ? 0x8000u : (tb >> 16);
+  auto id_passes = [&](uint32_t w, int e) -> bool {  // element e of a vector word w (its word e / (EPV / 4))
+    if constexpr (sizeof(Tin) == 2) {
+      const uint32_t h = (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+      return pos ? ((int)(short)h >= ts16) : (h <= tu16);
+    } else {
+      return tg_u2f(w) >= thf;
+    }
+  };
+  uint32_t vb = 0;
   if constexpr (sizeof(Tin) == 2) {
-    // bf16 x >= thf exactly on the 16-bit patterns: for thf > 0 a signed
-    // compare with ceil(thf bits / 2^16); otherwise (sign set, or +0) an
-    // unsigned compare with the truncated pattern (every non-negative
-    // pattern lies below it)
-    const uint32_t tb = tg_f2u(thf);
-    const bool pos = !(tb >> 31) && tb != 0u;
-    const int ts16 = (int)((tb + 0xFFFFu) >> 16);
-    const uint32_t tu16 = tb == 0u ? 0x8000u : (tb >> 16);
+    if (pos) {
 #pragma unroll
-    for (int i = 0; i < NW; i++) {
-      uint32_t acc = 0;
-      if (pos) {
-#pragma unroll
-        for (int t = 0; t < 16; t++) {
-          const int wi = i * 16 + t;
-          const uint32_t x = word_of(g.raw[wi >> 2], wi & 3);
-          acc = acc * 2u + (uint32_t)((int)(short)(x & 0xFFFFu) >= ts16);
-          acc = acc * 2u + (uint32_t)(((int)x >> 16) >= ts16);
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 16; t++) {
-          const int wi = i * 16 + t;
-          const uint32_t x = word_of(g.raw[wi >> 2], wi & 3);
-          acc = acc * 2u + (uint32_t)((x & 0xFFFFu) <= tu16);
-          acc = acc * 2u + (uint32_t)((x >> 16) <= tu16);
-        }
+      for (int j = 0; j < NVR; j++) {
+        const uint4 v = g.raw[j];
+        const uint32_t mx = pk_max_i16(pk_max_i16(v.x, v.y), pk_max_i16(v.z, v.w));
+        const int lo = (int)(short)(mx & 0xFFFFu), hi = (int)mx >> 16;
+        vb |= ((hi > lo ? hi : lo) >= ts16 ? 1u : 0u) << j;
       }
-      mb[i] = acc;
+    } else {
+      // per-half unsigned minima: signed minima of the patterns with their
+      // top bits flipped
+      constexpr uint32_t F = 0x80008000u;
+#pragma unroll
+      for (int j = 0; j < NVR; j++) {
+        const uint4 v = g.raw[j];
+        const uint32_t mn = pk_min_i16(pk_min_i16(v.x ^ F, v.y ^ F), pk_min_i16(v.z ^ F, v.w ^ F)) ^ F;
+        const uint32_t lo = mn & 0xFFFFu, hi = mn >> 16;
+        vb |= ((lo < hi ? lo : hi) <= tu16 ? 1u : 0u) << j;
+      }
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < NW; i++) {
-      uint32_t acc = 0;
-#pragma unroll
-      for (int t = 0; t < 32; t++) {
-        const int el = i * 32 + t;
-        if (el < NEL) {
-          const int j = el / EPV, e = el % EPV;
-          acc = acc * 2u + (uint32_t)(tg_u2f(word_of(g.raw[j], e)) >= thf);
-        }
-      }
-      constexpr int last = NEL - (NW - 1) * 32;  // elements in the last word
-      mb[i] = (i == NW - 1 && last < 32) ? acc << (32 - last) : acc;
+    for (int j = 0; j < NVR; j++) {
+      const uint4 v = g.raw[j];
+      const bool p = tg_u2f(v.x) >= thf || tg_u2f(v.y) >= thf || tg_u2f(v.z) >= thf || tg_u2f(v.w) >= thf;
+      vb |= (p ? 1u : 0u) << j;
     }
   }
-  unsigned cnt = 0;
-#pragma unroll
-  for (int i = 0; i < NW; i++) cnt += __builtin_popcount(mb[i]);
+  const unsigned cnt = (unsigned)__builtin_popcount(vb);
   if (threadIdx.x == 0) {
     ts.nc = 0;
     ts.ng = 0;
+    ts.na = 0;
   }
   for (int i = threadIdx.x; i < NB + 1; i += BT) {
     CI[i] = 0u;
@@ -637,45 +635,58 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
   }
   __syncthreads();
   {
+    // the vectors' indexes in the row, in cid
     const unsigned wincl = wave_incl_scan(cnt);
     unsigned wbase = 0;
     if (lane_id() == 63 && wincl) wbase = atomicAdd(&ts.nc, wincl);
     wbase = __shfl(wbase, 63, 64);
     unsigned slot = wbase + wincl - cnt;
-#pragma unroll
-    for (int i = 0; i < NW; i++) {
-      uint32_t mw = mb[i];
-      while (mw) {
-        const int q = __builtin_clz(mw);
-        mw ^= 0x80000000u >> q;
-        const int el = i * 32 + q;
-        if (slot < (unsigned)CAPK) cid[slot] = (uint32_t)(RG::vec_id(el / EPV) + el % EPV);
-        slot++;
-      }
+    uint32_t m = vb;
+    while (m) {
+      const int j = __builtin_ctz(m);
+      m &= m - 1u;
+      if (slot < (unsigned)CAPK) cid[slot] = (uint32_t)((int)threadIdx.x + j * BT);
+      slot++;
     }
   }
   __syncthreads();
-  const unsigned ncb = ts.nc;  // ids at or above the bound
-  if (ncb <= (unsigned)CAPK) {
-    // their composites (history ids skipped: added below with their
-    // penalised logits), read again from memory
-    uint32_t id[CPT];
-    float x[CPT];
+  const unsigned ncv = ts.nc;  // vectors holding an id at or above the bound
+  unsigned ncb = (unsigned)CAPK + 1u;  // candidates in cand[0, ncb) (beyond CAPK: overflow)
+  if (ncv <= (unsigned)CAPK) {
+    // each vector read again from memory (with its mask word); its ids that
+    // pass (history ids: composite 0, added below with their penalised
+    // logits) into cand by a wave-aggregated append
 #pragma unroll
-    for (int j = 0; j < CPT; j++) {
-      const int i = threadIdx.x + j * BT;
-      id[j] = i < (int)ncb ? cid[i] : 0u;
-    }
+    for (int q = 0; q < CPT; q++) {
+      if (q * BT >= (int)ncv) break;  // (uniform)
+      const int i = (int)threadIdx.x + q * BT;
+      const bool act = i < (int)ncv;
+      const int vid = act ? (int)cid[i] * EPV : 0;
+      const uint4 v = *(const uint4*)(rowp + vid);
+      const uint32_t mw = (MASK && r.mrow != nullptr) ? r.mrow[vid >> 5] >> (vid & 31) : 0xFFFFFFFFu;
+      uint32_t on = 0;
 #pragma unroll
-    for (int j = 0; j < CPT; j++) x[j] = Elem<Tin>::scalar(rowp, id[j]);
-#pragma unroll
-    for (int j = 0; j < CPT; j++) {
-      const int i = threadIdx.x + j * BT;
-      if (i < (int)ncb) {
-        const bool hist = r.use_pen && hist_bit(hbits, (int)id[j]);
-        cand[i] = hist ? 0ull : comp_of(x[j], true, r, (int)id[j]);
+      for (int e = 0; e < EPV; e++)
+        on |= (act && ((mw >> e) & 1u) && id_passes(word_of(v, e / (EPV / 4)), e) ? 1u : 0u) << e;
+      const unsigned c = (unsigned)__builtin_popcount(on);
+      const unsigned incl = wave_incl_scan(c);
+      const unsigned tot = readlane_u32(incl, 63);
+      unsigned base = 0;
+      if (lane_id() == 63 && tot) base = atomicAdd(&ts.na, tot);
+      unsigned sl = readlane_u32(base, 63) + incl - c;
+      while (on) {
+        const int e = __builtin_ctz(on);
+        on &= on - 1u;
+        const int id = vid + e;
+        const u64 x = (r.use_pen && hist_bit(hbits, id)) ? 0ull : comp_of(Elem<Tin>::get(v, e), true, r, id);
+        if (sl < (unsigned)CAPK) cand[sl] = x;
+        sl++;
       }
     }
+    __syncthreads();
+    ncb = ts.na;
+  }
+  if (ncb <= (unsigned)CAPK) {
     if (r.use_pen) {
       for (int i = threadIdx.x; i < a.TS; i += BT) {
         const int2 h = hash[i];
@@ -691,7 +702,7 @@ __device__ __forceinline__ void topk_row(const SampleArgs& a, Row& r, unsigned c
     }
   }
   __syncthreads();
-  int nc = (int)(ts.nc + ts.ng);  // ts.ng is cleared in the tail, past its first barrier
+  int nc = (int)(ncb + ts.ng);  // ts.ng is cleared in the tail, past its first barrier
   if (nc > CAPK) {
     // candidate overflow: radix selection over every id of the row, read
     // again from L2 / MALL (rare: massive ties at the bound); the kept set
