@@ -19,12 +19,13 @@
 //           Temperature is applied after the bound: 16 representable values
 //           of slack keep every id whose scaled logit could round to the
 //           bound's.
-//   collect one compare per id (16-bit compares on the raw bf16 halves)
-//           shifted into per-thread bit masks; the set bits become ids in LDS
-//           (block offsets from a wave scan); their logits are read again (a
-//           scattered gather) and turned into composites (logit desc, id
-//           asc), history ids skipped there and added with their penalised
-//           logits instead.
+//   collect one test per vector (a packed 16-bit maximum of its bf16
+//           patterns against the bound) into a per-thread bit mask; the
+//           passing vectors' indexes go to LDS (block offsets from a wave
+//           scan); each is read again (16 bytes, a scattered gather), its
+//           ids tested one by one, and the passing ids turned into
+//           composites (logit desc, id asc), history ids skipped there and
+//           added with their penalised logits instead.
 //   tail    over the candidates (at most 4096, four per thread): the maximum
 //           m, then a count and exact-mass histogram over 1024 buckets of
 //           width 1/32 below m (y - m <= -32, mass 0, in one more bucket).
