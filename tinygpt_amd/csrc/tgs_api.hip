@@ -223,7 +223,10 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
     a.ws_stride = 64;
     const size_t lds = (size_t)a.off_cand + (size_t)(tgs::K64_CAP + 16) * 8;
     if (lds + kK64Static > res.lds_limit) return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS");
-    hipError_t e = tgs::launch_k64(a, dt, lds, stream);
+    // a row in one chunk that one wave holds: the one-wave variant (its
+    // barriers and merges involve a single wave)
+    const bool small = a.S == 1 && V <= tgs::k64_small_ids(dt) && hist_cap <= tgs::K64_SMALL_MAX_HIST;
+    hipError_t e = tgs::launch_k64(a, dt, lds, stream, small);
     if (e != hipSuccess) return efail(err, TGS_EHIP, std::string("sample kernel launch: ") + hipGetErrorString(e));
     return TGS_OK;
   }

@@ -62,7 +62,8 @@ struct Geo {
   static constexpr int EPV = Elem<Tin>::EPV;
   static constexpr int NW = NTT / 64;
   static constexpr int CH = NTT * NVT * EPV;  // ids of a chunk at most
-  static constexpr int NHID = (K64_MAX_HIST + NTT - 1) / NTT;  // history ids per thread
+  static constexpr int MAXH = NTT >= K64_NT ? K64_MAX_HIST : K64_SMALL_MAX_HIST;  // longest history
+  static constexpr int NHID = (MAXH + NTT - 1) / NTT;  // history ids per thread
   static constexpr uint32_t GM = (1u << EPV) - 1u;
 };
 
@@ -657,7 +658,11 @@ hipError_t set_lds(size_t bytes) {
 
 int k64_chunk_ids(int dtype) { return K64_NT * K64_NVT * (dtype == 1 ? 8 : 4); }
 
-hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {
+int k64_small_ids(int dtype) { return K64_SMALL_NT * K64_NVT * (dtype == 1 ? 8 : 4); }
+
+hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st, bool small) {
+  if (small)
+    return dtype == 1 ? k64::launch_n<uint16_t, K64_SMALL_NT>(a, lds, st) : k64::launch_n<float, K64_SMALL_NT>(a, lds, st);
   return dtype == 1 ? k64::launch_n<uint16_t, K64_NT>(a, lds, st) : k64::launch_n<float, K64_NT>(a, lds, st);
 }
 
@@ -665,6 +670,8 @@ hipError_t set_k64_lds_limit(size_t bytes) {
   hipError_t e = hipSuccess, e2;
   if ((e2 = k64::set_lds<float, K64_NT>(bytes)) != hipSuccess) e = e2;
   if ((e2 = k64::set_lds<uint16_t, K64_NT>(bytes)) != hipSuccess) e = e2;
+  if ((e2 = k64::set_lds<float, K64_SMALL_NT>(bytes)) != hipSuccess) e = e2;
+  if ((e2 = k64::set_lds<uint16_t, K64_SMALL_NT>(bytes)) != hipSuccess) e = e2;
   return e;
 }
 

@@ -16,6 +16,8 @@ namespace tgs {
 constexpr int K64_NT = 256;
 constexpr int K64_NVT = 16;
 constexpr int K64_MAX_HIST = 1024;
+constexpr int K64_SMALL_NT = 64;        // one-wave variant for rows of one small chunk
+constexpr int K64_SMALL_MAX_HIST = 256;  // its longest history
 constexpr int K64_CAP = 2048;
 constexpr int K64_MAX_SPLIT = 16;
 constexpr int K64_CNT_STRIDE = 32;
@@ -146,7 +148,10 @@ hipError_t set_sample_lds_limit(size_t bytes);
 // The fused kernel for batches of greedy rows and rows with top_k <= 64:
 // K64_NT threads per workgroup, chunks of at most k64_chunk_ids(dtype) ids.
 int k64_chunk_ids(int dtype);
-hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st);
+// small: the one-wave variant (K64_SMALL_NT threads, one chunk per row of at
+// most k64_small_ids(dtype) ids, history <= K64_SMALL_MAX_HIST).
+int k64_small_ids(int dtype);
+hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st, bool small = false);
 hipError_t set_k64_lds_limit(size_t bytes);
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
 // Rows sampling top-p over the whole vocabulary (top_k disabled).
