@@ -765,7 +765,7 @@ TRAFFIC_FILES["lp"] = "lp_scoring_traffic.json"
 TRAFFIC_FILES["c2m"] = "k64_kernel_c2m_traffic.json"
 TRAFFIC_FILES["json"] = "json_rows_traffic.json"
 TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
-KERNELS = {"c1": "k64_kernel<float>", "c2": "k64_kernel<float>", "c2m": "k64_kernel<float> (mask variant)",
+KERNELS = {"c1": "k64_kernel<float> (one-wave)", "c2": "k64_kernel<float>", "c2m": "k64_kernel<float> (mask variant)",
            "c3": "topp_kernel<float, true>",
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
