@@ -3,7 +3,8 @@
 //
 // Workgroup (b, c) of K64_NT threads owns chunk c of row b: S chunks per
 // row, each at most K64_NT * K64_NVT sixteen-byte vectors (thread t holding
-// chunk vectors t, t + K64_NT, ...).  Everything a thread reads is requested
+// chunk vectors t, t + K64_NT, ...).  Rows that fit one chunk of
+// K64_SMALL_NT threads (one wave) run on that instantiation instead.  Everything a thread reads is requested
 // at entry: the row's parameters, its history ids, its vectors and (with a
 // mask table) their mask words, so the whole chunk is in flight at once.
 // Under a full-chip stream the chunk's data lands in one burst near the end
