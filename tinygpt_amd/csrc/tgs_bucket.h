@@ -175,5 +175,43 @@ __device__ __forceinline__ int first_rank(const u64* Q, unsigned n, u64 target, 
   return f;
 }
 
+// One wave ranks L[0, n) (n <= 64) into R (descending) and Q (inclusive
+// masses under m); no barrier.
+__device__ __forceinline__ void wave_rank64(const u64* L, unsigned n, float m, u64* R, u64* Q) {
+  const int lane = lane_id();
+  u64 x = lane < (int)n ? L[lane] : 0ull;
+  x = wave_sort_desc(x);
+  const u64 q = lane < (int)n ? mass_c(x, m) : 0ull;
+  const u64 ci = wave_incl_scan(q);
+  if (lane < (int)n) {
+    R[lane] = x;
+    Q[lane] = ci;
+  }
+}
+
+// The buckets whose inclusive masses first reach t1 and t2 (both in
+// [1, MI[NB - 1]]), in one pass and one barrier.
+template <int BT>
+__device__ __forceinline__ void find_mass2(const u64* MI, u64 t1, u64 t2, int* s1, int* s2) {
+  constexpr int PER = NB / BT;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int t = threadIdx.x * PER + i;
+    const u64 lo = t ? MI[t - 1] : 0ull, hi = MI[t];
+    if (hi >= t1 && lo < t1) *s1 = t;
+    if (hi >= t2 && lo < t2) *s2 = t;
+  }
+  __syncthreads();
+}
+
+// First rank of a ranked list whose inclusive mass reaches target (>= 1, at
+// most Q[n - 1]); one barrier, so each call needs a slot of its own.
+__device__ __forceinline__ int first_rank_once(const u64* Q, unsigned n, u64 target, int* slot) {
+  const int i = threadIdx.x;
+  if (i < (int)n && Q[i] >= target && (i == 0 || Q[i - 1] < target)) *slot = i;
+  __syncthreads();
+  return *slot;
+}
+
 }  // namespace bucket
 }  // namespace tgs

@@ -66,6 +66,8 @@ struct Scratch {
   int dsel;       // bound: histogram bin of the k'-th slot
   int sel[3];     // tail: buckets of the k-th, of the cut and of the draw
   int first;      // tail: first rank meeting a mass target
+  unsigned ng2;   // tail: members of the draw's bucket gathered with the cut's
+  int first2;     // tail: the draw's rank in the one-gather tail
 };
 
 template <typename T>
@@ -329,7 +331,13 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
   mx = wave_max(mx);
   if (lane == 0) ts.red64[w] = mx;
   __syncthreads();
-  if (threadIdx.x == 0) ts.ng = 0;  // every thread has read the candidate count
+  if (threadIdx.x == 0) {
+    ts.ng = 0;  // every thread has read the candidate count
+    ts.ng2 = 0;
+  }
+  u64* L2 = MI + NB + 1;  // the draw's bucket when gathered with the cut's: 64 (+ pad)
+  u64* R2 = L2 + 66;      // 64
+  u64* Q2 = R2 + 64;      // 64
   u64 M = ts.red64[0];
 #pragma unroll
   for (int i = 1; i < WT; i++) M = ts.red64[i] > M ? ts.red64[i] : M;
@@ -453,8 +461,10 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
     S = mex(bk) + mb;
   }
   // top-p: the cut, the first element whose inclusive prefix reaches P
+  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
   unsigned istar;
-  u64 Sp, cutc = 0;
+  u64 Sp, cutc = 0, pick = 0;
+  bool drawn = false;  // the draw resolved with the cut
   if (r.top_p < 1.0f) {
     const uint32_t pq = (uint32_t)(r.top_p * 16777216.0f);
     const u64 P = mul_shr24(S, pq);
@@ -463,12 +473,54 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
       cutc = M;
       Sp = tg_q40(1.0f);
     } else {
-      const int bp = find_mass(P, 1);
-      u64 before;
-      unsigned rank;
-      cutc = resolve_mass(bp, P - mex(bp), &before, &rank);
-      istar = cex(bp) + rank;
-      Sp = mex(bp) + before + bucket::mass_c(cutc, m);
+      // The draw's bucket while the cut is open: S' lies in [P, MI[bp]] (the
+      // cut's inclusive prefix reaches P and ends in bucket bp), so t lies in
+      // [floor(P u24 / 2^24), floor(MI[bp] u24 / 2^24)]; when one bucket holds
+      // every draw target of that range, the cut's and the draw's buckets are
+      // gathered in one pass over the candidates and ranked side by side.
+      const u64 tlo = mul_shr24(P, uq);
+      bucket::find_mass2<BT>(MI, P, tlo + 1, &ts.sel[1], &ts.sel[2]);
+      const int bp = ts.sel[1], btl = ts.sel[2];
+      const unsigned na = CI[bp] - cex(bp);
+      const unsigned nb2 = btl != bp ? CI[btl] - cex(btl) : 0u;
+      const bool one = MI[btl] >= mul_shr24(MI[bp], uq) + 1 && nb2 <= 64u && (rb == bp || na <= (unsigned)LCAP);
+      if (one) {
+        const bool gather_a = rb != bp;  // the cut's bucket not ranked yet
+        const int bb = btl != bp ? btl : -1;
+        if (gather_a && threadIdx.x == 0 && (na & 1)) L[na] = 0ull;  // pad below every composite
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+          if (gather_a && cd.bk[j] == bp) L[atomicAdd(&ts.ng, 1u)] = cd.c[j];
+          else if (bb >= 0 && cd.bk[j] == bb) L2[atomicAdd(&ts.ng2, 1u)] = cd.c[j];  // (bk -1: no candidate)
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          ts.ng = 0;  // read again only after the barriers below
+          ts.ng2 = 0;
+        }
+        if (bb >= 0 && w == 1) bucket::wave_rank64(L2, nb2, m, R2, Q2);
+        if (gather_a) {
+          bucket::rank_list<BT>(L, na, m, R, Q, ts.red64b);  // ends with a barrier
+          rb = bp;
+          rn = na;
+        } else {
+          __syncthreads();
+        }
+        const int i = bucket::first_rank_once(Q, rn, P - mex(bp), &ts.first);
+        cutc = R[i];
+        istar = cex(bp) + (unsigned)i;
+        Sp = mex(bp) + (i > 0 ? Q[i - 1] : 0ull) + bucket::mass_c(cutc, m);
+        const u64 tb = mul_shr24(Sp, uq) + 1 - mex(btl);
+        pick = bb >= 0 ? R2[bucket::first_rank_once(Q2, nb2, tb, &ts.first2)]
+                       : R[bucket::first_rank_once(Q, rn, tb, &ts.first2)];
+        drawn = true;
+      } else {
+        u64 before;
+        unsigned rank;
+        cutc = resolve_mass(bp, P - mex(bp), &before, &rank);
+        istar = cex(bp) + rank;
+        Sp = mex(bp) + before + bucket::mass_c(cutc, m);
+      }
     }
   } else {
     istar = nk - 1;
@@ -482,12 +534,13 @@ __device__ __forceinline__ void tail(const SampleArgs& a, const Row& r, int nc, 
     }
   }
   // the draw: the first element whose inclusive prefix exceeds t
-  const uint32_t uq = (uint32_t)(r.u * 16777216.0f);
-  const u64 t = mul_shr24(Sp, uq);
-  const int bt = find_mass(t + 1, 2);
-  u64 before;
-  unsigned rank;
-  const u64 pick = resolve_mass(bt, t + 1 - mex(bt), &before, &rank);
+  if (!drawn) {
+    const u64 t = mul_shr24(Sp, uq);
+    const int bt = find_mass(t + 1, 2);
+    u64 before;
+    unsigned rank;
+    pick = resolve_mass(bt, t + 1 - mex(bt), &before, &rank);
+  }
   if (threadIdx.x == 0) {
     a.out[b] = comp_id(pick);
     write_row_diag(a, b, (int)nk, (int)istar + 1, S, Sp, comp_id(cutc));
@@ -816,7 +869,7 @@ int topk_max_vocab(int dtype) { return topk::BT * 20 * (dtype == 1 ? 8 : 4); }
 size_t topk_lds_bytes(int V, int TS) {
   const int bw = TS > 0 ? (V + 31) / 32 : 0;
   return (size_t)((bw * 4 + 15) / 16) * 16 + (size_t)TS * 8 + (size_t)(TOPK_CAP + 3 * topk::LCAP + 2) * 8 +
-         (size_t)(topk::NB + 4) * 4 + (size_t)(topk::NB + 1) * 8;
+         (size_t)(topk::NB + 4) * 4 + (size_t)(topk::NB + 1) * 8 + (size_t)(66 + 64 + 64) * 8;
 }
 
 hipError_t launch_topk(const SampleArgs& a, int dtype, size_t lds, hipStream_t st) {

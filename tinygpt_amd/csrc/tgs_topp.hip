@@ -253,43 +253,6 @@ struct Tail {
   unsigned rn = 0;
 };
 
-// One wave ranks L[0, n) (n <= 64) into R (descending) and Q (inclusive
-// masses under m); no barrier.
-__device__ __forceinline__ void wave_rank64(const u64* L, unsigned n, float m, u64* R, u64* Q) {
-  const int lane = lane_id();
-  u64 x = lane < (int)n ? L[lane] : 0ull;
-  x = wave_sort_desc(x);
-  const u64 q = lane < (int)n ? bucket::mass_c(x, m) : 0ull;
-  const u64 ci = wave_incl_scan(q);
-  if (lane < (int)n) {
-    R[lane] = x;
-    Q[lane] = ci;
-  }
-}
-
-// The buckets whose inclusive masses first reach t1 and t2 (both in
-// [1, MI[NB - 1]]), in one pass and one barrier.
-__device__ __forceinline__ void find_mass2(const u64* MI, u64 t1, u64 t2, int* s1, int* s2) {
-  constexpr int PER = NB / BT;
-#pragma unroll
-  for (int i = 0; i < PER; i++) {
-    const int t = threadIdx.x * PER + i;
-    const u64 lo = t ? MI[t - 1] : 0ull, hi = MI[t];
-    if (hi >= t1 && lo < t1) *s1 = t;
-    if (hi >= t2 && lo < t2) *s2 = t;
-  }
-  __syncthreads();
-}
-
-// First rank of a ranked list whose inclusive mass reaches target (>= 1, at
-// most Q[n - 1]); one barrier, so each call needs a slot of its own.
-__device__ __forceinline__ int first_rank_once(const u64* Q, unsigned n, u64 target, int* slot) {
-  const int i = threadIdx.x;
-  if (i < (int)n && Q[i] >= target && (i == 0 || Q[i - 1] < target)) *slot = i;
-  __syncthreads();
-  return *slot;
-}
-
 // The element of bucket bq whose within-bucket inclusive prefix first
 // reaches target (>= 1): its composite, the mass ahead of it in the bucket
 // and its rank there.  The bucket's members are gathered from the row and
@@ -380,7 +343,7 @@ __device__ __forceinline__ void topp_rest(const SampleArgs& a, const Row& r, con
     ts.ng = 0;
     ts.ng2 = 0;
   }
-  find_mass2(tl.MI, cut_search ? P : tlo + 1, tlo + 1, &ts.sel[0], &ts.sel[1]);
+  bucket::find_mass2<BT>(tl.MI, cut_search ? P : tlo + 1, tlo + 1, &ts.sel[0], &ts.sel[1]);
   const int bp = ts.sel[0], btl = ts.sel[1];
   const int ba = cut_search ? bp : btl;               // list A: the cut's bucket (else the draw's)
   const int bb = (cut_search && btl != bp) ? btl : -1;  // list B: the draw's bucket when it differs
@@ -397,23 +360,23 @@ __device__ __forceinline__ void topp_rest(const SampleArgs& a, const Row& r, con
       else if (q == bb) tl.L2[atomicAdd(&ts.ng2, 1u)] = comp_key(tg_key(y), id);
     });
     __syncthreads();
-    if (bb >= 0 && (threadIdx.x >> 6) == 1) wave_rank64(tl.L2, nb2, m, tl.R2, tl.Q2);
+    if (bb >= 0 && (threadIdx.x >> 6) == 1) bucket::wave_rank64(tl.L2, nb2, m, tl.R2, tl.Q2);
     if (na > 64u) {
       bucket::rank_list<BT>(tl.L, na, m, tl.R, tl.Q, ts.red64b);  // ends with a barrier
     } else {
-      if ((threadIdx.x >> 6) == 0) wave_rank64(tl.L, na, m, tl.R, tl.Q);
+      if ((threadIdx.x >> 6) == 0) bucket::wave_rank64(tl.L, na, m, tl.R, tl.Q);
       __syncthreads();
     }
     if (cut_search) {
-      const int i = first_rank_once(tl.Q, na, P - bucket::mass_before(tl.MI, bp), &ts.first);
+      const int i = bucket::first_rank_once(tl.Q, na, P - bucket::mass_before(tl.MI, bp), &ts.first);
       cutc = tl.R[i];
       Sp = bucket::mass_before(tl.MI, bp) + (i > 0 ? tl.Q[i - 1] : 0ull) + bucket::mass_c(cutc, m);
       ntopp = bucket::count_before(tl.CI, bp) + (unsigned)i + 1u;
     }
     const u64 t = mul_shr24(Sp, uq);
     const u64 tb = t + 1 - bucket::mass_before(tl.MI, btl);
-    if (bb >= 0) pick = tl.R2[first_rank_once(tl.Q2, nb2, tb, &ts.first2)];
-    else pick = tl.R[first_rank_once(tl.Q, na, tb, &ts.first2)];
+    if (bb >= 0) pick = tl.R2[bucket::first_rank_once(tl.Q2, nb2, tb, &ts.first2)];
+    else pick = tl.R[bucket::first_rank_once(tl.Q, na, tb, &ts.first2)];
   } else {
     if (cut_search) {
       u64 before;
