@@ -33,6 +33,8 @@
 //           buckets find the bucket of the k-th composite, of the top-p cut
 //           and of the draw; only those buckets are ranked (a wave sort of
 //           at most 64, else counting ranks) to place the element inside.
+//           The cut's and the draw's buckets share one gather when the
+//           draw's bucket is fixed before the cut is resolved.
 //
 // A candidate list beyond its capacity (massive ties at the bound) falls
 // back to a radix selection over all ids of the row, read again from
