@@ -175,6 +175,38 @@ def test_random_rows_masked(sampler, oracle, V):
     _check(sampler, oracle, f"masked V={V}", x, params, u, hist, hist_len, mask_table=table, kept_cap=1025)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("kmax", [64, 1024])
+def test_specialised_kernels_masked(sampler, oracle, bf16, kmax):
+    """The batch-hint kernels with a grammar mask: the one-wave k64 instantiation
+    (kmax 64, rows of one 64-thread chunk) and the register-resident top-k kernel
+    (kmax 1024: its per-vector candidate test, masked ids as all-ones patterns,
+    negative bounds from shifted rows), against the oracle bit for bit."""
+    from tinygpt_amd import workloads as W
+
+    V = 4000 if kmax == 64 else 40000
+    g = np.random.default_rng(950 + kmax + (1 if bf16 else 0))
+    B = 40
+    x, params, u, hist, hist_len = _random_batch(g, B, V, oracle)
+    x[::4] -= 40.0  # every fourth row negative: bounds below zero
+    ks = np.array([1, 5, 40, 64, 65, 257, 1000])
+    ks = ks[(ks <= kmax) & (ks < V)]
+    params["top_k"] = g.choice(ks, size=B)
+    n_states = 5
+    words = (V + 31) // 32
+    table = g.integers(0, 1 << 32, size=(n_states, words), dtype=np.uint64).astype(np.uint32)
+    table[1] &= np.uint32(0x01010101)  # sparse
+    table[2] = 0                       # nothing allowed
+    table[3] = 0xFFFFFFFF              # everything allowed
+    table[4] = 0
+    table[4, 7] = 1 << 3               # one id
+    params["mask_state"] = g.integers(-1, n_states, size=B)
+    if bf16:
+        x = W.f32_to_bf16_bits(x)
+    _check(sampler, oracle, f"specialised masked V={V} kmax={kmax} bf16={bf16}", x, params, u, hist, hist_len,
+           mask_table=table, kept_cap=1025, hint="auto")
+
+
 def test_invalid_rows(sampler, oracle):
     V, B = 300, 12
     g = np.random.default_rng(77)
