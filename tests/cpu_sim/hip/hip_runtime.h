@@ -45,6 +45,9 @@ struct dim3 {
 struct uint4 {
   uint32_t x, y, z, w;
 };
+struct uint2 {
+  uint32_t x, y;
+};
 struct int2 {
   int x, y;
 };

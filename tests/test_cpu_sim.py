@@ -159,6 +159,19 @@ def test_noalloc_entry_point(sim, oracle, path):
         _check(sim, oracle, x, params, u, hist, hist_len, mask=mask, split=2, noalloc=True)
 
 
+@pytest.mark.parametrize("split", [1, 3])
+def test_k64_history_at_top(sim, oracle, split):
+    """Rows whose largest logits are penalised history ids, small top_k: the
+    chunk bounds come from the other ids."""
+    import tinygpt_amd as tg
+    from test_gpu_sampler import _history_at_top_batch
+
+    g = np.random.default_rng(47 + split)
+    V = 12000
+    x, params, u, hist, hist_len = _history_at_top_batch(g, 6, V, oracle, H_=256)
+    _check(sim, oracle, x, params, u, hist, hist_len, hint=tg.batch_hint(params, V), split=split, kept_cap=64)
+
+
 def test_k64_bf16_and_mask(sim, oracle):
     import tinygpt_amd as tg
     from tinygpt_amd import workloads as W

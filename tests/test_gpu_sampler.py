@@ -114,6 +114,43 @@ def _random_batch(g, B, V, oracle):
     return x, params, u, hist, hist_len
 
 
+def _history_at_top_batch(g, B, V, oracle, H_=512):
+    """Rows whose history holds their largest logits (a model repeating
+    itself): half of each row's history is its top H_/2 ids, the rest random
+    ids, with penalties strong enough to move those ids below the rest of the
+    top; top_k small, so the ids that decide each chunk's bound are history
+    ids."""
+    x = (g.standard_normal((B, V)) * 2.0).astype(np.float32)
+    params = oracle.make_params(B)
+    params["temperature"][:] = g.choice([0.3, 0.7, 1.0, 1.5], size=B)
+    params["top_k"][:] = g.choice([1, 2, 4, 8, 16, 50, 64], size=B)
+    params["top_p"][:] = g.choice([1.0, 0.9], size=B)
+    params["repetition"][:] = g.choice([1.0, 1.3], size=B)
+    params["presence"][:] = g.choice([0.0, 3.0], size=B)
+    params["frequency"][:] = g.choice([0.5, 2.0], size=B)
+    hist = g.integers(0, V, size=(B, H_)).astype(np.int32)
+    top = np.argsort(-x, axis=1)[:, :H_ // 2].astype(np.int32)
+    hist[:, 0::2] = top
+    hist_len = np.full(B, H_, np.int32)
+    hist_len[::5] = H_ // 3
+    u = (g.integers(0, 1 << 24, size=B) / (1 << 24)).astype(np.float32)
+    return x, params, u, hist, hist_len
+
+
+@pytest.mark.parametrize("V", [5000, 128256])
+def test_k64_history_at_top(sampler, oracle, V):
+    """The top_k <= 64 kernel on rows whose largest logits are penalised
+    history ids (the chunk bounds come from the other ids), fp32 and bf16."""
+    from tinygpt_amd import workloads as W
+
+    g = np.random.default_rng(960 + V)
+    B = 64
+    x, params, u, hist, hist_len = _history_at_top_batch(g, B, V, oracle)
+    for name, xx in (("f32", x), ("bf16", W.f32_to_bf16_bits(x))):
+        _check(sampler, oracle, f"history at top V={V} {name}", xx, params, u, hist, hist_len, kept_cap=64,
+               hint="auto")
+
+
 _FAULTED_256 = pytest.mark.skip(
     reason="faulted the GPU once under an earlier kernel layout (calls from the chunk kernel into "
            "out-of-line device functions); no cause was shown in the CPU simulation under ASan, so "

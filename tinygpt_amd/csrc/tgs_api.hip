@@ -213,9 +213,10 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
     const int L = ((V + S - 1) / S + epv - 1) / epv * epv;  // whole vectors: chunk starts stay aligned
     a.S = (V + L - 1) / L;
     a.L = L;
-    // dynamic LDS: history hash, history bitmap of the chunk, candidate
-    // buffer (+16 pad entries for the ranking)
-    a.BW = (L + 31) / 32;
+    // dynamic LDS: history hash, history bits of the chunk (packed per
+    // thread: one bit per id of the largest chunk), candidate buffer (+16
+    // pad entries for the ranking)
+    a.BW = tgs::k64_chunk_ids(dt) / 32;
     a.off_hash = 0;
     a.off_bitmap = a.TS * 8;
     a.off_cand = (a.off_bitmap + a.BW * 4 + 15) / 16 * 16;

@@ -10,12 +10,16 @@
 // Under a full-chip stream the chunk's data lands in one burst near the end
 // of the stream, so the steps after it are kept short:
 //   1. Vector maxima and thread maxima of the raw logits (ids the mask
-//      forbids and ids past the chunk left out; history ids included).
-//   2. A bound: the larger of (the minimum over waves of the wave's
-//      ceil(k / waves)-th largest thread maximum) and (the maximum over
-//      waves of the wave's k-th largest), read from one wave sort each.  At
-//      least k distinct ids have a raw logit at or above it.  The collection
-//      threshold cz lies 16 representable values below it.
+//      forbids and ids past the chunk left out).
+//   2. A bound: for m = 1 .. waves, the m-th largest over waves of the
+//      wave's ceil(k / m)-th largest thread maximum qualifies (m waves hold
+//      that many at or above it each); the bound is the largest of them,
+//      read from one wave sort each.  In the sort a thread whose maximum
+//      lies in a vector holding a history id of the chunk (the bits are in
+//      LDS before the chunk lands) takes the lowest key, so at least k
+//      distinct ids that are neither masked nor history ids have a raw
+//      logit at or above the bound.  The collection threshold cz lies 16
+//      representable values below it.
 //   3. Every vector whose maximum reaches cz is staged whole in its wave's
 //      LDS list.
 //   4. One staged vector per lane: the canonical logit y = z / T of each
@@ -26,9 +30,12 @@
 //      also counts the candidates strictly above yc = cz / T.
 //   5. An id left out is not a history id and has z < cz, so its y is at
 //      most yc: with at least k candidates strictly above yc the chunk's top
-//      k are among the candidates and are ranked into wave 0.  Otherwise
-//      (ties, penalties that move the top ids, skewed chunks) an exact radix
-//      selection runs over the chunk read again from memory.
+//      k are among the candidates and are ranked into wave 0.  The ids
+//      behind the bound make that count at least k unless their quotients
+//      by T collide (a temperature so small that z / T overflows, say);
+//      then, and when a wave stages more vectors than its list holds (a
+//      skewed chunk), an exact radix selection runs over the chunk read
+//      again from memory.
 //
 // Rows split over S > 1 chunks.  Each workgroup counts itself in the row's
 // arrival counter at entry (a relaxed device atomic issued with the loads).
@@ -67,6 +74,44 @@ struct Geo {
   static constexpr int NHID = (MAXH + NTT - 1) / NTT;  // history ids per thread
   static constexpr uint32_t GM = (1u << EPV) - 1u;
 };
+
+// The chunk's history bits in LDS, packed per thread: the EPV bits of chunk
+// vector j (bit e for its element e) lie in the HPW words of thread
+// j mod NTT, at bit (j div NTT) * EPV, so that a thread reads the bits of
+// all its vectors with one load.
+template <typename Tin, int NTT>
+struct HBits {
+  static constexpr int EPV = Elem<Tin>::EPV;
+  static constexpr int HPW = NVT * EPV / 32;  // words per thread
+  static constexpr int WORDS = NTT * HPW;
+  static constexpr uint32_t GM = (1u << EPV) - 1u;
+  __device__ static int word(int j) { return (j % NTT) * HPW + (j / NTT) * EPV / 32; }
+  __device__ static int shift(int j) { return (j / NTT) * EPV % 32; }
+  __device__ static uint32_t of(const uint32_t* bits, int j) { return (bits[word(j)] >> shift(j)) & GM; }
+};
+
+// max over m = 1 .. NW of the m-th largest of wkey[m - 1][0, NW) (NW one or
+// four), in every lane: lanes 4 (m - 1) + i load wkey[m - 1][i], each group
+// of four lanes sorts itself descending (comparators (0,1) (2,3), (0,2)
+// (1,3), (1,2) as lane exchanges), and lane 5 (m - 1) then holds the m-th
+// largest of group m - 1.  The exchanges are DPP quad permutes.
+template <int NW>
+__device__ __forceinline__ uint32_t bound_key(const uint32_t (*wkey)[NW], int lane) {
+  static_assert(NW == 1 || NW == 4, "waves per workgroup");
+  if constexpr (NW == 1) {
+    return wkey[0][0];
+  } else {
+    const int pos = lane & 3;
+    uint32_t x = wkey[(lane >> 2) & 3][pos];
+    uint32_t y = xor_lane32<1>(x);
+    x = (pos & 1) ? min(x, y) : max(x, y);
+    y = xor_lane32<2>(x);
+    x = (pos & 2) ? min(x, y) : max(x, y);
+    y = __builtin_amdgcn_update_dpp(0u, x, 0x1B, 0xF, 0xF, false);  // quad_perm [3,2,1,0]: lane ^ 3
+    x = pos == 1 ? max(x, y) : pos == 2 ? min(x, y) : x;
+    return max(max(readlane_u32(x, 0), readlane_u32(x, 5)), max(readlane_u32(x, 10), readlane_u32(x, 15)));
+  }
+}
 
 struct alignas(16) u64x2 {
   u64 x, y;
@@ -227,8 +272,7 @@ __device__ __forceinline__ void each_allowed(const SampleArgs& a, const Row& r, 
   for (int j = threadIdx.x; j < nvec; j += NTT) {
     const int vid = r.v0 + j * EPV;
     const uint4 v = load_vec<Tin>(rowp, vid, r.v1, a.aligned);
-    const uint32_t o = (uint32_t)(j * EPV);
-    const uint32_t hw = pen ? bitmap[o >> 5] >> (o & 31) : 0u;
+    const uint32_t hw = pen ? HBits<Tin, NTT>::of(bitmap, j) : 0u;
     const uint32_t mwv = masked ? r.mrow[vid >> 5] >> (vid & 31) : 0xFFFFFFFFu;
 #pragma unroll
     for (int e = 0; e < EPV; e++) {
@@ -271,8 +315,7 @@ __device__ __forceinline__ void post_logits_chunk(const SampleArgs& a, const Row
   for (int j = threadIdx.x; j < nvec; j += NTT) {
     const int vid = r.v0 + j * EPV;
     const uint4 v = load_vec<Tin>(rowp, vid, r.v1, a.aligned);
-    const uint32_t o = (uint32_t)(j * EPV);
-    const uint32_t hw = pen ? bitmap[o >> 5] >> (o & 31) : 0u;
+    const uint32_t hw = pen ? HBits<Tin, NTT>::of(bitmap, j) : 0u;
     const uint32_t mwv = masked ? r.mrow[vid >> 5] >> (vid & 31) : 0xFFFFFFFFu;
 #pragma unroll
     for (int e = 0; e < EPV; e++) {
@@ -294,7 +337,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   __shared__ u64 slots[NW][64];      // wave lists (merges, the ranked top k)
   __shared__ uint4 svec[NW][SCAP];   // per wave: vectors whose maximum reaches the collection threshold
   __shared__ int sidx[NW][SCAP];     // their vector index in the chunk
-  __shared__ uint32_t wkey[2][NW];   // per wave: its ceil(k / NW)-th and k-th largest thread maximum keys
+  __shared__ uint32_t wkey[NW][NW];  // [m - 1][wave]: the wave's ceil(k / m)-th largest thread maximum key
   __shared__ unsigned nbuf;          // candidates appended (low 16 bits), of them above yc (high 16)
   __shared__ int elect, tmo, spill;
   __shared__ BlockScratch bs;
@@ -378,7 +421,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   const bool masked = MASK && r.mrow != nullptr;
 
   // ---- history: each id of the chunk counted in the LDS hash (its
-  // producer is the lane that created its slot) and marked in the bitmap
+  // producer is the lane that created its slot) and marked in the packed
+  // history bits (HBits)
   if (threadIdx.x == 0) {
     nbuf = 0;
     tmo = 0;
@@ -386,13 +430,15 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     elect = a.S > 1 && arrived == (unsigned)(a.S - 1);
   }
   const bool pen = r.use_pen;
-  const int bmw = (v1 - v0 + 31) >> 5;
+  using HB = HBits<Tin, NTT>;
+  constexpr int HPW = HB::HPW;
   int hslot[NHID];
 #pragma unroll
   for (int q = 0; q < NHID; q++) hslot[q] = -1;
   if (pen) {
     for (int i = threadIdx.x; i < a.TS; i += NTT) hash[i] = make_int2(-1, 0);
-    for (int i = threadIdx.x; i < bmw; i += NTT) bitmap[i] = 0u;
+#pragma unroll
+    for (int q = 0; q < HPW; q++) bitmap[threadIdx.x * HPW + q] = 0u;
     __syncthreads();
     const unsigned tmask = (unsigned)a.TS - 1u;
 #pragma unroll
@@ -409,11 +455,32 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
           }
           h = (h + 1) & tmask;
         }
-        atomicOr(&bitmap[(id - v0) >> 5], 1u << ((id - v0) & 31));
+        const int j = (id - v0) / EPV;
+        atomicOr(&bitmap[HB::word(j)], 1u << (HB::shift(j) + (id - v0) % EPV));
       }
     }
   }
   __syncthreads();
+  // the history bits of this thread's vectors (vector i at bit i * EPV), one
+  // load while the chunk is still in flight
+  uint32_t hpk[HPW];
+  if (pen) {
+    if constexpr (HPW == 2) {
+      const uint2 t = *(const uint2*)(bitmap + threadIdx.x * HPW);
+      hpk[0] = t.x;
+      hpk[1] = t.y;
+    } else {
+      static_assert(HPW == 4, "history words per thread");
+      const uint4 t = *(const uint4*)(bitmap + threadIdx.x * HPW);
+      hpk[0] = t.x;
+      hpk[1] = t.y;
+      hpk[2] = t.z;
+      hpk[3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < HPW; q++) hpk[q] = 0u;
+  }
   // producers' logits (and mask words): one load per history id of the
   // chunk, first needed after the bound
   float zq[NHID];
@@ -428,11 +495,12 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     }
   }
 
-  // ---- 1. vector maxima and thread maximum of the raw logits (history ids
-  // included: a bound from them is checked by counting below); ids the mask
-  // forbids and vectors past the chunk are left out
+  // ---- 1. vector maxima and thread maximum of the raw logits (ids the
+  // mask forbids and vectors past the chunk left out; history ids included)
+  // and the first vector that holds the thread maximum
   float vm[NVT];
   float tm = -__builtin_inff();
+  int im = 0;
 #pragma unroll
   for (int i = 0; i < NVT; i++) {
     float m;
@@ -448,33 +516,32 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     }
     if (i >= nfull) m = ((int)threadIdx.x + i * NTT < nvec) ? m : -__builtin_inff();  // vectors past the chunk
     vm[i] = m;
+    im = m > tm ? i : im;
     tm = fmaxf(tm, m);
   }
 
-  // ---- 2. the bound: at least k thread maxima (distinct ids) are >= it:
-  // the larger of (min over waves of the wave's ceil(k / NW)-th largest)
-  // and (max over waves of the wave's k-th largest), both read from one sort
+  // ---- 2. the bound: at least k thread maxima (distinct ids) are >= it.
+  // For m = 1 .. NW, the m-th largest over waves of the wave's ceil(k / m)-th
+  // largest key qualifies (m waves hold ceil(k / m) keys at or above it
+  // each); the bound is the largest of them, all read from one sort per
+  // wave.  A thread whose maximum lies in a vector holding a history id
+  // sorts as the lowest key, so every thread maximum behind the bound is an
+  // id that is not a history id.
   {
-    const uint32_t tk = tm > -__builtin_inff() ? tg_key(tm) : 0u;
+    uint32_t hw = hpk[0];
+#pragma unroll
+    for (int q = 1; q < HPW; q++) hw = im * EPV / 32 == q ? hpk[q] : hw;
+    const bool hmax = ((hw >> (im * EPV % 32)) & GM) != 0u;
+    const uint32_t tk = (tm > -__builtin_inff() && !hmax) ? tg_key(tm) : 0u;
     const uint32_t srt = wave_sort_desc(tk);  // lane i: the (i+1)-th largest
-    const uint32_t v1k = readlane_u32(srt, (k + NW - 1) / NW - 1);
-    const uint32_t v2k = readlane_u32(srt, k - 1);
-    if (lane == 0) {
-      wkey[0][w] = v1k;
-      wkey[1][w] = v2k;
+#pragma unroll
+    for (int m = 1; m <= NW; m++) {
+      const uint32_t v = readlane_u32(srt, (k + m - 1) / m - 1);
+      if (lane == 0) wkey[m - 1][w] = v;
     }
   }
   __syncthreads();
-  uint32_t bkey;
-  {
-    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
-#pragma unroll
-    for (int i = 0; i < NW; i++) {
-      lo = wkey[0][i] < lo ? wkey[0][i] : lo;
-      hi = wkey[1][i] > hi ? wkey[1][i] : hi;
-    }
-    bkey = lo > hi ? lo : hi;
-  }
+  const uint32_t bkey = bound_key<NW>(wkey, lane);
   // the collection threshold: 16 representable values below the bound, so
   // that the ids that set the bound land strictly above its canonical value
   const bool all = bkey < KEY_MIN + 32u;  // no usable bound: collect every allowed id
@@ -518,7 +585,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
         j = sidx[w][si];
       }
       const int o = j * EPV;
-      const uint32_t hw = (pen && si < nst) ? bitmap[o >> 5] >> (o & 31) : 0u;
+      const uint32_t hw = (pen && si < nst) ? HB::of(bitmap, j) : 0u;
       uint32_t xm = 0u;
       if constexpr (MASK) xm = (masked && si < nst) ? ~(r.mrow[(v0 + o) >> 5] >> ((v0 + o) & 31)) : 0u;
 #pragma unroll
@@ -560,8 +627,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   if (!spill && nb <= CAP && (all || nab >= k)) {
     acc = select_top<NTT>(buf, nb, k, slots);
   } else {
-    // exact path (rare: ties, skewed chunks, penalties that move the top
-    // ids): the k-th composite of the chunk by radix selection over the
+    // exact path (rare: quotients that collide, skewed chunks): the k-th
+    // composite of the chunk by radix selection over the
     // chunk read again (L2 / MALL hits), then the k entries at or above it
     acc = exact_top<Tin, NTT, MASK>(a, r, rowp, nvec, pen, bitmap, masked, hcomp, k, buf, &nbuf, slots, bs);
   }
