@@ -320,6 +320,8 @@ inline hipError_t hipDeviceGetAttribute(int* v, int attr, int) {
   return hipSuccess;
 }
 inline hipError_t hipFuncSetAttribute(const void*, int, int) { return hipSuccess; }
+template <class F>
+inline hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int* n, F, int, size_t) { *n = 8; return hipSuccess; }
 // A __device__ variable is a host variable here: its symbol is its address.
 #define HIP_SYMBOL(x) (&(x))
 inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {

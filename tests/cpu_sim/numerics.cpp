@@ -6,6 +6,9 @@
 //   numerics exp N seed   tg_expf_nonpos(x) == tg_expf(x), x <= 0, -inf, NaN
 //   numerics q40 N seed   (u64)tg_q40d(e) == tg_q40(e), e in [0, 1]
 //   numerics divt N seed  tg_div_t(z, T, 1/T) == z / T, any z, T > 0 with 1/T finite
+//   numerics q40exp N seed  tg_q40d_exp_nonpos(x) == tg_q40d(tg_expf_nonpos(x))
+//   numerics pow2fma N seed the mass of fma(z, rT, -m) == the mass of RN(z rT) - m,
+//                           T a power of two, m = RN(zmax rT) with zmax >= z
 // Prints the number of mismatches (and the first few).
 #include <hip/hip_runtime.h>
 
@@ -85,6 +88,67 @@ int main(int argc, char** argv) {
       if (i == 1) e = 1.0f;
       const u64 q1 = (u64)tg_q40d(e), q0 = tg_q40(e);
       if (q1 != q0) report("q40", e, 0, (double)q1, (double)q0);
+    }
+  } else if (mode == "q40exp") {
+    // x <= 0 (every non-positive bit pattern, uniform [-40, 0], the region
+    // around the -32 and -27.73 cut-offs, specials) and tiny positive x.
+    // NaNs are quiet: the kernels pass the result of a subtraction or a
+    // fused multiply-add, never a signalling NaN (for which the host's
+    // fmaxf returns NaN).
+    for (long long i = 0; i < N; i++) {
+      const uint64_t r = g();
+      float x;
+      switch (i & 3) {
+        case 0: {
+          uint32_t u = (uint32_t)r & 0x7FFFFFFFu;
+          if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu)) u |= 0x400000u;
+          x = -bits(u);
+          break;
+        }
+        case 1: x = -(float)((double)(r >> 11) * 0x1p-53 * 40.0); break;
+        case 2: x = -27.0f - (float)((double)(r >> 11) * 0x1p-53 * 6.0); break;
+        default: x = -(float)((double)(r >> 11) * 0x1p-53 * 2.0); break;
+      }
+      if (i == 0) x = -__builtin_inff();
+      if (i == 1) x = bits(0x7FC00000u);
+      if (i == 2) x = -0.0f;
+      if (i == 3) x = 0.0f;
+      if (i == 4) x = -32.0f;
+      if (i == 5) x = bits(1u);
+      if (i == 6) x = bits(0x00800000u);
+      const double q1 = tg_q40d_exp_nonpos(x), q0 = tg_q40d(tg_expf_nonpos(x));
+      if (q1 != q0) report("q40exp", x, 0, q1, q0);
+    }
+  } else if (mode == "pow2fma") {
+    // a power-of-two temperature: the mass of y - m with y = z rT and the
+    // maximum m = RN(zmax rT), zmax >= z, equals the mass of the fused
+    // fma(z, rT, -m) (z rT is exact there except below the normal range,
+    // where both differences round to the same weight)
+    for (long long i = 0; i < N; i++) {
+      const uint64_t r = g();
+      const int et = (int)((r >> 8) % 41) - 20;
+      const float T = bits((uint32_t)(127 + et) << 23);
+      const float rT = 1.0f / T;
+      const int ez = (int)(r % 300) - 150;
+      const uint32_t mz = (uint32_t)(r >> 16) & 0x7FFFFFu;
+      float z = (ez <= -127) ? bits(mz >> (uint32_t)(-126 - ez > 23 ? 23 : -126 - ez))
+                             : bits(((uint32_t)(127 + (ez > 127 ? 127 : ez)) << 23) | mz);
+      if ((r >> 62) & 1) z = -z;
+      float dz = bits(((uint32_t)(127 + (int)((r >> 40) % 40) - 30) << 23) | ((uint32_t)(r >> 20) & 0x7FFFFFu));
+      switch ((r >> 56) & 7) {
+        case 0: dz = 0.0f; break;
+        case 1: dz = bits((uint32_t)(r >> 30) & 0xFFu); break;  // a few denormal ulps
+        case 2: z = -__builtin_inff(); break;
+        case 3: z = bits(0x7FC00000u); break;
+        default: break;
+      }
+      const float zmax = (z == z && z > -__builtin_inff()) ? z + dz : 1.0f;
+      if (!(zmax >= z) && z == z && z > -__builtin_inff()) continue;
+      const float m = zmax * rT;
+      if (!__builtin_isfinite(m)) continue;
+      const double q1 = tg_q40d_exp_nonpos(__builtin_fmaf(z, rT, -m));
+      const double q0 = tg_q40d(tg_expf_nonpos(z * rT - m));
+      if (q1 != q0) report("pow2fma", z, T, q1, q0);
     }
   } else if (mode == "divt") {
     // z: every exponent of the fast range and beyond it, both signs, plus

@@ -344,13 +344,17 @@ def test_spec_invalid_rows(sim, oracle):
 
 
 @pytest.mark.parametrize("mode,n", [("div", 20_000_000), ("exp", 20_000_000), ("q40", 10_000_000),
-                                    ("divt", 40_000_000)])
+                                    ("divt", 40_000_000),
+                                    ("q40exp", 20_000_000), ("pow2fma", 20_000_000)])
 def test_device_shortcuts_equal_canonical_ops(sim, mode, n):
     """tg_div_t == IEEE z / T (the temperature divide, every mode, with zeros,
     infinities, NaN, denormals and huge logits among the inputs),
     tg_div_rcp == IEEE a / b (weights over softmax denominators),
-    tg_expf_nonpos == tg_expf on x <= 0 / -inf / NaN, and f64-summed
-    tg_q40d == tg_q40, on the device header compiled for the host."""
+    tg_expf_nonpos == tg_expf on x <= 0 / -inf / NaN, f64-summed
+    tg_q40d == tg_q40, the one-step mass tg_q40d_exp_nonpos == tg_q40d of
+    tg_expf_nonpos, and a power-of-two temperature's fused fma(z, rT, -m)
+    giving the same mass as z rT - m, on the device header compiled for the
+    host."""
     import subprocess
 
     r = subprocess.run([os.path.join(HERE, "cpu_sim", "build", "numerics"), mode, str(n), "12345"],

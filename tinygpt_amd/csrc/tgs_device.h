@@ -92,6 +92,39 @@ __device__ __forceinline__ float tg_expf_nonpos(float x_in) {
 // convert to the same u64 as summing tg_q40 terms.
 __device__ __forceinline__ double tg_q40d(float e) { return (double)__builtin_floorf(e * 0x1p40f); }
 
+// tg_q40d(tg_expf_nonpos(x)) bit for bit, in four operations fewer, for the
+// passes that sum a mass for every element:
+//   * the scaling by 2^40 joins the scaling by 2^n: e = p 2^n is exact for
+//     n >= -47, so e 2^40 = p 2^(n + 40), and n + 40 is read from the bits
+//     of s = t + 1.5 2^23, an integer in [2^23, 2^24) whose last mantissa
+//     bits are n (one integer subtraction instead of a conversion);
+//   * no final select: below -32 (and for -inf and NaN, which fmaxf maps to
+//     -32) the polynomial runs on -32, where e 2^40 = 0.014, and floor gives
+//     the same 0 as the select did (every x < -27.73 floors to 0).
+// Checked against the two-step form in tests/cpu_sim/numerics.cpp, mode q40exp.
+__device__ __forceinline__ double tg_q40d_exp_nonpos(float x_in) {
+  const float x = fmaxf(x_in, -32.0f);
+  const float log2e = 0x1.715476p+0f;
+  const float ln2_hi = 0x1.62ep-1f;
+  const float ln2_lo = 0x1.0bfbe8p-15f;
+  const float shifter = 12582912.0f;  // 1.5 2^23, bits 0x4B400000
+  const float t = x * log2e;
+  const float s = t + shifter;
+  const float n = s - shifter;
+  float r = __builtin_fmaf(n, -ln2_hi, x);
+  r = __builtin_fmaf(n, -ln2_lo, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int n40 = (int)(tg_f2u(s) - (0x4B400000u - 40u));
+  return (double)__builtin_floorf(__builtin_ldexpf(p, n40));
+}
+
 // a / b correctly rounded from rb = RN(1 / b): q = RN(a * rb) is within one
 // ulp of a / b, the residual a - b q is exact through a fused multiply-add,
 // and one correction q + (a - b q) rb rounds to RN(a / b) (Markstein's

@@ -42,7 +42,7 @@ namespace tgs {
 namespace spec {
 
 constexpr int WPB = NT / 64;  // waves per workgroup
-constexpr int K1_WG_PER_CU = 8;  // resident workgroups per CU of the block kernel's grid
+constexpr int K1_WG_PER_CU = 8;  // most resident workgroups per CU of the block kernel's grid
 
 template <typename Tin>
 struct Tile {
@@ -65,9 +65,17 @@ __device__ __forceinline__ const Tin* row_ptr(const SpecArgs& a, int b, int r) {
   return (const Tin*)a.draft + ((long long)b * k + (r - k - 1)) * a.V;
 }
 
+// A block wholly inside the row of an aligned row (every block but a row's
+// last when V is not a multiple of the block) takes plain 16-byte loads
+// behind one wave-uniform test; the others test each vector.
 template <typename Tin>
 __device__ __forceinline__ void load_block(const Tin* rowp, int blk, int V, bool aligned,
                                            uint4 (&raw)[Tile<Tin>::NV]) {
+  if (aligned && (blk + 1) * SPEC_BLOCK <= V) {
+#pragma unroll
+    for (int i = 0; i < Tile<Tin>::NV; i++) raw[i] = *(const uint4*)(rowp + blk_id<Tin>(blk, i, 0));
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < Tile<Tin>::NV; i++) raw[i] = load_vec<Tin>(rowp, blk_id<Tin>(blk, i, 0), V, aligned);
 }
@@ -76,12 +84,13 @@ __device__ __forceinline__ void load_block(const Tin* rowp, int blk, int V, bool
 // reciprocal and the mode of the exact divide (greedy: T = 1).  NaN T is
 // reported by the decide kernel.
 struct SeqT {
-  bool greedy;
+  bool greedy, tnan;
   float T, rT;
   int tdiv;
 };
 __device__ __forceinline__ SeqT seq_temp(float T) {
   SeqT s;
+  s.tnan = __builtin_isnan(T);
   s.greedy = !(T > 0.0f);
   const float Tc = T > 1e-5f ? T : 1e-5f;
   s.T = s.greedy ? 1.0f : Tc;
@@ -103,7 +112,8 @@ __device__ __forceinline__ float scaled(float z, const SeqT& st) {
 // live: computed (NaN T is reported by the decide kernel, greedy sequences
 // skip their draft rows).  A wave walks consecutive blocks and updates the
 // cursor incrementally (wave-uniform scalar arithmetic; the temperature is
-// re-read only when the sequence changes).
+// read only when the sequence changes, so that no load in the walk waits
+// for the blocks in flight).
 struct BlockRef {
   int b, r, blk;
   bool live, greedy;
@@ -115,7 +125,7 @@ __device__ __forceinline__ void block_ref_temp(const SpecArgs& a, BlockRef& x) {
   x.greedy = x.st.greedy;
 }
 __device__ __forceinline__ bool block_live(const SpecArgs& a, const BlockRef& x) {
-  return !__builtin_isnan(a.T[x.b]) && !(x.greedy && x.r > a.k);
+  return !x.st.tnan && !(x.greedy && x.r > a.k);
 }
 __device__ __forceinline__ BlockRef block_ref(const SpecArgs& a, int f) {
   const int R = 2 * a.k + 1;
@@ -164,30 +174,43 @@ __device__ __forceinline__ void block_stats(const SpecArgs& a, const BlockRef& x
     return;
   }
   // y = z / T; NaN and -inf never raise the maximum and weigh 0 (y - m is
-  // NaN or -inf there), so they need no mapping
-  float y[TL::EPL];
+  // NaN or -inf there), so they need no mapping.  With a power-of-two T
+  // (C5's T = 1) v holds the logits z themselves: y = z rT is monotone in
+  // z, so m = RN(max z rT), and the mass term of y - m is that of the fused
+  // fma(z, rT, -m) (z rT is exact, or below the normal range where both
+  // forms weigh the same; tests/cpu_sim/numerics.cpp, mode pow2fma).
+  const bool pow2 = x.st.tdiv == TDIV_POW2;
+  float v[TL::EPL];
   float mx = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < TL::NV; i++)
 #pragma unroll
     for (int e = 0; e < TL::EPV; e++) {
-      y[i * TL::EPV + e] = tg_div_t(Elem<Tin>::get(raw[i], e), x.st.T, x.st.rT, x.st.tdiv);
-      mx = fmaxf(mx, y[i * TL::EPV + e]);
+      const float z = Elem<Tin>::get(raw[i], e);
+      v[i * TL::EPV + e] = pow2 ? z : tg_div_t(z, x.st.T, x.st.rT, x.st.tdiv);
+      mx = fmaxf(mx, v[i * TL::EPV + e]);
     }
   mx = wave_maxf(mx);
+  if (pow2) mx = mx * x.st.rT;
   u64 q = 0;
   if (mx > -__builtin_inff() && mx < __builtin_inff()) {
     // y - m <= 0 (y == m gives +-0 and weight 1): the non-positive exp, and
     // exact masses summed per lane in f64
     double qd = 0.0;
+    if (pow2) {
 #pragma unroll
-    for (int j = 0; j < TL::EPL; j++) qd += tg_q40d(tg_expf_nonpos(y[j] - mx));
+      for (int j = 0; j < TL::EPL; j++) qd += tg_q40d_exp_nonpos(__builtin_fmaf(v[j], x.st.rT, -mx));
+    } else {
+#pragma unroll
+      for (int j = 0; j < TL::EPL; j++) qd += tg_q40d_exp_nonpos(v[j] - mx);
+    }
     q = (u64)qd;
   } else if (mx > -__builtin_inff()) {
     // a +inf logit in the block (weight(inf, inf) = 1, everything else 0)
 #pragma unroll
     for (int j = 0; j < TL::EPL; j++) {
-      const float yy = (y[j] > -__builtin_inff()) ? y[j] : -__builtin_inff();
+      const float y = pow2 ? v[j] * x.st.rT : v[j];
+      const float yy = (y > -__builtin_inff()) ? y : -__builtin_inff();
       if (yy > -__builtin_inff()) q += tg_q40(tg_weight(yy, mx));
     }
   }
@@ -662,8 +685,17 @@ __global__ __launch_bounds__(NT) void spec_draw_kernel(SpecArgs a) {
 
 template <typename Tin>
 hipError_t launch_t(const SpecArgs& a, hipStream_t st) {
+  // the block kernel's grid: as many workgroups per CU as its registers let
+  // stay resident (asked once per element type), at most K1_WG_PER_CU, so
+  // that every wave's run of blocks starts at once
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, spec_block_kernel<Tin>, NT, 0) != hipSuccess || n < 1) n = 1;
+    per_cu = std::min(n, K1_WG_PER_CU);
+  }
   const long long nblk = (long long)a.B * (2 * a.k + 1) * a.nb;
-  const long long g1 = std::min<long long>((nblk + WPB - 1) / WPB, (long long)a.ncu * K1_WG_PER_CU);
+  const long long g1 = std::min<long long>((nblk + WPB - 1) / WPB, (long long)a.ncu * per_cu);
   hipLaunchKernelGGL(spec_block_kernel<Tin>, dim3((unsigned)g1), dim3(NT), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
