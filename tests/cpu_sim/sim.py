@@ -25,6 +25,15 @@ def build():
         subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
+def _san_env():
+    """Sanitizer options of every simulated run.  Device memory is never
+    zeroed on the GPU, so every allocation is filled with a poison byte: a
+    kernel that reads memory nothing wrote then sees garbage here too."""
+    return {"ASAN_OPTIONS": os.environ.get(
+                "ASAN_OPTIONS", "detect_leaks=0:abort_on_error=0:max_malloc_fill_size=2147483647:malloc_fill_byte=190"),
+            "UBSAN_OPTIONS": os.environ.get("UBSAN_OPTIONS", "halt_on_error=1:print_stacktrace=1")}
+
+
 def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=None, kept_cap=64,
                post=True, hint=None, split=None, timeout=600, noalloc=False):
     """hint: None (general kernel) or an int max_top_k.  noalloc: through
@@ -54,8 +63,7 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
             env["TGS_SPLIT"] = str(split)
         if noalloc:
             env["TGS_SIM_NOALLOC"] = "1"
-        env.setdefault("ASAN_OPTIONS", "detect_leaks=0:abort_on_error=0")
-        env.setdefault("UBSAN_OPTIONS", "halt_on_error=1:print_stacktrace=1")
+        env.update(_san_env())
         env["TGS_SIM_TRACE"] = "1"
         p = subprocess.run([BIN, "sample", d], capture_output=True, text=True, env=env, timeout=timeout)
         launches = [tuple(int(f.split("=")[1]) for f in l.split()[1:3])
@@ -89,7 +97,8 @@ def run_maskbuild(byte_class, trans, complete, tok_off, tok_bytes, states, rows,
             np.ascontiguousarray(arr, dt).tofile(os.path.join(d, name + ".bin"))
         with open(os.path.join(d, "meta.txt"), "w") as f:
             f.write(f"{trans.shape[0]} {trans.shape[1]} {V} {len(states)} {eos} {n_rows}\n")
-        r = subprocess.run([BIN, "maskbuild", d], capture_output=True, text=True, timeout=timeout)
+        r = subprocess.run([BIN, "maskbuild", d], capture_output=True, text=True, timeout=timeout,
+                           env={**os.environ, **_san_env()})
         if r.returncode != 0:
             raise RuntimeError(f"simulation failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")
         return np.fromfile(os.path.join(d, "out_post.bin"), np.float32).reshape(n_rows, V)
@@ -107,7 +116,8 @@ def run_logprob(logits, tokens, V=None, timeout=600):
         np.ascontiguousarray(tokens, np.int32).tofile(os.path.join(d, "tokens.bin"))
         with open(os.path.join(d, "meta.txt"), "w") as f:
             f.write(f"{B} {V} {stride} {dtype}\n")
-        r = subprocess.run([BIN, "logprob", d], capture_output=True, text=True, timeout=timeout)
+        r = subprocess.run([BIN, "logprob", d], capture_output=True, text=True, timeout=timeout,
+                           env={**os.environ, **_san_env()})
         if r.returncode != 0:
             raise RuntimeError(f"simulation failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")
         return (np.fromfile(os.path.join(d, "out_lp.bin"), np.float32),
@@ -129,7 +139,8 @@ def run_spec(target, draft, dtok, T, u_acc, u_res, timeout=600):
         np.ascontiguousarray(u_res, np.float32).tofile(os.path.join(d, "u_res.bin"))
         with open(os.path.join(d, "meta.txt"), "w") as f:
             f.write(f"{B} {k} {V} {dtype}\n")
-        r = subprocess.run([BIN, "spec", d], capture_output=True, text=True, timeout=timeout)
+        r = subprocess.run([BIN, "spec", d], capture_output=True, text=True, timeout=timeout,
+                           env={**os.environ, **_san_env()})
         if r.returncode != 0:
             raise RuntimeError(f"simulation failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")
         n_acc = np.fromfile(os.path.join(d, "out_nacc.bin"), np.int32)
