@@ -7,8 +7,8 @@
 //   numerics q40 N seed   (u64)tg_q40d(e) == tg_q40(e), e in [0, 1]
 //   numerics divt N seed  tg_div_t(z, T, 1/T) == z / T, any z, T > 0 with 1/T finite
 //   numerics q40exp N seed  tg_q40d_exp_nonpos(x) == tg_q40d(tg_expf_nonpos(x))
-//   numerics pow2fma N seed the mass of fma(z, rT, -m) == the mass of RN(z rT) - m,
-//                           T a power of two, m = RN(zmax rT) with zmax >= z
+//   numerics pow2fma N seed the mass and the weight of fma(z, rT, -m) == those of
+//                           RN(z rT) - m, T a power of two, m = RN(zmax rT), zmax >= z
 // Prints the number of mismatches (and the first few).
 #include <hip/hip_runtime.h>
 
@@ -146,9 +146,13 @@ int main(int argc, char** argv) {
       if (!(zmax >= z) && z == z && z > -__builtin_inff()) continue;
       const float m = zmax * rT;
       if (!__builtin_isfinite(m)) continue;
-      const double q1 = tg_q40d_exp_nonpos(__builtin_fmaf(z, rT, -m));
-      const double q0 = tg_q40d(tg_expf_nonpos(z * rT - m));
+      const float x1 = __builtin_fmaf(z, rT, -m), x0 = z * rT - m;
+      const double q1 = tg_q40d_exp_nonpos(x1);
+      const double q0 = tg_q40d(tg_expf_nonpos(x0));
       if (q1 != q0) report("pow2fma", z, T, q1, q0);
+      // the weight itself (the residual draw's operand), bit for bit
+      const float e1 = tg_expf_nonpos(x1), e0 = tg_expf_nonpos(x0);
+      if (ubits(e1) != ubits(e0)) report("pow2fma-w", z, T, e1, e0);
     }
   } else if (mode == "divt") {
     // z: every exponent of the fast range and beyond it, both signs, plus

@@ -265,21 +265,31 @@ struct alignas(16) SeqState {
 static_assert(sizeof(SeqState) == 32, "state layout");
 static_assert(Tile<float>::NV <= SPEC_GROUPS && Tile<uint16_t>::NV <= SPEC_GROUPS, "group sums per block");
 
-// Row statistics (m, S) of row r of sequence b from its block terms, by one
-// wave: m = max m_b; S = pairwise tree over term_b = (f32(Q_b) 2^-40)
-// weight(m_b, m), zero padded to 256 leaves (four per lane).
-__device__ __forceinline__ void row_stats(const SpecArgs& a, long long br, float* m_out, float* S_out) {
-  const int lane = lane_id();
+// Block terms of one row, four per lane (blocks 4 lane + j; -inf / 0 past
+// the row's blocks).
+struct RowTerms {
   float mb[4];
   u64 qb[4];
-  float m = -__builtin_inff();
+};
+__device__ __forceinline__ RowTerms row_terms(const SpecArgs& a, long long br) {
+  const int lane = lane_id();
+  RowTerms t;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int i = 4 * lane + j;
-    mb[j] = i < a.nb ? a.blk_m[br * a.nbs + i] : -__builtin_inff();
-    qb[j] = i < a.nb ? a.blk_q[br * a.nbs + i] : 0ull;
-    m = fmaxf(m, mb[j]);
+    t.mb[j] = i < a.nb ? a.blk_m[br * a.nbs + i] : -__builtin_inff();
+    t.qb[j] = i < a.nb ? a.blk_q[br * a.nbs + i] : 0ull;
   }
+  return t;
+}
+
+// Row statistics (m, S) of a row from its block terms, by one wave:
+// m = max m_b; S = pairwise tree over term_b = (f32(Q_b) 2^-40)
+// weight(m_b, m), zero padded to 256 leaves (four per lane).
+__device__ __forceinline__ void row_stats(const RowTerms& tt, float* m_out, float* S_out) {
+  const float (&mb)[4] = tt.mb;
+  const u64 (&qb)[4] = tt.qb;
+  float m = fmaxf(fmaxf(mb[0], mb[1]), fmaxf(mb[2], mb[3]));
   m = wave_maxf(m);
   float S = 0.0f;
   if (m > -__builtin_inff()) {
@@ -350,12 +360,25 @@ __global__ __launch_bounds__(DT) void spec_decide_kernel(SpecArgs a) {
       if (lane == 0) sarg[r] = x;
     }
   } else if (!__builtin_isnan(T)) {
-    for (int r = w; r < R; r += DW) {
+    // a wave's rows r and r + DW in pairs: both rows' terms requested
+    // before either is reduced (C5's 17 rows: one pair for wave 0)
+    for (int r = w; r < R; r += 2 * DW) {
+      const bool two = r + DW < R;
+      const RowTerms t0 = row_terms(a, br0 + r);
+      RowTerms t1 = {};
+      if (two) t1 = row_terms(a, br0 + r + DW);
       float m, S;
-      row_stats(a, br0 + r, &m, &S);
+      row_stats(t0, &m, &S);
       if (lane == 0) {
         sm[r] = m;
         sS[r] = S;
+      }
+      if (two) {
+        row_stats(t1, &m, &S);
+        if (lane == 0) {
+          sm[r + DW] = m;
+          sS[r + DW] = S;
+        }
       }
     }
   }
@@ -441,9 +464,14 @@ struct DrawRow {
   bool resid, fast;
   __device__ __forceinline__ double mass(float zt, float zd) const {
     if (fast) {
-      const float wt = tg_expf_nonpos(tg_div_t(zt, st.T, st.rT, st.tdiv) - mt);
-      if (!resid) return tg_q40d(wt);
-      const float wd = tg_expf_nonpos(tg_div_t(zd, st.T, st.rT, st.tdiv) - md);
+      // a power-of-two T: y - m as one fma (the block kernel's form; the
+      // weight, and so every mass below, is the same bit for bit)
+      const bool p2 = st.tdiv == TDIV_POW2;
+      const float xt = p2 ? __builtin_fmaf(zt, st.rT, -mt) : tg_div_t(zt, st.T, st.rT, st.tdiv) - mt;
+      if (!resid) return tg_q40d_exp_nonpos(xt);
+      const float wt = tg_expf_nonpos(xt);
+      const float xd = p2 ? __builtin_fmaf(zd, st.rT, -md) : tg_div_t(zd, st.T, st.rT, st.tdiv) - md;
+      const float wd = tg_expf_nonpos(xd);
       const float pa = tg_div_rcp(wt, St, rSt);
       const float pb = tg_div_rcp(wd, Sd, rSd);
       return tg_q40d(fmaxf(pa - pb, 0.0f));
