@@ -649,6 +649,37 @@ __device__ __forceinline__ T wave_sum(T x) {
   return x;
 }
 
+// G (2 or 4) sums at once, x[g] summed over the wave: lane l ends with the
+// sum for group l / (64 / G).  Each step halves the values a lane carries
+// (the lane keeps one half, sends the other to its partner at lane ^ 32,
+// then ^ 16) before the plain butterfly: one sum's cost instead of G.
+// Exact for integer sums.
+template <int G, typename T>
+__device__ __forceinline__ T wave_sum_groups(const T (&x)[G]) {
+  static_assert(G == 2 || G == 4, "groups");
+  const int lane = lane_id();
+  const bool h32 = (lane & 32) != 0;
+  T k;
+  if constexpr (G == 4) {
+    T k0 = h32 ? x[2] : x[0], k1 = h32 ? x[3] : x[1];
+    const T s0 = h32 ? x[0] : x[2], s1 = h32 ? x[1] : x[3];
+    k0 += xor_lane<32>(s0);
+    k1 += xor_lane<32>(s1);
+    const bool h16 = (lane & 16) != 0;
+    k = h16 ? k1 : k0;
+    k += xor_lane<16>(h16 ? k0 : k1);
+  } else {
+    k = h32 ? x[1] : x[0];
+    k += xor_lane<32>(h32 ? x[0] : x[1]);
+    k += xor_lane<16>(k);
+  }
+  k += xor_lane<8>(k);
+  k += xor_lane<4>(k);
+  k += xor_lane<2>(k);
+  k += xor_lane<1>(k);
+  return k;
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_max(T x) {
   T y;

@@ -528,6 +528,7 @@ __global__ __launch_bounds__(NT) void spec_mass_kernel(SpecArgs a) {
   load_block<Tin>(dw.tr, blk, dw.V, a.aligned, rt);
   if (dw.resid) load_block<Tin>(dw.dr, blk, dw.V, a.aligned, rd);
   u64* gw = a.blk_w + ((long long)b * a.nbs + blk) * SPEC_GROUPS;
+  u64 gq[TL::NV];
 #pragma unroll
   for (int i = 0; i < TL::NV; i++) {
     double ws[TL::EPV];
@@ -535,9 +536,12 @@ __global__ __launch_bounds__(NT) void spec_mass_kernel(SpecArgs a) {
     double ls = 0.0;
 #pragma unroll
     for (int e = 0; e < TL::EPV; e++) ls += ws[e];
-    const u64 q = wave_sum((u64)ls);
-    if (lane_id() == 0) gw[i] = q;
+    gq[i] = (u64)ls;
   }
+  // the groups' sums in one reduction: lane 64 / NV * i holds group i's
+  const u64 q = wave_sum_groups<TL::NV>(gq);
+  constexpr int LPG = 64 / TL::NV;
+  if ((lane_id() & (LPG - 1)) == 0) gw[lane_id() / LPG] = q;
 }
 
 struct DrawScratch {
