@@ -152,9 +152,29 @@ __device__ __forceinline__ BlockRef block_next(const SpecArgs& a, const BlockRef
   return y;
 }
 
-// One block's statistics from its loaded vectors; lane 0 stores them.
+// A block of finite maximum whose exact mass waits, as per-lane partial
+// sums, to be reduced together with the wave's next such block: one grouped
+// reduction per pair of blocks instead of one per block (exact: integers).
+struct PendingMass {
+  u64 q;        // this lane's partial sum
+  float m;      // the block's maximum
+  long long o;  // its slot; -1: none (wave-uniform)
+};
+__device__ __forceinline__ void flush_pending(const SpecArgs& a, PendingMass& p) {
+  if (p.o < 0) return;
+  const u64 q = wave_sum(p.q);
+  if (lane_id() == 0) {
+    a.blk_m[p.o] = p.m;
+    a.blk_q[p.o] = q;
+  }
+  p.o = -1;
+}
+
+// One block's statistics from its loaded vectors; lane 0 stores them (lane
+// 32 too when a pending block is reduced with this one).
 template <typename Tin>
-__device__ __forceinline__ void block_stats(const SpecArgs& a, const BlockRef& x, const uint4 (&raw)[Tile<Tin>::NV]) {
+__device__ __forceinline__ void block_stats(const SpecArgs& a, const BlockRef& x, const uint4 (&raw)[Tile<Tin>::NV],
+                                            PendingMass& pend) {
   using TL = Tile<Tin>;
   const long long o = ((long long)x.b * (2 * a.k + 1) + x.r) * a.nbs + x.blk;
   if (x.greedy) {
@@ -205,6 +225,26 @@ __device__ __forceinline__ void block_stats(const SpecArgs& a, const BlockRef& x
       for (int j = 0; j < TL::EPL; j++) qd += tg_q40d_exp_nonpos(v[j] - mx);
     }
     q = (u64)qd;
+    if (pend.o < 0) {
+      pend.q = q;
+      pend.m = mx;
+      pend.o = o;
+      return;
+    }
+    // lanes 0-31 end with the pending block's sum, lanes 32-63 with this one's
+    const u64 pair[2] = {pend.q, q};
+    const u64 s2 = wave_sum_groups<2>(pair);
+    const int lane = lane_id();
+    if (lane == 0) {
+      a.blk_m[pend.o] = pend.m;
+      a.blk_q[pend.o] = s2;
+    }
+    if (lane == 32) {
+      a.blk_m[o] = mx;
+      a.blk_q[o] = s2;
+    }
+    pend.o = -1;
+    return;
   } else if (mx > -__builtin_inff()) {
     // a +inf logit in the block (weight(inf, inf) = 1, everything else 0)
 #pragma unroll
@@ -235,6 +275,10 @@ __global__ __launch_bounds__(NT) void spec_block_kernel(SpecArgs a) {
   const int n = min(per, nwork - f0);
   if (n <= 0) return;
   BlockRef x = block_ref(a, f0);
+  PendingMass pend;
+  pend.q = 0;
+  pend.m = 0.0f;
+  pend.o = -1;
   uint4 cur[TL::NV];
   if (x.live) load_block<Tin>(row_ptr<Tin>(a, x.b, x.r), x.blk, a.V, a.aligned, cur);
   for (int i = 0; i < n; i++) {
@@ -245,12 +289,13 @@ __global__ __launch_bounds__(NT) void spec_block_kernel(SpecArgs a) {
       xn = block_next(a, x);
       if (xn.live) load_block<Tin>(row_ptr<Tin>(a, xn.b, xn.r), xn.blk, a.V, a.aligned, nxt);
     }
-    if (x.live) block_stats<Tin>(a, x, cur);
+    if (x.live) block_stats<Tin>(a, x, cur, pend);
     if (!more) break;
 #pragma unroll
     for (int v = 0; v < TL::NV; v++) cur[v] = nxt[v];
     x = xn;
   }
+  flush_pending(a, pend);
 }
 
 // ------------------------------------------------------------------ K2
