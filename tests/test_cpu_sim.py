@@ -333,6 +333,16 @@ def test_spec_zero_residual_falls_back_to_target(sim, oracle):
     assert (o["n_acc"] == 0).all() and (o["info"]["resampled"] == 2).all()
 
 
+@pytest.mark.parametrize("T", [1.0, 0.5, 0.7])
+def test_spec_special_blocks(sim, oracle, T):
+    """The GPU test's batch of -inf, NaN and +inf blocks between finite ones
+    (deferred block masses across blocks stored at once), greedy and NaN-T
+    sequences among them."""
+    from test_gpu_spec import special_blocks_case
+
+    _spec_check(sim, oracle, special_blocks_case(T))
+
+
 def test_spec_invalid_rows(sim, oracle):
     from tinygpt_amd import workloads as W
 

@@ -89,3 +89,31 @@ def test_spec_k64_all_accepted(sampler, oracle):
     c["u_acc"][:] = 0.0
     o = _check(sampler, oracle, "spec k64", c)
     assert (o["n_acc"] == 64).all()
+
+
+def special_blocks_case(T):
+    """Blocks whose maximum is -inf (every id -inf or NaN) or +inf between
+    finite ones, so that a block's exact mass that waits to be reduced with
+    the wave's next finite block crosses blocks that store theirs at once; a
+    greedy and a NaN-temperature sequence among stochastic ones.  T 1.0 and
+    0.5 take the power-of-two form, 0.7 the exact divide."""
+    from tinygpt_amd import workloads as W
+
+    c = W.config5(B=6, k=3, V=4096, seed_offset=14, T=1.0)  # four blocks of 1024 ids per row
+    c["T"][:] = T
+    c["T"][2] = 0.0
+    c["T"][4] = np.nan
+    tg, dr = c["target"], c["draft"]
+    tg[0, 1, 1024:2048] = -np.inf
+    dr[0, 0, 2048:3072] = np.nan
+    tg[1, 2, 3000] = np.inf
+    dr[3, 1, 5] = np.inf
+    tg[5, 0, :] = -np.inf  # a whole target row without mass
+    tg[5, 0, 7] = 1.0
+    c["dtok"][0, 1] = 1500  # inside target row 1's -inf block: p_target 0, rejected there if reached
+    return c
+
+
+@pytest.mark.parametrize("T", [1.0, 0.5, 0.7])
+def test_spec_special_blocks(sampler, oracle, T):
+    _check(sampler, oracle, f"special_blocks T={T}", special_blocks_case(T))
