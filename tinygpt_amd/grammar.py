@@ -20,7 +20,7 @@ import re
 
 import numpy as np
 
-__all__ = ["GrammarError", "Dfa", "compile_gbnf", "token_csr", "PACE_TOOL_TAGS"]
+__all__ = ["GrammarError", "Dfa", "compile_gbnf", "token_bytes_table", "token_csr", "PACE_TOOL_TAGS"]
 
 
 class GrammarError(ValueError):
@@ -358,6 +358,31 @@ def compile_gbnf(text: str, max_states: int = 200000) -> Dfa:
     tc = np.where(tc >= 0, remap[np.where(tc >= 0, tc, 0)], -1)[live]
     full = tc[:, np.array(cls)]  # [n, 256]
     return Dfa(full.astype(np.int32), accept[live])
+
+
+def token_bytes_table(vocab_size: int, decode=None) -> list[bytes]:
+    """The per-id byte strings that grammar masks test, built as the server
+    builds them at start-up (native-mac/Sources/TinyGPTServe/Serve.swift:398-408,
+    `Array(tok.decode([id]).utf8)` for every id): each id decoded on its own
+    and the string encoded as UTF-8.
+
+    decode None: the byte-level tokenizer of the from-scratch models
+      (TokenizerBox.byteLevel, Serve.swift:1887-1893; ByteTokenizer.decode,
+      native-mac/Sources/TinyGPTModel/Tokenizer.swift:35-41): an id below 256
+      is that byte, decoded as UTF-8 with each invalid sequence replaced by
+      U+FFFD.  Ids 0-127 give their byte; ids 128-255 (a lone non-ASCII byte)
+      give EF BF BD; ids from 256 on give no bytes.
+    decode a callable (list of ids -> str): an HF tokenizer's decode
+      (HFTokenizer.decode calls swift-transformers' decode(tokens:), which
+      keeps special tokens), e.g. `lambda ids: tok.decode(ids,
+      skip_special_tokens=False)` for a `tokenizers.Tokenizer`.  A token
+      holding part of a multi-byte character decodes to U+FFFD there too, so
+      its entry is EF BF BD, not its own bytes.
+    """
+    if decode is None:
+        return [bytes([i]).decode("utf-8", errors="replace").encode("utf-8") if i < 256 else b""
+                for i in range(vocab_size)]
+    return [decode([i]).encode("utf-8") for i in range(vocab_size)]
 
 
 def token_csr(tokens: list[bytes]) -> tuple[np.ndarray, np.ndarray]:
