@@ -194,3 +194,43 @@ def test_mask_table_update_batches(sampler):
     with pytest.raises(Exception):
         sampler.update_mask_rows(np.array([1, n], np.int32), new[:2])
     check("rejected update")
+
+
+def test_byte_level_token_table_rows(sampler, oracle):
+    """Rows over the byte-level model's token table as the server builds it
+    (token_bytes_table: ids 128-255 decode to U+FFFD), for every tool-tag
+    DFA state, built on the device and read back through the sampler,
+    bit-exact against the DFA replay oracle; no row allows ids 128-255,
+    whose table bytes EF BF BD the tool-tag language never holds."""
+    import torch
+
+    import tinygpt_amd as tg
+    from tinygpt_amd import grammar as G
+
+    V = 256
+    d = G.compile_gbnf(G.PACE_TOOL_TAGS)
+    toks = G.token_bytes_table(V)
+    off, data = G.token_csr(toks)
+    states = np.arange(d.n, dtype=np.int32)
+    n = len(states)
+    sampler.set_mask_table(np.full((n, (V + 31) // 32), 0xFFFFFFFF, np.uint32), V)
+    dev = "cuda:0"
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    H.log(f"case byte-level token table: V={V} states={n}")
+    bc, ct = d.byte_classes()
+    sampler.mask_rows_from_dfa(T(bc), T(ct), T(d.complete.astype(np.uint8)), T(off), T(data), T(states),
+                               T(np.arange(n, dtype=np.int32)))
+    params = tg.make_params(n, temperature=0.0, mask_state=list(range(n)))
+    post = torch.full((n, V), float("nan"), dtype=torch.float32, device=dev)
+    # the batch's hint (every row greedy) keeps these V = 256 rows on the k64
+    # kernel, the path the byte-level decode loop runs
+    sampler.sample(torch.zeros(n, V, dtype=torch.float32, device=dev), tg.params_to_device(params, dev),
+                   torch.zeros(n, dtype=torch.float32, device=dev), vocab=V, debug={"post_logits": post},
+                   hint=tg.batch_hint(params, V))
+    torch.cuda.synchronize()
+    got = post.cpu().numpy() == 0.0
+    want = oracle.dfa_mask_rows(d.trans, d.complete, toks, states, eos=-1)
+    bits = ((want[:, np.arange(V) >> 5] >> (np.arange(V) & 31).astype(np.uint32)) & 1).astype(bool)
+    np.testing.assert_array_equal(got, bits)
+    assert not got[:, 128:].any()
+    H.log("case byte-level token table: ok")
