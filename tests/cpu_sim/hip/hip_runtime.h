@@ -7,8 +7,11 @@
 // intrinsics (__shfl*, __ballot) exchange values among the 64 threads of a
 // wave through a per-wave buffer between two barriers.  A thread leaving
 // the kernel drops out of its barriers (exited waves do not take part in
-// later barriers on the GPU either).  __shared__ variables are static:
-// blocks never run concurrently, so one instance per kernel suffices.
+// later barriers on the GPU either).  __shared__ variables are static (one
+// instance per kernel); a kernel whose static LDS is one TGS_STATIC_SMEM
+// object gets a copy per block instead.  With TGS_SIM_CONCURRENT set, every
+// block of a launch runs at once (for kernels whose blocks wait on each
+// other; only kernels with no plain __shared__ variables may run so).
 // Device memory is host memory.
 #pragma once
 
@@ -37,6 +40,7 @@
 extern "C" unsigned char __start_tgs_lds[], __stop_tgs_lds[];
 #define __align__(x) alignas(x)
 #define TGS_DYN_SMEM(name) unsigned char* name = hipcpu::dyn_smem()
+#define TGS_STATIC_SMEM(type, name) type& name = *reinterpret_cast<type*>(hipcpu::static_smem(sizeof(type)))
 
 struct dim3 {
   unsigned x, y, z;
@@ -60,6 +64,8 @@ enum {
   hipSuccess = 0,
   hipErrorOutOfMemory = 2,
   hipErrorInvalidValue = 1,
+  hipStreamCaptureStatusNone = 0,
+  hipStreamCaptureStatusActive = 1,
   hipMemcpyHostToDevice = 1,
   hipMemcpyDeviceToHost = 2,
   hipDeviceAttributeMultiprocessorCount = 1,
@@ -73,18 +79,22 @@ struct WaveCtx {
   std::unique_ptr<std::barrier<>> bar;
   uint64_t buf[64];
 };
+constexpr size_t kStaticSmem = 65536;  // per-block static LDS object (TGS_STATIC_SMEM) at most
 struct BlockCtx {
   std::unique_ptr<std::barrier<>> bar;
   std::vector<WaveCtx> waves;
   std::vector<unsigned char> smem;
+  std::vector<unsigned char> ssmem;
 };
-inline BlockCtx*& block_ctx() {
-  static BlockCtx* b = nullptr;
-  return b;
-}
+inline thread_local BlockCtx* t_ctx = nullptr;
+inline BlockCtx*& block_ctx() { return t_ctx; }
 inline thread_local dim3 t_thread, t_block;
 inline dim3 g_block_dim, g_grid_dim;
 inline unsigned char* dyn_smem() { return block_ctx()->smem.data(); }
+inline unsigned char* static_smem(size_t n) {
+  if (n > kStaticSmem) std::abort();
+  return block_ctx()->ssmem.data();
+}
 
 inline int lane() { return (int)(t_thread.x & 63); }
 inline WaveCtx& wave() { return block_ctx()->waves[t_thread.x / 64]; }
@@ -118,30 +128,41 @@ inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args
   if (std::getenv("TGS_SIM_TRACE"))  // launch log (tests check which kernel ran)
     std::fprintf(stderr, "launch grid=%u block=%u lds=%zu\n", grid.x, block.x, shmem);
   const unsigned nt = block.x;
-  for (unsigned bi = 0; bi < grid.x * grid.y; bi++) {
-    const unsigned bx = bi % grid.x, by = bi / grid.x;
-    BlockCtx ctx;
-    ctx.bar = std::make_unique<std::barrier<>>(nt);
-    ctx.waves.resize((nt + 63) / 64);
-    for (unsigned w = 0; w < ctx.waves.size(); w++) {
-      const unsigned n = std::min(64u, nt - 64 * w);
-      ctx.waves[w].bar = std::make_unique<std::barrier<>>(n);
+  const unsigned nblk = grid.x * grid.y;
+  const bool conc = std::getenv("TGS_SIM_CONCURRENT") != nullptr;
+  const unsigned group = conc ? nblk : 1u;  // blocks started together
+  for (unsigned b0 = 0; b0 < nblk; b0 += group) {
+    const unsigned nb = std::min(group, nblk - b0);
+    std::vector<std::unique_ptr<BlockCtx>> ctxs(nb);
+    for (unsigned i = 0; i < nb; i++) {
+      auto ctx = std::make_unique<BlockCtx>();
+      ctx->bar = std::make_unique<std::barrier<>>(nt);
+      ctx->waves.resize((nt + 63) / 64);
+      for (unsigned w = 0; w < ctx->waves.size(); w++) {
+        const unsigned n = std::min(64u, nt - 64 * w);
+        ctx->waves[w].bar = std::make_unique<std::barrier<>>(n);
+      }
+      ctx->smem.assign(shmem ? shmem : 1, 0xA5);
+      ctx->ssmem.assign(kStaticSmem, 0xA5);
+      ctxs[i] = std::move(ctx);
     }
-    ctx.smem.assign(shmem ? shmem : 1, 0xA5);
     std::memset(__start_tgs_lds, 0xA5, (size_t)(__stop_tgs_lds - __start_tgs_lds));
-    block_ctx() = &ctx;
     std::vector<std::thread> th;
-    th.reserve(nt);
-    for (unsigned t = 0; t < nt; t++)
-      th.emplace_back([&, t]() {
-        t_thread = dim3(t);
-        t_block = dim3(bx, by);
-        k(args...);
-        ctx.waves[t / 64].bar->arrive_and_drop();
-        ctx.bar->arrive_and_drop();
-      });
+    th.reserve((size_t)nb * nt);
+    for (unsigned i = 0; i < nb; i++) {
+      const unsigned bi = b0 + i, bx = bi % grid.x, by = bi / grid.x;
+      BlockCtx* ctx = ctxs[i].get();
+      for (unsigned t = 0; t < nt; t++)
+        th.emplace_back([=]() {
+          t_ctx = ctx;
+          t_thread = dim3(t);
+          t_block = dim3(bx, by);
+          k(args...);
+          ctx->waves[t / 64].bar->arrive_and_drop();
+          ctx->bar->arrive_and_drop();
+        });
+    }
     for (auto& x : th) x.join();
-    block_ctx() = nullptr;
   }
 }
 
@@ -312,6 +333,11 @@ inline hipError_t hipMemset(void* p, int v, size_t n) { std::memset(p, v, n); re
 inline hipError_t hipMemcpy(void* d, const void* s, size_t n, int) { std::memcpy(d, s, n); return hipSuccess; }
 inline hipError_t hipDeviceSynchronize() { return hipSuccess; }
 inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+typedef int hipStreamCaptureStatus;
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* s) {
+  *s = hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
 inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
 inline hipError_t hipSetDevice(int) { return hipSuccess; }
 inline hipError_t hipGetDeviceCount(int* n) { *n = 1; return hipSuccess; }

@@ -4,6 +4,7 @@
 //                           writes the outputs next to them.
 #include <cstdint>
 #include <cstdio>
+#include <algorithm>
 #include <cstdlib>
 #include <string>
 #include <vector>
@@ -59,6 +60,12 @@ int main(int argc, char** argv) {
     tgs_debug dbg = {kid.data(), kpr.data(), kept_cap, counts.data(), mass.data(), cut.data(),
                      post ? postv.data() : nullptr};
     tgs_batch_hint hb = {hint, hint_min};
+    // TGS_SIM_REPEAT=n: n calls on the same inputs, each of whose ids must
+    // equal the first call's (the split kernel's state carries over calls)
+    const char* rep_env = std::getenv("TGS_SIM_REPEAT");
+    const int reps = rep_env ? std::max(1, std::atoi(rep_env)) : 1;
+    std::vector<int32_t> first;
+    for (int it = 0; it < reps; it++) {
     if (std::getenv("TGS_SIM_NOALLOC")) {  // the allocation-free entry point (static workspace)
       rc = tgs_sample_noalloc(0, logits.data(), (tgs_dtype)dtype, B, V, stride,
                               hist_cap ? (const int32_t*)hist.data() : nullptr,
@@ -74,7 +81,14 @@ int main(int argc, char** argv) {
                       (const float*)u.data(), out.data(), hint >= 0 ? &hb : nullptr, &dbg, nullptr);
       if (rc) { std::printf("sample %d %s\n", rc, tgs_last_error(h)); return 7; }
     }
-    dump(dir + "/out_ids.bin", out.data(), out.size() * 4);
+    if (it == 0) {
+      first = out;
+    } else if (out != first) {
+      std::printf("call %d: ids differ from the first call's\n", it);
+      return 9;
+    }
+    }
+    dump(dir + "/out_ids.bin", first.data(), first.size() * 4);
     dump(dir + "/out_kept_ids.bin", kid.data(), kid.size() * 4);
     dump(dir + "/out_kept_probs.bin", kpr.data(), kpr.size() * 4);
     dump(dir + "/out_counts.bin", counts.data(), counts.size() * 4);

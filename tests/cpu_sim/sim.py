@@ -35,9 +35,13 @@ def _san_env():
 
 
 def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=None, kept_cap=64,
-               post=True, hint=None, split=None, timeout=600, noalloc=False):
+               post=True, hint=None, split=None, timeout=600, noalloc=False, concurrent=False, repeat=1,
+               env_extra=None):
     """hint: None (general kernel) or an int max_top_k.  noalloc: through
-    tgs_sample_noalloc (static workspace) instead of a handle."""
+    tgs_sample_noalloc (static workspace) instead of a handle.  concurrent:
+    every workgroup of a launch runs at once (the split k64 kernel's chunks
+    then exchange their row-wide bound; only launches of that kernel may run
+    so).  repeat: that many calls, each of whose ids must equal the first's."""
     B = logits.shape[0]
     V = logits.shape[1] if V is None else V
     dtype = 1 if logits.dtype == np.uint16 else 0
@@ -63,6 +67,17 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
             env["TGS_SPLIT"] = str(split)
         if noalloc:
             env["TGS_SIM_NOALLOC"] = "1"
+        if concurrent:
+            env["TGS_SIM_CONCURRENT"] = "1"
+        else:
+            # workgroups run one after another here: a chunk's partners have
+            # not run yet when it polls their keys, so it gives up at once
+            # and keeps its own bound (the row's last chunk sees every key)
+            env.setdefault("TGS_KEY_SPINS", "1")
+        if repeat > 1:
+            env["TGS_SIM_REPEAT"] = str(repeat)
+        if env_extra:
+            env.update(env_extra)
         env.update(_san_env())
         env["TGS_SIM_TRACE"] = "1"
         p = subprocess.run([BIN, "sample", d], capture_output=True, text=True, env=env, timeout=timeout)

@@ -108,4 +108,6 @@ def test_noalloc_rejects_sizes_beyond_its_workspace(lib):
                                   None) == -1  # a table needs its pointer
     assert lib.tgs_sample_noalloc(0, p, 5, 4, 1000, 1000, None, None, 0, p, p, p, None, 0, 0, None, None,
                                   None) == -1  # dtype
-    assert lib.tgs_sample_noalloc(*args(0, 1000, 0)) == 0  # empty batch: nothing to do
+    # an empty batch only prepares the device (the set-up a captured call
+    # cannot do): TGS_OK on a GPU, TGS_EHIP where there is none
+    assert lib.tgs_sample_noalloc(*args(0, 1000, 0)) in (0, -3)

@@ -188,6 +188,86 @@ def test_k64_bf16_and_mask(sim, oracle):
            hint=tg.batch_hint(params, V), split=3, kept_cap=64)
 
 
+def _check_conc(sim, oracle, x, params, u, hist, hist_len, mask=None, split=None, repeat=3, xmap=True):
+    """The k64 kernel with every workgroup of the launch running at once, so
+    that split rows exchange their row-wide bound; `repeat` calls on one
+    handle (each call's ids must equal the first's: the exchange state, the
+    epoch and the cleared list entries carry over calls)."""
+    import tinygpt_amd as tg
+
+    V = x.shape[1]
+    env = {} if xmap else {"TGS_XMAP": "0"}
+    r = sim.run_sample(x, params, u, hist, hist_len, mask_table=mask, kept_cap=64, hint=tg.batch_hint(params, V),
+                       split=split, concurrent=True, repeat=repeat, env_extra=env)
+    o = oracle.sample_batch(x, params, u, hist=hist, hist_len=hist_len, mask_table=mask, kept_cap=64,
+                            want_post=True)
+    assert len(r["launches"]) == repeat  # one k64 launch per call
+    return r, o, H.compare(r, o, params, V, what="sim-concurrent")
+
+
+def _c2_like(g, B, V, oracle, H_=128):
+    """C2's statistics at a simulated size: N(0, 3^2), 8 spikes at 12.0 per
+    row (ties), Zipf history, presence and frequency penalties, top-k 50."""
+    from tinygpt_amd import workloads as W
+
+    x = W.normal_f32(g, (B, V), 3.0)
+    for b in range(B):
+        x[b, g.choice(V, size=8, replace=False)] = 12.0
+    params = oracle.make_params(B, temperature=0.7, top_k=50, top_p=0.9, presence=0.5, frequency=0.3)
+    hist = W.zipf_ids(g, 0, V, shape=(B, H_))
+    hist_len = np.full(B, H_, np.int32)
+    u = W.uniforms(g, B)
+    return x, params, u, hist, hist_len
+
+
+@pytest.mark.parametrize("split,xmap", [(4, True), (8, False)])
+def test_k64_exchange_c2_like(sim, oracle, split, xmap):
+    """Split rows sharing the row-wide bound (C2's statistics), with and
+    without the XCD-aware workgroup order, over three calls."""
+    g = np.random.default_rng(60 + split)
+    x, params, u, hist, hist_len = _c2_like(g, 8 if xmap else 2, 40000, oracle)
+    params["temperature"][1] = 0.0  # a greedy row
+    params["top_k"][0] = 1
+    _check_conc(sim, oracle, x, params, u, hist, hist_len, split=split, xmap=xmap)
+
+
+def test_k64_exchange_mixed_rows(sim, oracle):
+    """The exchange on the random batches' rows (ties, special values, equal
+    rows, ascending rows whose top ids share one chunk, penalties that lift
+    or sink history ids), k up to 64: rows whose candidates outgrow a list
+    or the staging take the sorted top-k and exact paths."""
+    g = np.random.default_rng(63)
+    V = 20000
+    x, params, u, hist, hist_len = _batch(63, 7, V, oracle)
+    params = _k64_params(g, params, V)
+    _check_conc(sim, oracle, x, params, u, hist, hist_len, split=2, xmap=False)
+
+
+def test_k64_exchange_mask_bf16(sim, oracle):
+    """The exchange with a grammar mask (dense, sparse and empty rows) on
+    bf16 logits."""
+    from tinygpt_amd import workloads as W
+
+    g = np.random.default_rng(64)
+    V = 24000
+    x, params, u, hist, hist_len = _c2_like(g, 4, V, oracle, H_=64)
+    params = _k64_params(g, params, V)
+    table = g.integers(0, 1 << 32, size=(3, (V + 31) // 32), dtype=np.uint64).astype(np.uint32)
+    table[1] &= np.uint32(0x00100001)
+    table[2] = 0
+    params["mask_state"] = np.array([0, 1, 2, -1])
+    _check_conc(sim, oracle, W.f32_to_bf16_bits(x), params, u, hist, hist_len, mask=table, split=3, xmap=False)
+
+
+def test_k64_exchange_history_at_top(sim, oracle):
+    """The exchange where the rows' largest logits are penalised history ids."""
+    from test_gpu_sampler import _history_at_top_batch
+
+    g = np.random.default_rng(65)
+    x, params, u, hist, hist_len = _history_at_top_batch(g, 4, 16000, oracle, H_=256)
+    _check_conc(sim, oracle, x, params, u, hist, hist_len, split=4, xmap=False)
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_token_logprobs(sim, oracle, bf16):
     """tgs_token_logprobs: one workgroup per row, rows split into chunks

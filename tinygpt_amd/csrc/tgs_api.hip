@@ -30,8 +30,9 @@ struct tgs_ctx {
   unsigned long long* ws = nullptr;
   int* ws_cnt = nullptr;
   int ws_rows = 0;  // chunk lists of KMAX entries the workspace holds
-  unsigned* k64_cnt = nullptr;  // fused kernel arrival counters, one line per row
+  unsigned* k64_cnt = nullptr;  // fused kernel exchange lines (arrival counter, epoch, count words), one per row
   unsigned long long* k64_lists = nullptr;  // fused kernel chunk lists, [max_batch * kMaxSplit][64]
+  unsigned long long* k64_keys = nullptr;   // fused kernel bound-exchange keys, [max_batch][K64_KEYS]
   uint32_t* mask_table = nullptr;
   int n_states = 0, mask_vocab = 0, mask_words = 0;
   void* mask_stage = nullptr;  // tgs_mask_table_update staging (grown on demand)
@@ -131,10 +132,39 @@ int choose_split(int num_cu, int ws_rows, int B, int V) {
   return S;
 }
 
-// Static LDS of the fused kernel beyond its dynamic carve-up: the wave
-// lists of its merges (4 waves x 64 u64), its staging (4 waves x 64 vectors
-// and their indices), the radix-select scratch and a few words.
-constexpr size_t kK64Static = 4 * 64 * 8 + 4 * 64 * (16 + 4) + sizeof(tgs::BlockScratch) + 128;
+// Static LDS of the fused kernel beyond its dynamic carve-up (wave lists,
+// staging, the radix-select scratch and the merge's words), with room for
+// alignment.
+size_t k64_static() { return tgs::k64_static_lds() + 256; }
+
+// Whether a split k64 launch of `wgs` workgroups is resident on the device
+// at once (then its chunks can wait on each other for the row-wide bound),
+// from the runtime's occupancy of the instantiation; cached per variant and
+// LDS size.  TGS_XCHG=0 turns the exchange off (tuning, tests).
+bool k64_resident(int num_cu, int dt, bool whole_vec, bool mask, size_t lds, long long wgs) {
+  const char* env = std::getenv("TGS_XCHG");
+  if (env && std::atoi(env) == 0) return false;
+  struct Entry {
+    int key;
+    size_t lds;
+    int n;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  const int key = dt * 4 + (whole_vec ? 2 : 0) + (mask ? 1 : 0);
+  int n = -1;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+      if (e.key == key && e.lds == lds) n = e.n;
+  }
+  if (n < 0) {
+    n = tgs::k64_resident_per_cu(dt, whole_vec, mask, lds);
+    std::lock_guard<std::mutex> lock(mu);
+    cache.push_back({key, lds, n});
+  }
+  return n > 0 && wgs <= (long long)n * num_cu;
+}
 
 // What a sampling call launches with: the device's size, and the workspace
 // and mask table it uses (a handle's allocations, or the allocation-free
@@ -145,8 +175,9 @@ struct SampleRes {
   unsigned long long* ws = nullptr;  // [ws_rows][KMAX] general-path chunk lists
   int* ws_cnt = nullptr;             // [ws_rows * (KMAX / 64)]
   int ws_rows = 0;
-  unsigned* k64_cnt = nullptr;              // [rows * K64_CNT_STRIDE], zero between calls
-  unsigned long long* k64_lists = nullptr;  // [rows * kMaxSplit][64], all ~0 between calls
+  unsigned* k64_cnt = nullptr;              // [rows * K64_CNT_STRIDE], zeroed at set-up
+  unsigned long long* k64_lists = nullptr;  // [rows * kMaxSplit][64], entries 0 between calls
+  unsigned long long* k64_keys = nullptr;   // [rows * K64_KEYS], zeroed at set-up
   const uint32_t* mask_table = nullptr;     // nullptr: no table
   int n_states = 0, mask_words = 0;
 };
@@ -197,6 +228,7 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
   a.ws_cnt = res.ws_cnt;
   a.cnt = res.k64_cnt;
   a.lists = res.k64_lists;
+  a.keys = res.k64_keys;
   a.dbg = dz;
   // Kernels: the fused top_k <= 64 kernel when the hint says every row is
   // greedy or has top_k <= 64; otherwise the chunk kernel (+ merge kernel
@@ -223,10 +255,32 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
     a.capt = tgs::K64_CAP;
     a.ws_stride = 64;
     const size_t lds = (size_t)a.off_cand + (size_t)(tgs::K64_CAP + 16) * 8;
-    if (lds + kK64Static > res.lds_limit) return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS");
+    if (lds + k64_static() > res.lds_limit) return efail(err, TGS_ETOOBIG, "history / vocab too large for LDS");
+    if (a.S > 1 && V > (1 << 18)) return efail(err, TGS_ETOOBIG, "vocab beyond 2^18 ids (split-row list entries)");
+    // split rows share a row-wide bound when every workgroup of the launch
+    // is resident at once: each wave publishes its kq largest thread maxima
+    // (at least 64 keys per row, at most K64_KEYS)
+    a.xchg = a.S > 1 && k64_resident(res.num_cu, dt, a.whole_vec != 0, res.mask_table != nullptr && res.n_states > 0,
+                                     lds, (long long)B * a.S);
+    a.kq = a.S >= 4 ? 4 : 8;
+    // polls of the row's keys before a chunk keeps its own bound: far more
+    // than a resident row needs (TGS_KEY_SPINS overrides: tests)
+    {
+      const char* env = std::getenv("TGS_KEY_SPINS");
+      a.key_spins = env ? std::max(0, std::atoi(env)) : 2048;
+    }
+    // the chunks of a row on one XCD (workgroups are dealt out to the XCDs in
+    // turn); TGS_XMAP=0 turns it off
+    {
+      const char* env = std::getenv("TGS_XMAP");
+      a.xmap = a.S > 1 && B % 8 == 0 && !(env && std::atoi(env) == 0);
+    }
     // a row in one chunk that one wave holds: the one-wave variant (its
     // barriers and merges involve a single wave)
     const bool small = a.S == 1 && V <= tgs::k64_small_ids(dt) && hist_cap <= tgs::K64_SMALL_MAX_HIST;
+    if (std::getenv("TGS_LOG_LAUNCH"))  // diagnostics: the launch's shape
+      std::fprintf(stderr, "tgs k64: B=%d V=%d S=%d L=%d lds=%zu xchg=%d kq=%d xmap=%d small=%d\n", B, V, a.S, a.L,
+                   lds, a.xchg, a.kq, a.xmap, (int)small);
     hipError_t e = tgs::launch_k64(a, dt, lds, stream, small);
     if (e != hipSuccess) return efail(err, TGS_EHIP, std::string("sample kernel launch: ") + hipGetErrorString(e));
     return TGS_OK;
@@ -282,22 +336,25 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
 // tgs_sample_noalloc takes its workspace from `scratch`, a static device
 // array of fixed size (each GPU the library runs on holds its own copy until
 // the process ends) instead of a handle's allocations:
-//   [k64 chunk lists: kNaRows * kMaxSplit * 64 u64, all ~0 between calls]
+//   [k64 chunk lists: kNaRows * kMaxSplit * 64 u64, entries 0 between calls]
+//   [k64 bound-exchange keys: kNaRows * K64_KEYS u64]
 //   [general-path chunk lists: kNaWsRows * KMAX u64]
-//   [k64 arrival counters: kNaRows * K64_CNT_STRIDE u32, zero between calls]
+//   [k64 exchange lines: kNaRows * K64_CNT_STRIDE u32, counters zero between calls]
 //   [general-path list counts: kNaWsRows * (KMAX / 64) i32]
 // The k64 kernel leaves its lists and counters in that state after every
-// call; the first call on a device puts them there with a fill kernel.
+// call; the first call on a device zeroes the whole array with a fill kernel
+// (a call with B = 0 does only that, outside any graph capture).
 // Host code never passes `scratch` itself to a kernel: its address on each
 // device comes from hipGetSymbolAddress.
 constexpr int kNaRows = 256;    // rows per call
 constexpr int kNaWsRows = 512;  // general-path (row, chunk) lists
 constexpr int kNaHist = tgs::K64_MAX_HIST;
 constexpr size_t kNaListWords = (size_t)kNaRows * kMaxSplitK64 * 64;
+constexpr size_t kNaKeyWords = (size_t)kNaRows * tgs::K64_KEYS;
 constexpr size_t kNaWsWords = (size_t)kNaWsRows * tgs::KMAX;
 constexpr size_t kNaCntU32 = (size_t)kNaRows * tgs::K64_CNT_STRIDE;
 constexpr size_t kNaWsCntI32 = (size_t)kNaWsRows * (tgs::KMAX / 64);
-constexpr size_t kNaWords = kNaListWords + kNaWsWords + (kNaCntU32 + kNaWsCntI32) / 2;
+constexpr size_t kNaWords = kNaListWords + kNaKeyWords + kNaWsWords + (kNaCntU32 + kNaWsCntI32) / 2;
 static_assert(kNaCntU32 % 2 == 0 && kNaWsCntI32 % 2 == 0, "whole 8-byte words");
 
 constexpr int kNaMaxDevices = 64;
@@ -311,10 +368,9 @@ std::mutex g_na_mu;
 NoAllocDevice g_na[kNaMaxDevices];
 thread_local std::string g_na_err;
 
-__global__ void na_fill_kernel(unsigned long long* p, size_t n_ones, size_t n_zero) {
+__global__ void na_fill_kernel(unsigned long long* p, size_t n) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_ones + n_zero; i += stride)
-    p[i] = i < n_ones ? ~0ull : 0ull;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0ull;
 }
 
 }  // namespace
@@ -322,6 +378,11 @@ __global__ void na_fill_kernel(unsigned long long* p, size_t n_ones, size_t n_ze
 static __device__ __align__(256) unsigned long long scratch[kNaWords];
 
 namespace {
+
+bool noalloc_ready(int device) {
+  std::lock_guard<std::mutex> lock(g_na_mu);
+  return g_na[device].ready;
+}
 
 // Once per device, with that device current: the address of its scratch,
 // its size limits, the kernels' LDS ceilings and the lists' initial state.
@@ -340,12 +401,11 @@ int noalloc_setup(int device, NoAllocDevice*& out) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
       d.lds_limit = (size_t)v;
     if (tgs::set_sample_lds_limit(d.lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
-    if (tgs::set_k64_lds_limit(d.lds_limit - kK64Static) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_k64_lds_limit(d.lds_limit - k64_static()) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topp_lds_limit(d.lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topk_lds_limit(d.lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
-    // k64 lists "not written" (~0); everything after them zero
-    hipLaunchKernelGGL(na_fill_kernel, dim3(1024), dim3(256), 0, nullptr, d.ptr, kNaListWords,
-                       kNaWords - kNaListWords);
+    // everything zero: k64 lists "not written", counters and epochs zero
+    hipLaunchKernelGGL(na_fill_kernel, dim3(1024), dim3(256), 0, nullptr, d.ptr, kNaWords);
     e = hipGetLastError();
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return efail(g_na_err, TGS_EHIP, std::string("scratch set-up: ") + hipGetErrorString(e));
@@ -421,13 +481,16 @@ int tgs_create(tgs_handle* out, int device, int max_batch, int max_vocab, int ma
   if (e == hipSuccess) e = hipMemset(h->k64_cnt, 0, cnt_bytes);
   const size_t list_bytes = sizeof(unsigned long long) * (size_t)max_batch * kMaxSplit * 64;
   if (e == hipSuccess) e = hipMalloc(&h->k64_lists, list_bytes);
-  if (e == hipSuccess) e = hipMemset(h->k64_lists, 0xFF, list_bytes);  // every entry "not written"
+  if (e == hipSuccess) e = hipMemset(h->k64_lists, 0, list_bytes);  // every entry "not written"
+  const size_t key_bytes = sizeof(unsigned long long) * (size_t)max_batch * tgs::K64_KEYS;
+  if (e == hipSuccess) e = hipMalloc(&h->k64_keys, key_bytes);
+  if (e == hipSuccess) e = hipMemset(h->k64_keys, 0, key_bytes);
   if (e == hipSuccess) {
     // raise the dynamic-LDS ceiling to the device limit; a runtime that
     // rejects the attribute keeps its default (calls that need more fail
     // with TGS_ETOOBIG / TGS_EHIP instead)
     if (tgs::set_sample_lds_limit(h->lds_limit - sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
-    if (tgs::set_k64_lds_limit(h->lds_limit - kK64Static) != hipSuccess) (void)hipGetLastError();
+    if (tgs::set_k64_lds_limit(h->lds_limit - k64_static()) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topp_lds_limit(h->lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     if (tgs::set_topk_lds_limit(h->lds_limit - 2 * sizeof(tgs::BlockScratch)) != hipSuccess) (void)hipGetLastError();
     e = hipDeviceSynchronize();
@@ -447,6 +510,7 @@ void tgs_destroy(tgs_handle h) {
   if (h->ws_cnt) (void)hipFree(h->ws_cnt);
   if (h->k64_cnt) (void)hipFree(h->k64_cnt);
   if (h->k64_lists) (void)hipFree(h->k64_lists);
+  if (h->k64_keys) (void)hipFree(h->k64_keys);
   if (h->mask_table) (void)hipFree(h->mask_table);
   if (h->mask_stage) (void)hipFree(h->mask_stage);
   free_spec(h);
@@ -561,6 +625,7 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
   res.ws_rows = h->ws_rows;
   res.k64_cnt = h->k64_cnt;
   res.k64_lists = h->k64_lists;
+  res.k64_keys = h->k64_keys;
   const bool table_ok = h->mask_table && h->mask_vocab >= V;
   res.mask_table = table_ok ? h->mask_table : nullptr;
   res.n_states = table_ok ? h->n_states : 0;
@@ -583,19 +648,30 @@ int tgs_sample_noalloc(int device, const void* d_logits, tgs_dtype dt, int B, in
   if (n_states < 0 || (n_states > 0 && (!d_mask_table || mask_vocab < V)))
     return efail(g_na_err, TGS_EINVAL, "mask table: n_states >= 0; a table needs a pointer and mask_vocab >= V");
   if (device < 0 || device >= kNaMaxDevices) return efail(g_na_err, TGS_EINVAL, "device");
-  if (B == 0) return TGS_OK;
   DeviceGuard g(device);
   if (!g.ok) return efail(g_na_err, TGS_EHIP, "hipSetDevice");
+  // The device's set-up (a fill kernel and a synchronisation) cannot run
+  // under graph capture: the first call on a device, which a call with B = 0
+  // can be, has to come before any capture.
   NoAllocDevice* d = nullptr;
+  if (!noalloc_ready(device)) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return efail(g_na_err, TGS_EINVAL,
+                   "tgs_sample_noalloc: the first call on a device sets it up and must not be captured "
+                   "(call it once with B = 0 before capturing)");
+  }
   const int rc = noalloc_setup(device, d);
   if (rc != TGS_OK) return rc;
+  if (B == 0) return TGS_OK;
   SampleRes res;
   res.num_cu = d->num_cu;
   res.lds_limit = d->lds_limit;
   res.k64_lists = d->ptr;
-  res.ws = d->ptr + kNaListWords;
+  res.k64_keys = d->ptr + kNaListWords;
+  res.ws = d->ptr + kNaListWords + kNaKeyWords;
   res.ws_rows = kNaWsRows;
-  res.k64_cnt = (unsigned*)(d->ptr + kNaListWords + kNaWsWords);
+  res.k64_cnt = (unsigned*)(d->ptr + kNaListWords + kNaKeyWords + kNaWsWords);
   res.ws_cnt = (int*)(res.k64_cnt + kNaCntU32);
   res.mask_table = n_states > 0 ? d_mask_table : nullptr;
   res.n_states = n_states;

@@ -21,6 +21,11 @@
 #ifndef TGS_DYN_SMEM
 #define TGS_DYN_SMEM(name) extern __shared__ __align__(16) unsigned char name[]
 #endif
+// A kernel's static LDS gathered in one object (the CPU simulation gives
+// each workgroup its own copy, so that workgroups can run concurrently).
+#ifndef TGS_STATIC_SMEM
+#define TGS_STATIC_SMEM(type, name) __shared__ type name
+#endif
 
 namespace tgs {
 
@@ -700,6 +705,17 @@ __device__ __forceinline__ float wave_maxf(float x) {
   x = fmaxf(x, tg_u2f(xor_lane32<2>(tg_f2u(x))));
   x = fmaxf(x, tg_u2f(xor_lane32<1>(tg_f2u(x))));
   return x;
+}
+
+// Bitwise OR over the wave, as a wave-uniform (scalar) value.
+__device__ __forceinline__ uint32_t wave_or(uint32_t x) {
+  x |= xor_lane32<32>(x);
+  x |= xor_lane32<16>(x);
+  x |= xor_lane32<8>(x);
+  x |= xor_lane32<4>(x);
+  x |= xor_lane32<2>(x);
+  x |= xor_lane32<1>(x);
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
 }
 
 // Number of set bits of a wave mask below this lane.

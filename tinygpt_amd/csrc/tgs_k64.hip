@@ -4,52 +4,68 @@
 // Workgroup (b, c) of K64_NT threads owns chunk c of row b: S chunks per
 // row, each at most K64_NT * K64_NVT sixteen-byte vectors (thread t holding
 // chunk vectors t, t + K64_NT, ...).  Rows that fit one chunk of
-// K64_SMALL_NT threads (one wave) run on that instantiation instead.  Everything a thread reads is requested
-// at entry: the row's parameters, its history ids, its vectors and (with a
-// mask table) their mask words, so the whole chunk is in flight at once.
-// Under a full-chip stream the chunk's data lands in one burst near the end
-// of the stream, so the steps after it are kept short:
+// K64_SMALL_NT threads (one wave) run on that instantiation instead.
+// Everything a thread reads is requested at entry: the row's parameters,
+// its history ids, its vectors and (with a mask table) their mask words, so
+// the whole chunk is in flight at once.  Under a full-chip stream the
+// chunk's data lands in one burst near the end of the stream, so the steps
+// after it are kept short:
 //   1. Vector maxima and thread maxima of the raw logits (ids the mask
 //      forbids and ids past the chunk left out).
-//   2. A bound: for m = 1 .. waves, the m-th largest over waves of the
-//      wave's ceil(k / m)-th largest thread maximum qualifies (m waves hold
-//      that many at or above it each); the bound is the largest of them,
-//      read from one wave sort each.  In the sort a thread whose maximum
-//      lies in a vector holding a history id of the chunk (the bits are in
-//      LDS before the chunk lands) takes the lowest key, so at least k
-//      distinct ids that are neither masked nor history ids have a raw
-//      logit at or above the bound.  The collection threshold cz lies 16
-//      representable values below it.
+//   2. A bound B: a raw logit such that at least k distinct ids of the row
+//      that are neither masked nor history ids lie at or above it.
+//        * The chunk's own bound: for m = 1 .. waves, the m-th largest over
+//          waves of the wave's ceil(k / m)-th largest thread maximum (m
+//          waves hold that many at or above it each), read from one wave
+//          sort each.  In the sort a thread whose maximum lies in a vector
+//          holding a history id of the chunk takes the lowest key.
+//        * Split rows whose whole grid is resident at once (the launch's
+//          exchange flag) also share a row-wide bound: each wave publishes
+//          the kq largest keys of its sort, tagged with the call's epoch,
+//          and every wave polls the row's S * waves * kq keys and takes
+//          their k-th largest (to 24 key bits).  Those keys belong to
+//          distinct threads, so k of them are k distinct qualifying ids.
+//          The row's k-th largest thread maximum lies close to its k-th
+//          largest logit, so a chunk collects a few ids instead of its own
+//          top k.  A wave whose poll does not complete in the launch's
+//          key_spins rounds keeps the chunk's bound.
+//      A wave collects from cz, 16 representable values below its bound
+//      (the larger of the two).
 //   3. Every vector whose maximum reaches cz is staged whole in its wave's
 //      LDS list.
 //   4. One staged vector per lane: the canonical logit y = z / T of each
 //      element (correctly rounded, tg_div_t), history ids left to their
 //      producers (the lane whose insertion created the id's LDS hash slot
 //      loads its logit at entry and adds its penalised value), the mask
-//      test, and a wave-aggregated append to the LDS candidate buffer that
-//      also counts the candidates strictly above yc = cz / T.
+//      test, and a wave-aggregated append to the LDS candidate buffer.
 //   5. An id left out is not a history id and has z < cz, so its y is at
-//      most yc: with at least k candidates strictly above yc the chunk's top
-//      k are among the candidates and are ranked into wave 0.  The ids
-//      behind the bound make that count at least k unless their quotients
-//      by T collide (a temperature so small that z / T overflows, say);
-//      then, and when a wave stages more vectors than its list holds (a
-//      skewed chunk), an exact radix selection runs over the chunk read
-//      again from memory.
+//      most yc = cz / T, while the k ids behind the bound have y at least
+//      y(B): when y(B) > yc, every id of the row's top k that lies in this
+//      chunk is a candidate.  When the quotients collide (a temperature so
+//      small that z / T overflows, say) or a wave stages more vectors than
+//      its list holds, the chunk's exact top k comes from a radix selection
+//      over the chunk read again from memory instead.
 //
 // Rows split over S > 1 chunks.  Each workgroup counts itself in the row's
-// arrival counter at entry (a relaxed device atomic issued with the loads).
+// arrival counter at entry (a relaxed device atomic issued with the loads)
+// and reads the row's epoch word; the call's tag is that word plus one.
 // The workgroup that arrives last merges the row: every other workgroup of
-// the row has started by then and stores its sorted list with agent-coherent
-// stores (written through past the per-XCD L2s, which are not coherent with
-// each other) without waiting for anything.  The merging workgroup polls
-// those lists with agent-coherent loads, one list per wave, until no entry
-// holds the empty marker, merges them with its own (a tree of wave merges),
-// finishes the row (masses, top-p, draw) and resets the lists to the marker
-// and the counter to zero for the next call.  The wait is bounded: one that
-// runs out (it cannot while every workgroup runs) writes id -4 for the row.
-// No fence is issued: on this part an agent-scope release or acquire fence
-// writes back or invalidates the whole L2 of the XCD.
+// the row has started by then.  The others publish their list with
+// agent-coherent stores (written through past the per-XCD L2s, which are
+// not coherent with each other) and exit: their candidates unsorted when
+// the row-wide bound left at most 64, else their sorted top k, then a count
+// word tagged with the epoch.  A list entry is the candidate's composite
+// with the epoch's low 14 bits between its key and its 18-bit id, so that
+// entries of one call order as their composites.  The merging workgroup
+// polls the count words, then the entries (until each holds the call's
+// tag), sorts the union in one wave when it holds at most 64 entries (a
+// tree of wave merges otherwise), finishes the row (masses, top-p, draw),
+// clears the entries it read (0: not written), and resets the counter and
+// advances the epoch for the next call.  Stale entries of an earlier call
+// carry another tag.  Every wait is bounded: a merge wait that runs out (it
+// cannot while every workgroup runs) writes id -4 for the row.  No fence is
+// issued: on this part an agent-scope release or acquire fence writes back
+// or invalidates the whole L2 of the XCD.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 #include "tgs_row.h"
@@ -58,12 +74,13 @@ namespace tgs {
 namespace k64 {
 
 constexpr int NVT = K64_NVT;         // 16-byte vectors per thread
-constexpr int P1 = NVT / 2;          // vectors behind the bound
-constexpr int KM = 64;               // largest top_k served
+constexpr int KM = 64;               // largest top_k served; longest published list
 constexpr int CAP = K64_CAP;         // candidate buffer entries
-constexpr u64 EMPTY = ~0ull;         // list entry not written yet: above every composite
-constexpr int SPIN_LIMIT = 1 << 18;  // polls of one list before the wait gives up
+constexpr u64 EMPTY = 0ull;          // list entry not written: a published entry never is 0
+constexpr int SPIN_LIMIT = 1 << 18;  // merge: polls of one list before the wait gives up
 constexpr uint32_t KEY_MIN = 0x00800000u;  // key of -FLT_MAX: below it only -inf and NaN
+constexpr uint32_t TAG_MASK = 0x3FFFu;     // epoch bits a list entry carries
+constexpr uint32_t ID_MASK = 0x3FFFFu;     // list entry id bits (V <= 2^18)
 
 template <typename Tin, int NTT>
 struct Geo {
@@ -71,8 +88,27 @@ struct Geo {
   static constexpr int NW = NTT / 64;
   static constexpr int CH = NTT * NVT * EPV;  // ids of a chunk at most
   static constexpr int MAXH = NTT >= K64_NT ? K64_MAX_HIST : K64_SMALL_MAX_HIST;  // longest history
-  static constexpr int NHID = (MAXH + NTT - 1) / NTT;  // history ids per thread
+  static constexpr int NHID = (MAXH + NTT - 1) / NTT;  // history ids per thread (its share of the row's)
   static constexpr uint32_t GM = (1u << EPV) - 1u;
+};
+
+// The static LDS of one workgroup.
+template <int NW>
+struct Shared {
+  u64 slots[NW][64];      // wave lists (merges, the ranked top k)
+  uint4 svec[NW][64];     // per wave: vectors whose maximum reaches the collection threshold
+  int sidx[NW][64];       // their vector index in the chunk
+  u64 own[64];            // merging workgroup: its own sorted top k
+  uint32_t wkey[NW][NW];  // [m - 1][wave]: the wave's ceil(k / m)-th largest thread maximum key
+  unsigned nbuf;          // candidates appended
+  int elect, tmo, spill;
+  int lcnt[K64_MAX_SPLIT];     // merging workgroup: entries of each chunk's list
+  int lsort[K64_MAX_SPLIT];    // 1: that list is sorted
+  int fast;                    // merging workgroup: entries laid out in mer (-1: the merge tree)
+  uint32_t rkey;               // the row-wide bound key (0: none)
+  alignas(16) u64 mer[66];     // merging workgroup: the lists end to end (+ a pad entry)
+  u64 mer2[64];                // ... and ranked
+  BlockScratch bs;
 };
 
 // The chunk's history bits in LDS, packed per thread: the EPV bits of chunk
@@ -111,6 +147,99 @@ __device__ __forceinline__ uint32_t bound_key(const uint32_t (*wkey)[NW], int la
     x = pos == 1 ? max(x, y) : pos == 2 ? min(x, y) : x;
     return max(max(readlane_u32(x, 0), readlane_u32(x, 5)), max(readlane_u32(x, 10), readlane_u32(x, 15)));
   }
+}
+
+// The row's published keys as one wave polls them: lane l holds keys l,
+// l + 64, ... (NJ = ceil(nk / 64) <= 4 of them); keys of this call carry its
+// epoch ep in their high word.  Every slot is loaded (a slot past nk reads
+// the last key) and slots past nk count as current keys of value 0, so that
+// the loops carry no branch (a branch per slot made each step of the k-th
+// key search a chain of scalar branches).
+template <int NJ>
+struct RowKeys {
+  u64 e[NJ];
+};
+template <int NJ>
+__device__ __forceinline__ void keys_issue(RowKeys<NJ>& K, const u64* keys, int nk) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const int i = lane + 64 * j;
+    K.e[j] = __hip_atomic_load(keys + (i < nk ? i : nk - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+template <int NJ>
+__device__ __forceinline__ bool keys_current(const RowKeys<NJ>& K, int nk, uint32_t ep) {
+  const int lane = lane_id();
+  bool stale = false;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) stale = stale || (lane + 64 * j < nk && (uint32_t)(K.e[j] >> 32) != ep);
+  return __ballot(stale) == 0ull;
+}
+
+// The row-wide bound key: one wave polls the row's nk keys until every key
+// holds the call's tag, then takes their k-th largest to 20 bits (the
+// largest multiple of 2^12 that at least k of them reach, one wave-wide
+// count per bit; 2^-11 of relative slack).  Returns 0 (no bound) when
+// max_spins polls did not see every key.
+template <int NJ>
+__device__ __forceinline__ uint32_t row_bound(const u64* keys, int nk, uint32_t ep, int k, int max_spins) {
+  const int lane = lane_id();
+  RowKeys<NJ> K;
+  keys_issue(K, keys, nk);
+  for (int spins = 0;; spins++) {
+    if (keys_current(K, nk, ep)) break;
+    if (spins >= max_spins) return 0u;
+    __builtin_amdgcn_s_sleep(1);
+    keys_issue(K, keys, nk);
+  }
+  uint32_t kk[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) kk[j] = lane + 64 * j < nk ? (uint32_t)K.e[j] : 0u;
+  uint32_t X = 0u;
+#pragma unroll
+  for (int bit = 31; bit >= 12; bit--) {
+    const uint32_t t = X | (1u << bit);
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) n += __popcll(__ballot(kk[j] >= t));
+    X = n >= k ? t : X;
+  }
+  return X;
+}
+
+// A list entry: composite x with the epoch's low bits between its key and
+// its id (entries of one call order as their composites; never 0, since a
+// candidate's key is above that of -inf).
+__device__ __forceinline__ u64 tag_entry(u64 x, uint32_t ep) {
+  const uint32_t id = (uint32_t)comp_id(x);
+  return (x & 0xFFFFFFFF00000000ull) | ((u64)(ep & TAG_MASK) << 18) | (u64)(ID_MASK - id);
+}
+__device__ __forceinline__ bool entry_ok(u64 e, uint32_t ep) {
+  return e != EMPTY && (uint32_t)((e >> 18) & TAG_MASK) == (ep & TAG_MASK);
+}
+__device__ __forceinline__ u64 untag_entry(u64 e) {
+  return comp_key((uint32_t)(e >> 32), (int)(ID_MASK - (uint32_t)(e & ID_MASK)));
+}
+
+// One list entry of another chunk for each lane with act (entry p of list
+// lp), polled until it holds the call's tag (bounded), then cleared for the
+// next call.  Returns the composite (0 without act or after a timeout, which
+// sets *tmo).
+__device__ __forceinline__ u64 take_entry(u64* lp, bool act, uint32_t ep, bool* tmo) {
+  u64 e = act ? __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : EMPTY;
+  int spins = 0;
+  while (__ballot(act && !entry_ok(e, ep)) != 0ull) {
+    if (++spins > SPIN_LIMIT) {
+      *tmo = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    if (act && !entry_ok(e, ep)) e = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!act) return 0ull;
+  __hip_atomic_store(lp, EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return entry_ok(e, ep) ? untag_entry(e) : 0ull;
 }
 
 struct alignas(16) u64x2 {
@@ -194,39 +323,21 @@ __device__ __forceinline__ u64 select_top(u64* buf, int n, int k, u64 (*slots)[6
   return lane < k ? acc : 0ull;
 }
 
-// Wave-aggregated append of composite x (when ok) to the LDS buffer.
-__device__ __forceinline__ void append(bool ok, u64 x, u64* buf, unsigned* nbuf) {
-  const u64 bal = __ballot(ok);
-  if (bal == 0ull) return;
-  unsigned base = 0;
-  if (lane_id() == 0) base = atomicAdd(nbuf, (unsigned)__popcll(bal));
-  base = (unsigned)__shfl((int)base, 0, 64);
-  const unsigned sl = base + lanes_below(bal);
-  if (ok && sl < (unsigned)CAP) buf[sl] = x;
-}
-
 // Wave-aggregated append of up to N composites per lane (entry q when
-// ok[q]) to the LDS buffer, counting the appended entries whose key is above
-// kc: one LDS atomic per wave on a packed counter (appended entries in the
-// low 16 bits, entries above kc in the high 16), slots from a wave prefix
-// sum of the lanes' counts.
+// ok[q]) to the LDS buffer: one LDS atomic per wave on the counter, slots
+// from a wave prefix sum of the lanes' counts.
 template <int N>
-__device__ __forceinline__ void append_n(const u64 (&x)[N], const bool (&ok)[N], uint32_t kc, u64* buf,
-                                         unsigned* packed) {
-  unsigned cnt = 0, abv = 0;
+__device__ __forceinline__ void append_n(const u64 (&x)[N], const bool (&ok)[N], u64* buf, unsigned* count) {
+  unsigned cnt = 0;
 #pragma unroll
-  for (int q = 0; q < N; q++) {
-    cnt += ok[q] ? 1u : 0u;
-    abv += (ok[q] && (uint32_t)(x[q] >> 32) > kc) ? 1u : 0u;
-  }
-  const unsigned v = cnt | (abv << 16);
-  const unsigned incl = wave_incl_scan(v);
+  for (int q = 0; q < N; q++) cnt += ok[q] ? 1u : 0u;
+  const unsigned incl = wave_incl_scan(cnt);
   const unsigned tot = readlane_u32(incl, 63);
   if (tot == 0u) return;
   unsigned base = 0;
-  if (lane_id() == 0) base = atomicAdd(packed, tot);
-  base = readlane_u32(base, 0) & 0xFFFFu;
-  unsigned sl = base + ((incl - v) & 0xFFFFu);
+  if (lane_id() == 0) base = atomicAdd(count, tot);
+  base = readlane_u32(base, 0);
+  unsigned sl = base + (incl - cnt);
 #pragma unroll
   for (int q = 0; q < N; q++)
     if (ok[q]) {
@@ -259,6 +370,20 @@ __device__ __forceinline__ void wave_finish_row(const SampleArgs& a, const Row& 
     float* kp = a.dbg.kept_probs + (long long)b * a.dbg.kept_cap;
     for (int i = lane; i < a.dbg.kept_cap; i += 64) kp[i] = (i == 0 && id >= 0) ? 1.0f : 0.0f;
   }
+}
+
+// Finish of a merged row (wave 0): x sorted descending, id -4 after a wait
+// that gave up.
+__device__ __forceinline__ void finish_merged(const SampleArgs& a, const Row& r, u64 x, int k, bool tmo) {
+  if (tmo) {
+    if (lane_id() == 0) {
+      a.out[r.b] = -4;
+      write_row_diag(a, r.b, 0, 0, 0, 0, -1);
+    }
+    return;
+  }
+  const int n = __popcll(__ballot(x != 0ull));
+  wave_finish_row(a, r, lane_id() < k ? x : 0ull, n < k ? n : k);
 }
 
 // Calls f(composite) for every allowed, non-history id of the chunk (and
@@ -334,19 +459,24 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   constexpr uint32_t GM = G::GM;
   constexpr int SCAP = 64;   // staged vectors per wave
   TGS_DYN_SMEM(smem);
-  __shared__ u64 slots[NW][64];      // wave lists (merges, the ranked top k)
-  __shared__ uint4 svec[NW][SCAP];   // per wave: vectors whose maximum reaches the collection threshold
-  __shared__ int sidx[NW][SCAP];     // their vector index in the chunk
-  __shared__ uint32_t wkey[NW][NW];  // [m - 1][wave]: the wave's ceil(k / m)-th largest thread maximum key
-  __shared__ unsigned nbuf;          // candidates appended (low 16 bits), of them above yc (high 16)
-  __shared__ int elect, tmo, spill;
-  __shared__ BlockScratch bs;
+  TGS_STATIC_SMEM(Shared<NW>, sh);
   int2* hash = (int2*)(smem + a.off_hash);
   uint32_t* bitmap = (uint32_t*)(smem + a.off_bitmap);
   u64* buf = (u64*)(smem + a.off_cand);
   const int w = threadIdx.x >> 6, lane = lane_id();
 
-  const int b = blockIdx.x / a.S, c = blockIdx.x % a.S;
+  // workgroup -> (row, chunk); with xmap (B a multiple of 8) the S chunks of
+  // a row are workgroups g = x (mod 8), which the dispatcher places on one
+  // XCD when it deals workgroups out to the eight XCDs in turn
+  int b, c;
+  if (a.xmap) {
+    const int g = (int)blockIdx.x, j = g >> 3;
+    b = (g & 7) + 8 * (j / a.S);
+    c = j % a.S;
+  } else {
+    b = (int)blockIdx.x / a.S;
+    c = (int)blockIdx.x % a.S;
+  }
   if (b >= a.B) return;
   const int v0 = c * a.L, v1 = min(a.V, v0 + a.L);  // a.L is a multiple of EPV
   const int nvec = (v1 - v0 + EPV - 1) / EPV;
@@ -356,29 +486,31 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
 
   // ---- everything read first, in the order it is needed (a wave's loads
   // return in order): the row's parameters, its history length and ids, the
-  // arrival count, the chunk, the mask words
+  // mask words, the chunk, then the row's arrival count and epoch word
   const tgs_row_params p = a.params[b];
   const float ub = a.u[b];
   const int hlr = *(a.hist_len ? a.hist_len + b : (const int*)a.params);
   const bool hv = a.hist && a.hist_cap > 0;
   const int* hp = hv ? a.hist + (long long)b * a.hist_cap : (const int*)a.params;
   const int hlast = hv ? a.hist_cap - 1 : 0;
-  int hid[NHID];
+  // the row's epoch word (every wave reads it: one request per wave) and
+  // arrival count
+  const uint32_t epw = __hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int hid[NHID];  // this thread's share of the history: entries threadIdx.x + q NTT
 #pragma unroll
   for (int q = 0; q < NHID; q++) {
     const int j = (int)threadIdx.x + q * NTT;
     hid[q] = hp[j < hlast ? j : hlast];
   }
-  unsigned arrived = 0;
-  if (a.S > 1 && threadIdx.x == 0)
-    arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // the mask words depend on the parameters: requested before the chunk so
   // that they do not queue behind it (a state out of range reads the first
   // row, and the row is rejected below)
   uint32_t mw[MASK ? NVT : 1];
+  const uint32_t* mrow_any = a.mask_table;  // the row's mask row (the first row for a state out of range)
   if constexpr (MASK) {
     const uint32_t* mrow = a.mask_table;
     if (p.mask_state >= 0 && p.mask_state < a.n_states) mrow += (long long)p.mask_state * a.mask_words;
+    mrow_any = mrow;
 #pragma unroll
     for (int i = 0; i < NVT; i++) {
       const int j = (int)threadIdx.x + i * NTT;
@@ -401,6 +533,10 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       raw[i] = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);  // NaN: never counted
     }
   }
+  // Behind the chunk: the row's arrival count (a device atomic queues far
+  // longer than a load, and a wave's loads return in order, so issued before
+  // the chunk it would hold the chunk's data back) and the epoch word (every
+  // wave reads it: one request per wave).
   const int hl = a.hist_len ? hlr : a.hist_cap;
 
   Row r;
@@ -410,57 +546,59 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       a.out[b] = valid ? -3 : -2;  // -3: row outside the launch hint
       write_row_diag(a, b, 0, 0, 0, 0, -1);
     }
-    // the row's last arrival clears the counter (no lists were written)
-    if (a.S > 1 && threadIdx.x == 0 && arrived == (unsigned)(a.S - 1))
-      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
+    return;  // no workgroup of the row counts itself in or publishes anything
   }
   const int k = r.mode == 0 ? 1 : r.k;
   r.v0 = v0;
   r.v1 = v1;
   const bool masked = MASK && r.mrow != nullptr;
 
-  // ---- history: each id of the chunk counted in the LDS hash (its
-  // producer is the lane that created its slot) and marked in the packed
-  // history bits (HBits)
+  // ---- history, first its bits: each id of the chunk marked in the packed
+  // history bits (HBits), all the bound needs.  The id -> count table is
+  // cleared here and filled once the bound's keys have gone out.
   if (threadIdx.x == 0) {
-    nbuf = 0;
-    tmo = 0;
-    spill = 0;
-    elect = a.S > 1 && arrived == (unsigned)(a.S - 1);
+    sh.nbuf = 0;
+    sh.tmo = 0;
+    sh.spill = 0;
   }
   const bool pen = r.use_pen;
   using HB = HBits<Tin, NTT>;
   constexpr int HPW = HB::HPW;
-  int hslot[NHID];
-#pragma unroll
-  for (int q = 0; q < NHID; q++) hslot[q] = -1;
   if (pen) {
     for (int i = threadIdx.x; i < a.TS; i += NTT) hash[i] = make_int2(-1, 0);
 #pragma unroll
     for (int q = 0; q < HPW; q++) bitmap[threadIdx.x * HPW + q] = 0u;
     __syncthreads();
-    const unsigned tmask = (unsigned)a.TS - 1u;
 #pragma unroll
     for (int q = 0; q < NHID; q++) {
       const int id = hid[q];
       if ((int)threadIdx.x + q * NTT < r.H && id >= v0 && id < v1) {
-        unsigned h = hash_slot(id, a.ts_shift);
-        for (;;) {  // the table has at least twice as many slots as history entries
-          const int old = atomicCAS(&hash[h].x, -1, id);
-          if (old == -1 || old == id) {
-            atomicAdd(&hash[h].y, 1);
-            if (old == -1) hslot[q] = (int)h;
-            break;
-          }
-          h = (h + 1) & tmask;
-        }
         const int j = (id - v0) / EPV;
         atomicOr(&bitmap[HB::word(j)], 1u << (HB::shift(j) + (id - v0) % EPV));
       }
     }
   }
   __syncthreads();
+  int hslot[NHID];
+#pragma unroll
+  for (int q = 0; q < NHID; q++) hslot[q] = -1;
+  // The logits (and mask words) of this thread's history entries, read now,
+  // right behind the chunk, so that they have landed when the penalties are
+  // applied after the bound.  Every lane loads (an entry outside the chunk
+  // reads the chunk's first id), so that the loads carry no branch: a branch
+  // would leave the compiler to wait for them wherever the chunk is waited
+  // for.
+  float zq[NHID];
+  uint32_t mq[NHID];
+#pragma unroll
+  for (int q = 0; q < NHID; q++) {
+    const int id = hid[q];
+    const bool in = (int)threadIdx.x + q * NTT < r.H && id >= v0 && id < v1;
+    const int lid = in ? id : v0;
+    zq[q] = Elem<Tin>::scalar(rowp, lid);
+    mq[q] = 0xFFFFFFFFu;
+    if constexpr (MASK) mq[q] = mrow_any[lid >> 5];
+  }
   // the history bits of this thread's vectors (vector i at bit i * EPV), one
   // load while the chunk is still in flight
   uint32_t hpk[HPW];
@@ -480,19 +618,6 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   } else {
 #pragma unroll
     for (int q = 0; q < HPW; q++) hpk[q] = 0u;
-  }
-  // producers' logits (and mask words): one load per history id of the
-  // chunk, first needed after the bound
-  float zq[NHID];
-  uint32_t mq[NHID];
-#pragma unroll
-  for (int q = 0; q < NHID; q++) {
-    zq[q] = 0.0f;
-    mq[q] = 0xFFFFFFFFu;
-    if (hslot[q] >= 0) {
-      zq[q] = Elem<Tin>::scalar(rowp, hid[q]);
-      if (masked) mq[q] = r.mrow[hid[q] >> 5];
-    }
   }
 
   // ---- 1. vector maxima and thread maximum of the raw logits (ids the
@@ -520,13 +645,14 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     tm = fmaxf(tm, m);
   }
 
-  // ---- 2. the bound: at least k thread maxima (distinct ids) are >= it.
-  // For m = 1 .. NW, the m-th largest over waves of the wave's ceil(k / m)-th
-  // largest key qualifies (m waves hold ceil(k / m) keys at or above it
-  // each); the bound is the largest of them, all read from one sort per
-  // wave.  A thread whose maximum lies in a vector holding a history id
-  // sorts as the lowest key, so every thread maximum behind the bound is an
-  // id that is not a history id.
+  uint32_t ep;
+  // ---- 2. the bound.  A thread whose maximum lies in a vector holding a
+  // history id sorts as the lowest key, so every thread maximum behind a
+  // bound is an id that is not a history id.  The chunk's bound: for
+  // m = 1 .. NW, the m-th largest over waves of the wave's ceil(k / m)-th
+  // largest key (m waves hold ceil(k / m) keys at or above it each), all
+  // read from one sort per wave.  With the exchange, the wave's kq largest
+  // keys go out to the row first.
   {
     uint32_t hw = hpk[0];
 #pragma unroll
@@ -534,45 +660,124 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     const bool hmax = ((hw >> (im * EPV % 32)) & GM) != 0u;
     const uint32_t tk = (tm > -__builtin_inff() && !hmax) ? tg_key(tm) : 0u;
     const uint32_t srt = wave_sort_desc(tk);  // lane i: the (i+1)-th largest
+    // the call's tag: never 0 (the exchange memory starts zeroed, and the
+    // epoch word never holds ~0)
+    ep = epw + 1u;
+    if (a.xchg) {
+      if (lane < a.kq)
+        __hip_atomic_store(a.keys + (long long)b * K64_KEYS + (c * NW + w) * a.kq + lane, ((u64)ep << 32) | srt,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 #pragma unroll
     for (int m = 1; m <= NW; m++) {
       const uint32_t v = readlane_u32(srt, (k + m - 1) / m - 1);
-      if (lane == 0) wkey[m - 1][w] = v;
+      if (lane == 0) sh.wkey[m - 1][w] = v;
     }
   }
-  __syncthreads();
-  const uint32_t bkey = bound_key<NW>(wkey, lane);
+  // The row's arrival count, issued by the last wave (which polls nothing)
+  // once its keys are out: the workgroup whose arrival is the row's last
+  // merges it, and every other workgroup of the row is past its loads by
+  // then.  Its result is first needed after the collection.  The history
+  // logits are taken first, so that no wait for them lands behind the
+  // atomic (a wave's memory operations return in order).
+  unsigned arrived = 0;
+  if (a.S > 1 && w == NW - 1) {
+#pragma unroll
+    for (int q = 0; q < NHID; q++) asm volatile("" ::"v"(zq[q]), "v"(mq[q]));
+    if (lane == 63) arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();  // the table clear and the wave keys
+  // ---- history counts: each id of the chunk counted in the LDS hash (its
+  // producer is the lane that created its slot)
+  if (pen) {
+    const unsigned tmask = (unsigned)a.TS - 1u;
+#pragma unroll
+    for (int q = 0; q < NHID; q++) {
+      const int id = hid[q];
+      if ((int)threadIdx.x + q * NTT < r.H && id >= v0 && id < v1) {
+        unsigned h = hash_slot(id, a.ts_shift);
+        for (;;) {  // the table has at least twice as many slots as history entries
+          const int old = atomicCAS(&hash[h].x, -1, id);
+          if (old == -1 || old == id) {
+            atomicAdd(&hash[h].y, 1);
+            if (old == -1) hslot[q] = (int)h;
+            break;
+          }
+          h = (h + 1) & tmask;
+        }
+      }
+    }
+  }
+  uint32_t bkey = bound_key<NW>(sh.wkey, lane);
+  if (a.xchg) {
+    if (w == 0) {
+      // wave 0 polls for the workgroup
+      const int nk = a.S * NW * a.kq;
+      const u64* rk_keys = a.keys + (long long)b * K64_KEYS;
+      const uint32_t rk = nk <= 64    ? row_bound<1>(rk_keys, nk, ep, k, a.key_spins)
+                          : nk <= 128 ? row_bound<2>(rk_keys, nk, ep, k, a.key_spins)
+                                      : row_bound<4>(rk_keys, nk, ep, k, a.key_spins);
+      if (lane == 0) sh.rkey = rk;
+    }
+    __syncthreads();  // also publishes the table
+    const uint32_t rk = sh.rkey;
+    bkey = rk > bkey ? rk : bkey;
+  } else if (pen) {
+    __syncthreads();  // the table
+  }
   // the collection threshold: 16 representable values below the bound, so
   // that the ids that set the bound land strictly above its canonical value
   const bool all = bkey < KEY_MIN + 32u;  // no usable bound: collect every allowed id
   const float cz = all ? -__builtin_inff() : tg_unkey(bkey - 16u);
   const float yc = all ? -__builtin_inff() : row_y(r, cz);
   const uint32_t kc = tg_key(yc);
-
-  // ---- 3. collection: every vector whose maximum reaches cz is staged
-  // whole (its bits and its chunk index) in its wave's list
-  unsigned ns = 0;  // staged vectors of the wave (uniform)
+  // quotients that collide at the bound: the exact path
+  if (!all && !(row_y(r, tg_unkey(bkey)) > yc) && lane == 0) sh.spill = 1;
+  // the producers' composites (their penalised canonical logits; the loads
+  // went out before the bound)
+  u64 hcomp[NHID];
 #pragma unroll
-  for (int i = 0; i < NVT; i++) {
-    const bool pass = vm[i] >= cz && vm[i] > -__builtin_inff();  // (cz may be -inf)
-    const u64 bal = __ballot(pass);
-    if (bal != 0ull) {
+  for (int q = 0; q < NHID; q++) {
+    u64 x = 0ull;
+    if (hslot[q] >= 0) {
+      const int id = hid[q];
+      const float y = row_y(r, penalise(zq[q], hash[hslot[q]].y, r));
+      const bool ok = y > -__builtin_inff() && (!masked || ((mq[q] >> (id & 31)) & 1u));
+      if (ok) x = comp_key(tg_key(y), id);
+      if (a.dbg.post_logits) a.dbg.post_logits[(long long)b * a.V + id] = ok ? y : -__builtin_inff();
+    }
+    hcomp[q] = x;
+  }
+
+  // ---- 3. collection: the vectors whose maximum reaches cz, staged whole
+  // (their bits and their chunk index) in the wave's LDS list.  Each lane
+  // marks its own (one bit per vector, plain compares), and the wave's union
+  // of those marks skips the empty vector slots with a scalar bit test (a
+  // ballot per slot cost more than the staging itself).
+  uint32_t pm = 0u;
+#pragma unroll
+  for (int i = 0; i < NVT; i++)
+    pm |= (vm[i] >= cz && vm[i] > -__builtin_inff()) ? (1u << i) : 0u;  // (cz may be -inf)
+  const uint32_t PM = wave_or(pm);
+  {
+    unsigned ns = 0;  // staged vectors of the wave (uniform)
+#pragma unroll
+    for (int i = 0; i < NVT; i++) {
+      if (!(PM & (1u << i))) continue;  // uniform
+      const bool pass = (pm >> i) & 1u;
+      const u64 bal = __ballot(pass);
       const unsigned sl = ns + lanes_below(bal);
       if (pass && sl < (unsigned)SCAP) {
-        svec[w][sl] = raw[i];
-        sidx[w][sl] = (int)threadIdx.x + i * NTT;
+        sh.svec[w][sl] = raw[i];
+        sh.sidx[w][sl] = (int)threadIdx.x + i * NTT;
       }
       ns += (unsigned)__popcll(bal);
     }
-  }
-  if (ns > (unsigned)SCAP && lane == 0) spill = 1;
-  wave_lds_sync();
+    if (ns > (unsigned)SCAP && lane == 0) sh.spill = 1;
+    wave_lds_sync();
 
-  // ---- 4. the staged vectors (one per lane) and the history ids: exact
-  // canonical logits, history ids left to their producers, into the
-  // candidate buffer; the high half of the packed counter counts candidates
-  // strictly above yc
-  {
+    // ---- 4. the staged vectors (one per lane): exact canonical logits,
+    // history ids left to their producers, into the candidate buffer
     const unsigned nst = ns < (unsigned)SCAP ? ns : (unsigned)SCAP;
     for (unsigned s0 = 0; s0 < nst; s0 += 64) {
       const unsigned si = s0 + (unsigned)lane;
@@ -581,8 +786,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       uint4 v = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);
       int j = 0;
       if (si < nst) {
-        v = svec[w][si];
-        j = sidx[w][si];
+        v = sh.svec[w][si];
+        j = sh.sidx[w][si];
       }
       const int o = j * EPV;
       const uint32_t hw = (pen && si < nst) ? HB::of(bitmap, j) : 0u;
@@ -596,41 +801,34 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
                 j < nvec;
         x[e] = comp_key(tg_key(y), v0 + o + e);
       }
-      append_n<EPV>(x, ok, kc, buf, &nbuf);
+      append_n<EPV>(x, ok, buf, &sh.nbuf);
     }
   }
-  u64 hcomp[NHID];
   {
     bool hok[NHID];
 #pragma unroll
-    for (int q = 0; q < NHID; q++) {
-      u64 x = 0ull;
-      if (hslot[q] >= 0) {
-        const int id = hid[q];
-        const float y = row_y(r, penalise(zq[q], hash[hslot[q]].y, r));
-        const bool ok = y > -__builtin_inff() && (!masked || ((mq[q] >> (id & 31)) & 1u));
-        if (ok) x = comp_key(tg_key(y), id);
-        if (a.dbg.post_logits) a.dbg.post_logits[(long long)b * a.V + id] = ok ? y : -__builtin_inff();
-      }
-      hcomp[q] = x;
-      hok[q] = x != 0ull && (uint32_t)(x >> 32) >= kc;
-    }
-    append_n<NHID>(hcomp, hok, kc, buf, &nbuf);
+    for (int q = 0; q < NHID; q++) hok[q] = hcomp[q] != 0ull && (uint32_t)(hcomp[q] >> 32) >= kc;
+    append_n<NHID>(hcomp, hok, buf, &sh.nbuf);
   }
+  if (threadIdx.x == NTT - 1) sh.elect = a.S > 1 && arrived == (unsigned)(a.S - 1);
   __syncthreads();
 
-  // ---- 5. the chunk's sorted top k: from the candidates when they hold at
-  // least k entries strictly above yc (then no id left out can be among the
-  // top k) or every allowed id; otherwise the exact path
-  u64 acc;
-  const int nb = (int)(nbuf & 0xFFFFu), nab = (int)(nbuf >> 16);
-  if (!spill && nb <= CAP && (all || nab >= k)) {
-    acc = select_top<NTT>(buf, nb, k, slots);
-  } else {
-    // exact path (rare: quotients that collide, skewed chunks): the k-th
-    // composite of the chunk by radix selection over the
-    // chunk read again (L2 / MALL hits), then the k entries at or above it
-    acc = exact_top<Tin, NTT, MASK>(a, r, rowp, nvec, pen, bitmap, masked, hcomp, k, buf, &nbuf, slots, bs);
+  // ---- 5. the chunk's list: its candidates as they stand when a split row
+  // shares the row-wide bound and they number at most 64, else its sorted
+  // top k (from the candidates, or from the exact path)
+  const int nb = (int)sh.nbuf;
+  const bool exact = sh.spill || nb > CAP;
+  const bool raw_list = a.S > 1 && a.xchg && !exact && nb <= KM;
+  u64 acc = 0ull;
+  if (!raw_list) {
+    if (!exact) {
+      acc = select_top<NTT>(buf, nb, k, sh.slots);
+    } else {
+      // exact path (rare: quotients that collide, skewed chunks): the k-th
+      // composite of the chunk by radix selection over the chunk read again
+      // (L2 / MALL hits), then the k entries at or above it
+      acc = exact_top<Tin, NTT, MASK>(a, r, rowp, nvec, pen, bitmap, masked, hcomp, k, buf, &sh.nbuf, sh.slots, sh.bs);
+    }
   }
   if (a.dbg.post_logits) post_logits_chunk<Tin, NTT>(a, r, rowp, nvec, pen, bitmap, masked);
 
@@ -642,57 +840,156 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     }
     return;
   }
-  u64* lists = a.lists + (long long)b * a.S * KM;
-  if (!elect) {
-    // publish the chunk's list for the row's merging workgroup
-    if (w == 0) __hip_atomic_store(lists + (long long)c * KM + lane, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  u64* lists = a.lists + (long long)b * K64_MAX_SPLIT * KM;
+  u64* cw = (u64*)(cnt + K64_CNT_WORDS);  // the row's count words, one per chunk
+  if (!sh.elect) {
+    // publish the chunk's list (entries, then its count word) and leave
+    if (raw_list) {
+      for (int t = threadIdx.x; t < nb; t += NTT)
+        __hip_atomic_store(lists + (long long)c * KM + t, tag_entry(buf[t], ep), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0)
+        __hip_atomic_store(cw + c, ((u64)ep << 32) | (u64)nb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (w == 0) {
+      const int n = __popcll(__ballot(acc != 0ull));
+      if (lane < n)
+        __hip_atomic_store(lists + (long long)c * KM + lane, tag_entry(acc, ep), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0)
+        __hip_atomic_store(cw + c, ((u64)ep << 32) | 0x100u | (u64)n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     return;
   }
-  // the row's last arrival: one list per wave (own list from wave 0's
-  // registers through LDS), polled in parallel, then a tree of merges
-  u64* own = slots[NW - 1];
-  if (w == 0) own[lane] = acc;
-  __syncthreads();
-  u64 racc = 0ull;
-  bool first = true;
-  for (int cc = w; cc < a.S; cc += NW) {
-    u64 x;
-    if (cc == c) {
-      x = own[lane];
-    } else {
-      const u64* lp = lists + (long long)cc * KM + lane;
-      x = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      int spins = 0;
-      while (__ballot(x == EMPTY) != 0ull) {
-        if (++spins > SPIN_LIMIT) {
-          if (lane == 0) tmo = 1;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        x = __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (x == EMPTY) x = 0ull;
-    }
-    racc = first ? x : wave_merge_top64(racc, x);
-    first = false;
-  }
-  __syncthreads();  // own[] (a slot of the merge tree) read by its wave
-  racc = merge_waves<NW>(racc, slots);
+
+  // ---- the row's last arrival: its own list stays in LDS.  Wave 0 reads
+  // every other chunk's count word and the first E = 128 / S entries of its
+  // list in one round of requests (two entries per lane), polled until each
+  // count word and each entry below its count holds the call's tag.  When
+  // the lists hold at most 64 entries, none beyond its first E, they are
+  // laid end to end in LDS and ranked there (an entry's rank is the number
+  // of entries above it); otherwise every wave takes part in a tree of wave
+  // merges over the lists read again.
   if (w == 0) {
-    if (tmo) {
-      if (lane == 0) {
-        a.out[b] = -4;
-        write_row_diag(a, b, 0, 0, 0, 0, -1);
+    const int own_n = raw_list ? nb : __popcll(__ballot(acc != 0ull));
+    if (!raw_list) sh.own[lane] = acc;
+    const int E = 128 / a.S;  // S <= 16: E >= 8
+    const bool cl = lane < a.S && lane != c;  // this lane polls list `lane`'s count word
+    int ec[2], epo[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int idx = lane + 64 * j;
+      ec[j] = idx < a.S * E ? idx / E : -1;
+      epo[j] = idx % E;
+      if (ec[j] == c) ec[j] = -1;  // the own list is in LDS
+    }
+    u64 cwv = cl ? __hip_atomic_load(cw + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ((u64)ep << 32);
+    u64 ent[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      ent[j] = ec[j] >= 0 ? __hip_atomic_load(lists + (long long)ec[j] * KM + epo[j], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : EMPTY;
+    bool tmo = false;
+    int ncl = 0;  // lanes below S: that list's entries
+    int nce[2] = {0, 0};  // entries of the list of each slot
+    for (int spins = 0;; spins++) {
+      const bool cok = (uint32_t)(cwv >> 32) == ep;
+      ncl = cok ? (int)(cwv & 0xFFu) : 0;
+      bool pend = cl && !cok;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int src = ec[j] >= 0 ? ec[j] : 0;
+        const int okc = __shfl((int)cok, src, 64);
+        nce[j] = __shfl(ncl, src, 64);
+        if (ec[j] >= 0) pend = pend || !okc || (epo[j] < nce[j] && !entry_ok(ent[j], ep));
       }
-    } else {
-      const int nr = __popcll(__ballot(racc != 0ull));
-      wave_finish_row(a, r, lane < k ? racc : 0ull, nr < k ? nr : k);
+      if (__ballot(pend) == 0ull) break;
+      if (spins >= SPIN_LIMIT) {
+        tmo = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      if (cl && !cok) cwv = __hip_atomic_load(cw + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        if (ec[j] >= 0 && !entry_ok(ent[j], ep))
+          ent[j] = __hip_atomic_load(lists + (long long)ec[j] * KM + epo[j], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ncl = ncl < KM ? ncl : KM;
+    if (lane == c) ncl = own_n;
+    if (lane >= a.S) ncl = 0;
+    if (lane < a.S) {
+      sh.lcnt[lane] = ncl;
+      sh.lsort[lane] = lane == c ? (raw_list ? 0 : 1) : (int)((cwv >> 8) & 1u);
+    }
+    const int incl = (int)wave_incl_scan((uint32_t)ncl);
+    const int total = (int)readlane_u32((uint32_t)incl, 63);
+    const int maxn = (int)wave_max((uint32_t)(lane == c ? 0 : ncl));
+    const bool fast = !tmo && total <= KM && maxn <= E;
+    if (fast) {
+      // the lists end to end: list q from the sum of the counts before it
+      const int off = incl - ncl;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int src = ec[j] >= 0 ? ec[j] : 0;
+        const int o = __shfl(off, src, 64);
+        if (ec[j] >= 0 && epo[j] < nce[j]) {
+          sh.mer[o + epo[j]] = untag_entry(ent[j]);
+          __hip_atomic_store(lists + (long long)ec[j] * KM + epo[j], EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      const int oo = __shfl(off, c, 64);
+      if (lane < own_n) sh.mer[oo + lane] = raw_list ? buf[lane] : sh.own[lane];
+      if (lane == 0) sh.mer[total] = 0ull;  // pad: the ranking reads pairs
+    }
+    if (lane == 0) {
+      sh.fast = fast ? total : -1;
+      if (tmo) sh.tmo = 1;
     }
   }
-  // ready for the next call: lists empty, counter zero
-  for (int cc = w; cc < a.S; cc += NW)
-    if (cc != c) __hip_atomic_store(lists + (long long)cc * KM + lane, EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int nfast = sh.fast;
+  if (nfast >= 0) {
+    if (w == 0) {
+      const u64 x = lane < nfast ? sh.mer[lane] : 0ull;
+      int rk = 0;
+      const u64x2* q = (const u64x2*)sh.mer;
+      for (int j = 0; j < (nfast + 1) / 2; j++) {
+        const u64x2 e = q[j];
+        rk += (e.x > x) + (e.y > x);
+      }
+      if (lane < nfast) sh.mer2[rk] = x;
+      wave_lds_sync();
+      const u64 y = lane < nfast ? sh.mer2[lane] : 0ull;
+      finish_merged(a, r, y, k, false);
+    }
+  } else {
+    // a tree of wave merges: wave w takes lists w, w + NW, ...
+    u64 racc = 0ull;
+    bool first = true, tmo = false;
+    for (int cc = w; cc < a.S; cc += NW) {
+      const int n = sh.lcnt[cc];
+      u64 x;
+      if (cc == c) {
+        x = lane < n ? (raw_list ? buf[lane] : sh.own[lane]) : 0ull;
+      } else {
+        x = take_entry(lists + (long long)cc * KM + lane, lane < n, ep, &tmo);
+      }
+      if (!sh.lsort[cc]) x = wave_sort_desc(x);
+      racc = first ? x : wave_merge_top64(racc, x);
+      first = false;
+    }
+    if (tmo && lane == 0) sh.tmo = 1;
+    racc = merge_waves<NW>(racc, sh.slots);
+    if (w == 0) finish_merged(a, r, racc, k, sh.tmo != 0);
+  }
+  // ready for the next call: counter zero, epoch advanced (entries were
+  // cleared as they were read)
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(cnt + 1, ep == 0xFFFFFFFFu ? 0u : ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 template <typename Tin, int NTT>
@@ -704,6 +1001,22 @@ hipError_t launch_n(const SampleArgs& a, size_t lds, hipStream_t st) {
   else if (mask) hipLaunchKernelGGL((k64_kernel<Tin, NTT, false, true>), g, blk, lds, st, a);
   else hipLaunchKernelGGL((k64_kernel<Tin, NTT, false, false>), g, blk, lds, st, a);
   return hipGetLastError();
+}
+
+// Workgroups of the K64_NT instantiation one CU holds at once with lds bytes
+// of dynamic LDS (0 when the runtime cannot say).
+template <typename Tin>
+int resident_n(bool vec, bool mask, size_t lds) {
+  const void* f = vec && mask ? (const void*)k64_kernel<Tin, K64_NT, true, true>
+                  : vec       ? (const void*)k64_kernel<Tin, K64_NT, true, false>
+                  : mask      ? (const void*)k64_kernel<Tin, K64_NT, false, true>
+                              : (const void*)k64_kernel<Tin, K64_NT, false, false>;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, K64_NT, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
 }
 
 template <typename Tin, int NTT>
@@ -727,6 +1040,12 @@ hipError_t set_lds(size_t bytes) {
 int k64_chunk_ids(int dtype) { return K64_NT * K64_NVT * (dtype == 1 ? 8 : 4); }
 
 int k64_small_ids(int dtype) { return K64_SMALL_NT * K64_NVT * (dtype == 1 ? 8 : 4); }
+
+size_t k64_static_lds() { return sizeof(k64::Shared<K64_NT / 64>); }
+
+int k64_resident_per_cu(int dtype, bool whole_vec, bool mask, size_t lds) {
+  return dtype == 1 ? k64::resident_n<uint16_t>(whole_vec, mask, lds) : k64::resident_n<float>(whole_vec, mask, lds);
+}
 
 hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st, bool small) {
   if (small)

@@ -11,8 +11,10 @@ namespace tgs {
 // Fused top_k <= 64 kernel: threads per workgroup, 16-byte vectors per
 // thread (a chunk is at most K64_NT x K64_NVT vectors), longest history it
 // takes, candidate buffer entries (u64; 16 more are reserved for ranking
-// pads), chunks per row at most, and the stride (in unsigned words) between
-// the per-row arrival counters (one 128-byte line each).
+// pads), chunks per row at most, the stride (in unsigned words) between the
+// per-row exchange lines (word 0 the arrival counter, word 1 the epoch word,
+// from word K64_CNT_WORDS on one 64-bit count word per chunk), and the
+// bound-exchange keys per row.
 constexpr int K64_NT = 256;
 constexpr int K64_NVT = 16;
 constexpr int K64_MAX_HIST = 1024;
@@ -20,7 +22,9 @@ constexpr int K64_SMALL_NT = 64;        // one-wave variant for rows of one smal
 constexpr int K64_SMALL_MAX_HIST = 256;  // its longest history
 constexpr int K64_CAP = 2048;
 constexpr int K64_MAX_SPLIT = 16;
-constexpr int K64_CNT_STRIDE = 32;
+constexpr int K64_CNT_STRIDE = 64;
+constexpr int K64_CNT_WORDS = 32;
+constexpr int K64_KEYS = 256;
 
 // Top-p kernel (rows without a top-k): threads per workgroup and the most
 // ids of one histogram bucket ranked in LDS.
@@ -54,8 +58,13 @@ struct SampleArgs {
   unsigned long long* ws;  // [B*S][ws_stride] chunk candidate lists
   int ws_stride;         // entries per chunk list (64 fast variant, KMAX otherwise)
   int* ws_cnt;           // [B*S]
-  unsigned* cnt;         // fused kernel: [B * K64_CNT_STRIDE] arrival counters (zero between calls)
-  unsigned long long* lists;  // fused kernel: [B * S][64] chunk lists (all ~0 between calls)
+  unsigned* cnt;         // fused kernel: [B * K64_CNT_STRIDE] exchange lines (counter zero between calls)
+  unsigned long long* lists;  // fused kernel: [B][K64_MAX_SPLIT][64] chunk lists (entries 0 between calls)
+  unsigned long long* keys;   // fused kernel: [B][K64_KEYS] bound-exchange keys
+  int xchg;              // fused kernel: split rows share a row-wide bound (the grid is resident at once)
+  int kq;                // fused kernel: keys each wave publishes (S * 4 * kq <= K64_KEYS, >= 64)
+  int xmap;              // fused kernel: a row's chunks are workgroups congruent mod 8 (B a multiple of 8)
+  int key_spins;         // fused kernel: polls of the row's keys before a wave keeps its chunk's bound
   int full_rows;         // 1: full_kernel runs after the chunk kernels
   int hint_k;            // the launch hint's max_top_k (INT_MAX without a hint)
   int topp_all;          // 1: the top-p kernel alone serves the batch (its greedy rows too)
@@ -152,6 +161,11 @@ int k64_chunk_ids(int dtype);
 // most k64_small_ids(dtype) ids, history <= K64_SMALL_MAX_HIST).
 int k64_small_ids(int dtype);
 hipError_t launch_k64(const SampleArgs& a, int dtype, size_t lds, hipStream_t st, bool small = false);
+// Workgroups of the K64_NT instantiation that one CU holds at once with lds
+// bytes of dynamic LDS (0 when the runtime cannot tell).
+int k64_resident_per_cu(int dtype, bool whole_vec, bool mask, size_t lds);
+// Static LDS of the K64_NT instantiation.
+size_t k64_static_lds();
 hipError_t set_k64_lds_limit(size_t bytes);
 hipError_t launch_spec(const SpecArgs& a, int dtype, hipStream_t st);
 // Rows sampling top-p over the whole vocabulary (top_k disabled).
