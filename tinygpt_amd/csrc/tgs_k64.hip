@@ -104,6 +104,7 @@ struct Shared {
   int elect, tmo, spill;
   int lcnt[K64_MAX_SPLIT];     // merging workgroup: entries of each chunk's list
   int lsort[K64_MAX_SPLIT];    // 1: that list is sorted
+  int lz[K64_MAX_SPLIT];       // 1: that list holds logits before the temperature
   int fast;                    // merging workgroup: entries laid out in mer (-1: the merge tree)
   uint32_t rkey;               // the row-wide bound key (0: none)
   alignas(16) u64 mer[66];     // merging workgroup: the lists end to end (+ a pad entry)
@@ -177,22 +178,24 @@ __device__ __forceinline__ bool keys_current(const RowKeys<NJ>& K, int nk, uint3
   return __ballot(stale) == 0ull;
 }
 
-// The row-wide bound key: one wave polls the row's nk keys until every key
-// holds the call's tag, then takes their k-th largest to 20 bits (the
-// largest multiple of 2^12 that at least k of them reach, one wave-wide
-// count per bit; 2^-11 of relative slack).  Returns 0 (no bound) when
-// max_spins polls did not see every key.
-template <int NJ>
-__device__ __forceinline__ uint32_t row_bound(const u64* keys, int nk, uint32_t ep, int k, int max_spins) {
-  const int lane = lane_id();
-  RowKeys<NJ> K;
-  keys_issue(K, keys, nk);
+// One wave polls the row's nk keys K (requested earlier by the caller)
+// until every key holds the call's tag; false when max_spins polls did not
+// see every key.
+__device__ __forceinline__ bool keys_wait(RowKeys<4>& K, const u64* keys, int nk, uint32_t ep, int max_spins) {
   for (int spins = 0;; spins++) {
-    if (keys_current(K, nk, ep)) break;
-    if (spins >= max_spins) return 0u;
+    if (keys_current(K, nk, ep)) return true;
+    if (spins >= max_spins) return false;
     __builtin_amdgcn_s_sleep(1);
     keys_issue(K, keys, nk);
   }
+}
+
+// The k-th largest of the row's keys (NJ = ceil(nk / 64) slots per lane), to
+// 20 bits: the largest multiple of 2^12 that at least k of them reach, one
+// wave-wide count per bit (2^-11 of relative slack).
+template <int NJ>
+__device__ __forceinline__ uint32_t keys_kth(const RowKeys<4>& K, int nk, int k) {
+  const int lane = lane_id();
   uint32_t kk[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; j++) kk[j] = lane + 64 * j < nk ? (uint32_t)K.e[j] : 0u;
@@ -206,6 +209,18 @@ __device__ __forceinline__ uint32_t row_bound(const u64* keys, int nk, uint32_t 
     X = n >= k ? t : X;
   }
   return X;
+}
+
+// The candidate buffer holds composites of the logits before the
+// temperature (z, or the penalised z of a history id): z / T is monotone in
+// z, so the collection threshold applies to them exactly, and only a
+// selection needs the canonical logit's order (distinct z can share one
+// y = z / T, whose ties go to the lower id).  y-composite of a z-composite
+// (0: none, or y = -inf, which is not allowed).
+__device__ __forceinline__ u64 z_to_y(u64 x, const Row& r) {
+  if (x == 0ull) return 0ull;
+  const float y = row_y(r, tg_unkey((uint32_t)(x >> 32)));
+  return y > -__builtin_inff() ? comp_key(tg_key(y), comp_id(x)) : 0ull;
 }
 
 // A list entry: composite x with the epoch's low bits between its key and
@@ -713,10 +728,13 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     if (w == 0) {
       // wave 0 polls for the workgroup
       const int nk = a.S * NW * a.kq;
-      const u64* rk_keys = a.keys + (long long)b * K64_KEYS;
-      const uint32_t rk = nk <= 64    ? row_bound<1>(rk_keys, nk, ep, k, a.key_spins)
-                          : nk <= 128 ? row_bound<2>(rk_keys, nk, ep, k, a.key_spins)
-                                      : row_bound<4>(rk_keys, nk, ep, k, a.key_spins);
+      RowKeys<4> rkeys;
+      uint32_t rk = 0u;
+      // (a first poll issued as soon as the keys went out measured slower:
+      // it mostly returns before the row's other keys are out)
+      keys_issue(rkeys, a.keys + (long long)b * K64_KEYS, nk);
+      if (keys_wait(rkeys, a.keys + (long long)b * K64_KEYS, nk, ep, a.key_spins))
+        rk = nk <= 64 ? keys_kth<1>(rkeys, nk, k) : nk <= 128 ? keys_kth<2>(rkeys, nk, k) : keys_kth<4>(rkeys, nk, k);
       if (lane == 0) sh.rkey = rk;
     }
     __syncthreads();  // also publishes the table
@@ -730,21 +748,24 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   const bool all = bkey < KEY_MIN + 32u;  // no usable bound: collect every allowed id
   const float cz = all ? -__builtin_inff() : tg_unkey(bkey - 16u);
   const float yc = all ? -__builtin_inff() : row_y(r, cz);
-  const uint32_t kc = tg_key(yc);
+  const uint32_t kcz = tg_key(cz);  // z-composites at or above it are candidates
   // quotients that collide at the bound: the exact path
   if (!all && !(row_y(r, tg_unkey(bkey)) > yc) && lane == 0) sh.spill = 1;
-  // the producers' composites (their penalised canonical logits; the loads
-  // went out before the bound)
+  // the producers' composites (their penalised logits; the loads went out
+  // before the bound)
   u64 hcomp[NHID];
 #pragma unroll
   for (int q = 0; q < NHID; q++) {
     u64 x = 0ull;
     if (hslot[q] >= 0) {
       const int id = hid[q];
-      const float y = row_y(r, penalise(zq[q], hash[hslot[q]].y, r));
-      const bool ok = y > -__builtin_inff() && (!masked || ((mq[q] >> (id & 31)) & 1u));
-      if (ok) x = comp_key(tg_key(y), id);
-      if (a.dbg.post_logits) a.dbg.post_logits[(long long)b * a.V + id] = ok ? y : -__builtin_inff();
+      const float zp = penalise(zq[q], hash[hslot[q]].y, r);
+      const bool okm = !masked || ((mq[q] >> (id & 31)) & 1u);
+      if (okm && zp > -__builtin_inff()) x = comp_key(tg_key(zp), id);  // (NaN fails the compare)
+      if (a.dbg.post_logits) {
+        const float y = row_y(r, zp);
+        a.dbg.post_logits[(long long)b * a.V + id] = (okm && y > -__builtin_inff()) ? y : -__builtin_inff();
+      }
     }
     hcomp[q] = x;
   }
@@ -796,10 +817,9 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
 #pragma unroll
       for (int e = 0; e < EPV; e++) {
         const float z = Elem<Tin>::get(v, e);
-        const float y = row_y(r, z);
-        ok[e] = si < nst && z >= cz && !((hw >> e) & 1u) && !((xm >> e) & 1u) && y > -__builtin_inff() &&
+        ok[e] = si < nst && z >= cz && z > -__builtin_inff() && !((hw >> e) & 1u) && !((xm >> e) & 1u) &&
                 j < nvec;
-        x[e] = comp_key(tg_key(y), v0 + o + e);
+        x[e] = comp_key(tg_key(z), v0 + o + e);
       }
       append_n<EPV>(x, ok, buf, &sh.nbuf);
     }
@@ -807,7 +827,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   {
     bool hok[NHID];
 #pragma unroll
-    for (int q = 0; q < NHID; q++) hok[q] = hcomp[q] != 0ull && (uint32_t)(hcomp[q] >> 32) >= kc;
+    for (int q = 0; q < NHID; q++) hok[q] = hcomp[q] != 0ull && (uint32_t)(hcomp[q] >> 32) >= kcz;
     append_n<NHID>(hcomp, hok, buf, &sh.nbuf);
   }
   if (threadIdx.x == NTT - 1) sh.elect = a.S > 1 && arrived == (unsigned)(a.S - 1);
@@ -821,7 +841,14 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   const bool raw_list = a.S > 1 && a.xchg && !exact && nb <= KM;
   u64 acc = 0ull;
   if (!raw_list) {
+    // a selection orders by the canonical logit: the candidates (and the
+    // producers' composites, which the exact path enumerates) become
+    // y-composites first
+#pragma unroll
+    for (int q = 0; q < NHID; q++) hcomp[q] = z_to_y(hcomp[q], r);
     if (!exact) {
+      for (int t = threadIdx.x; t < nb; t += NTT) buf[t] = z_to_y(buf[t], r);
+      __syncthreads();
       acc = select_top<NTT>(buf, nb, k, sh.slots);
     } else {
       // exact path (rare: quotients that collide, skewed chunks): the k-th
@@ -848,8 +875,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       for (int t = threadIdx.x; t < nb; t += NTT)
         __hip_atomic_store(lists + (long long)c * KM + t, tag_entry(buf[t], ep), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-      if (threadIdx.x == 0)
-        __hip_atomic_store(cw + c, ((u64)ep << 32) | (u64)nb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0)  // 0x200: entries hold logits before the temperature
+        __hip_atomic_store(cw + c, ((u64)ep << 32) | 0x200u | (u64)nb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if (w == 0) {
       const int n = __popcll(__ballot(acc != 0ull));
       if (lane < n)
@@ -922,6 +949,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     if (lane < a.S) {
       sh.lcnt[lane] = ncl;
       sh.lsort[lane] = lane == c ? (raw_list ? 0 : 1) : (int)((cwv >> 8) & 1u);
+      sh.lz[lane] = lane == c ? (raw_list ? 1 : 0) : (int)((cwv >> 9) & 1u);
     }
     const int incl = (int)wave_incl_scan((uint32_t)ncl);
     const int total = (int)readlane_u32((uint32_t)incl, 63);
@@ -934,14 +962,16 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       for (int j = 0; j < 2; j++) {
         const int src = ec[j] >= 0 ? ec[j] : 0;
         const int o = __shfl(off, src, 64);
+        const int zl = __shfl((int)((cwv >> 9) & 1u), src, 64);
         if (ec[j] >= 0 && epo[j] < nce[j]) {
-          sh.mer[o + epo[j]] = untag_entry(ent[j]);
+          const u64 xe = untag_entry(ent[j]);
+          sh.mer[o + epo[j]] = zl ? z_to_y(xe, r) : xe;
           __hip_atomic_store(lists + (long long)ec[j] * KM + epo[j], EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
       const int oo = __shfl(off, c, 64);
-      if (lane < own_n) sh.mer[oo + lane] = raw_list ? buf[lane] : sh.own[lane];
-      if (lane == 0) sh.mer[total] = 0ull;  // pad: the ranking reads pairs
+      if (lane < own_n) sh.mer[oo + lane] = raw_list ? z_to_y(buf[lane], r) : sh.own[lane];
+      if (lane >= total) sh.mer[lane] = 0ull;  // pads: never above an entry
     }
     if (lane == 0) {
       sh.fast = fast ? total : -1;
@@ -952,16 +982,18 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   const int nfast = sh.fast;
   if (nfast >= 0) {
     if (w == 0) {
-      const u64 x = lane < nfast ? sh.mer[lane] : 0ull;
+      const u64 x = sh.mer[lane];
       int rk = 0;
       const u64x2* q = (const u64x2*)sh.mer;
-      for (int j = 0; j < (nfast + 1) / 2; j++) {
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
         const u64x2 e = q[j];
         rk += (e.x > x) + (e.y > x);
       }
-      if (lane < nfast) sh.mer2[rk] = x;
+      if (lane < nfast && x != 0ull) sh.mer2[rk] = x;
       wave_lds_sync();
-      const u64 y = lane < nfast ? sh.mer2[lane] : 0ull;
+      const int nv = __popcll(__ballot(lane < nfast && x != 0ull));  // entries left after z / T
+      const u64 y = lane < nv ? sh.mer2[lane] : 0ull;
       finish_merged(a, r, y, k, false);
     }
   } else {
@@ -976,6 +1008,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       } else {
         x = take_entry(lists + (long long)cc * KM + lane, lane < n, ep, &tmo);
       }
+      if (sh.lz[cc]) x = z_to_y(x, r);
       if (!sh.lsort[cc]) x = wave_sort_desc(x);
       racc = first ? x : wave_merge_top64(racc, x);
       first = false;
