@@ -26,14 +26,19 @@ same generator set (tinygpt_amd/workloads.py):
       pace-fm-response-v11 schema per call, local DFA on the host and rows on
       the device (tinygpt_amd.json_schema), V=151,936; timed eagerly (host work
       inside each call)
+  read  the plain read of C2's logits with the fused kernel's grid and load
+      pattern (libtgs_floor.so): the floor under the headline.  The default
+      c2 line carries it and c2m as sub-objects ("read_floor", "c2m"), timed
+      the same way (--no-c2m leaves both out)
 
 Inputs are resident in HBM before timing; distinct input sets rotate so the
 256 MB Infinity Cache cannot serve repeats (at least 512 MB in rotation
-where a set is large).  The calls are captured in HIP graphs (one call per
-set; a second graph holds the remainder when --steps is not a multiple of
-the rotation) and replayed so that exactly --steps calls are timed; the
-timed region is bracketed by synchronisations and HIP events on the launch
-stream.  Then 256 eager calls, each between two HIP events, give the per-call
+where a set is large).  The calls are captured in one HIP graph of --steps calls
+cycling over the sets (above 4096 steps: a graph of at most 4096 calls
+replayed, plus one graph of the remainder) so that exactly --steps calls are
+timed; an untimed replay of the same graph goes first, so the timed calls
+queue behind GPU work as they would behind a model's forward pass.  The timed
+region is bracketed by synchronisations and HIP events on the launch stream.  Then 256 eager calls, each between two HIP events, give the per-call
 p10 / p50 / p90.
 
 Prints one JSON line with the roofline of the call, the CPU oracle timed on
@@ -69,7 +74,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c2m", "c3", "c4", "c5", "lp", "mask", "json", "jsondec"])
+    ap.add_argument("--workload", default="c2",
+                    choices=["c1", "c2", "c2m", "c3", "c4", "c5", "lp", "mask", "json", "jsondec", "read"])
+    ap.add_argument("--no-c2m", action="store_true", help="leave the masked chain out of the default c2 line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
@@ -698,6 +705,45 @@ class JsonDecode:
         return fn
 
 
+class FloorRead:
+    """read: the plain-read floor under the C2 headline.  The same 16
+    rotating 64 x 128256 fp32 sets, read by libtgs_floor.so with the fused
+    top_k <= 64 kernel's grid and load pattern (8 chunks per row, 256
+    threads, 16 non-temporal 16-byte loads per thread at entry) and nothing
+    computed but each chunk's maximum: the time the sampling chain adds its
+    work to.  Not part of the sampler; no CPU baseline."""
+
+    def __init__(self, name, torch, tg, W):
+        import ctypes as C
+
+        dev = "cuda:0"
+        self.rot, self.B, self.V, self.S = 16, 64, 128256, 8
+        lib = C.CDLL(os.path.join(ROOT, "tinygpt_amd", "libtgs_floor.so"))
+        lib.tgs_floor_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_longlong, C.c_int, C.c_void_p, C.c_void_p]
+        lib.tgs_floor_read.restype = C.c_int
+        self.lib, self.C = lib, C
+        self.x = [torch.from_numpy(W.config2(B=self.B, V=self.V, seed_offset=i * 1000)["logits"]).to(dev)
+                  for i in range(self.rot)]
+        self.out = torch.empty(self.B * self.S, dtype=torch.float32, device=dev)
+        self.config = {"workload": "read_floor_c2", "B": self.B, "V": self.V, "chunks_per_row": self.S,
+                       "threads_per_chunk": 256, "loads": "16 non-temporal 16-byte loads per thread"}
+        self.dtype = "f32"
+        self.alg_bytes = 4 * self.V * self.B
+        self.units_per_step = self.B
+        self.unit = "rows/s"
+        self.metric = "rows/sec read by a plain read of the C2 logits (the floor under the headline)"
+
+    def launch(self, i, stream):
+        C = self.C
+        rc = self.lib.tgs_floor_read(C.c_void_p(self.x[i % self.rot].data_ptr()), self.B, self.V, self.V, self.S,
+                                     C.c_void_p(self.out.data_ptr()), C.c_void_p(stream))
+        if rc != 0:
+            raise RuntimeError(f"tgs_floor_read: {rc}")
+
+    def gpu_outputs(self):
+        return {}
+
+
 def cpu_baseline(wl, seconds):
     """The oracle (C restatement of the reference sampler) on this host:
     units/s with all host threads (up to 16) and with one thread."""
@@ -765,13 +811,85 @@ TRAFFIC_FILES["lp"] = "lp_scoring_traffic.json"
 TRAFFIC_FILES["c2m"] = "k64_kernel_c2m_traffic.json"
 TRAFFIC_FILES["json"] = "json_rows_traffic.json"
 TRAFFIC_FILES["mask"] = "mask_rows_traffic.json"
-KERNELS = {"c1": "k64_kernel<float> (one-wave)", "c2": "k64_kernel<float>", "c2m": "k64_kernel<float> (mask variant)",
+TRAFFIC_FILES["read"] = "read_floor_c2_traffic.json"
+KERNELS = {"read": "floor_read_kernel (libtgs_floor.so)", "c1": "k64_kernel<float> (one-wave)", "c2": "k64_kernel<float>", "c2m": "k64_kernel<float> (mask variant)",
            "c3": "topp_kernel<float, true>",
            "c4": "topk_kernel<bf16, 20>",
            "c5": "spec_block_kernel + spec_decide_kernel + spec_mass_kernel + spec_draw_kernel (one call)",
            "lp": "lp::chunk_kernel<float>", "mask": "maskb::prep_image + maskb::build_lds (one call)",
            "json": "host local DFA + maskb kernels (one call)",
            "jsondec": "host automaton + mask rows + topp_kernel per step"}
+
+
+def time_calls(torch, wl, stream, steps, eager):
+    """GPU time per call of `steps` calls of wl, between two events on the
+    launch stream.  Graph replay: the timed calls are one captured graph of
+    `per` calls (cycling over the rotating input sets), replayed `reps` times;
+    per = steps up to 4096 calls, so that a short run launches one graph.
+    Returns (ms per call, the graph or None)."""
+    ROT = wl.rot
+    per = steps if steps <= 4096 else ROT * max(1, 4096 // ROT)
+    reps, rem = divmod(steps, per)
+
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+            for i in range(n):
+                wl.launch(i, stream.cuda_stream)
+        torch.cuda.synchronize()
+        return g
+
+    graph = graph_rem = None
+    if not eager:
+        graph = capture(per) if reps else None
+        graph_rem = capture(rem) if rem else None
+        for g in (graph, graph_rem):
+            if g is not None:
+                g.replay()
+        torch.cuda.synchronize()
+
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        # The same calls, untimed, ahead of the start event keep the GPU busy
+        # while the host submits the timed graph, so the timed region holds
+        # the K calls alone (in a decode loop the sampler is queued behind
+        # the model's forward pass the same way).
+        if not eager:
+            for g in (graph, graph_rem):
+                if g is not None:
+                    g.replay()
+        else:
+            torch.cuda._sleep(200000)
+        ev0.record(stream)
+        if not eager:
+            for _ in range(reps):
+                graph.replay()
+            if graph_rem is not None:
+                graph_rem.replay()
+        else:
+            for i in range(steps):
+                wl.launch(i, stream.cuda_stream)
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps, graph
+
+
+def sub_line(torch, wl, stream, steps, args, name):
+    """One more workload timed like the main line, reported as a sub-object."""
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            wl.launch(i, stream.cuda_stream)
+    torch.cuda.synchronize()
+    ms, graph = time_calls(torch, wl, stream, steps, args.eager)
+    achieved = wl.alg_bytes / (ms * 1e-3) / 1e9
+    return {"workload": wl.config["workload"], "us_per_call": round(ms * 1e3, 3),
+            "value": round(wl.units_per_step / (ms * 1e-3), 1), "unit": wl.unit,
+            "timing": "graph replay" if graph is not None else "eager", "steps": steps,
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "alg_bytes_per_launch": wl.alg_bytes,
+                         "kernel": KERNELS[name]}}
 
 
 def main():
@@ -802,6 +920,9 @@ def main():
     elif args.workload == "jsondec":
         wl = JsonDecode(args.workload, torch, tg, W)
         args.eager = True
+    elif args.workload == "read":
+        wl = FloorRead(args.workload, torch, tg, W)
+        args.no_cpu = True  # a measurement floor, not a sampler: nothing to compare
     else:
         wl = Sampling(args.workload, torch, tg, W)
     torch.cuda.synchronize()
@@ -816,56 +937,7 @@ def main():
     steps = max(1, args.steps)
     if isinstance(wl, (JsonRows, JsonDecode)):
         steps = min(steps, 64 if isinstance(wl, JsonRows) else 200)  # host work in every call
-    # Graph replay: the timed calls are one captured graph of `per` calls
-    # (cycling over the rotating input sets), replayed `reps` times; per =
-    # steps up to 4096 calls, so the driver's short runs launch one graph.
-    per = steps if steps <= 4096 else ROT * max(1, 4096 // ROT)
-    reps, rem = divmod(steps, per)
-
-    def capture(n):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
-            for i in range(n):
-                wl.launch(i, stream.cuda_stream)
-        torch.cuda.synchronize()
-        return g
-
-    graph = graph_rem = None
-    if not args.eager:
-        graph = capture(per) if reps else None
-        graph_rem = capture(rem) if rem else None
-        for g in (graph, graph_rem):
-            if g is not None:
-                g.replay()
-        torch.cuda.synchronize()
-
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        # The same calls, untimed, ahead of the start event keep the GPU busy
-        # while the host submits the timed graph, so the timed region holds
-        # the K calls alone (in a decode loop the sampler is queued behind
-        # the model's forward pass the same way).
-        if not args.eager:
-            for g in (graph, graph_rem):
-                if g is not None:
-                    g.replay()
-        else:
-            torch.cuda._sleep(200000)
-        ev0.record(stream)
-        if not args.eager:
-            for _ in range(reps):
-                graph.replay()
-            if graph_rem is not None:
-                graph_rem.replay()
-        else:
-            for i in range(steps):
-                wl.launch(i, stream.cuda_stream)
-        ev1.record(stream)
-    torch.cuda.synchronize()
-    ms_total = ev0.elapsed_time(ev1)
-    ms_per_step = ms_total / steps
+    ms_per_step, graph = time_calls(torch, wl, stream, steps, args.eager)
 
     # per-call distribution: eager calls, each between two events
     n_calls = 16 if isinstance(wl, (JsonRows, JsonDecode)) else 256
@@ -933,6 +1005,12 @@ def main():
         "parity": parity,
         "per_call_us": per_call_us,
     }
+    if args.workload == "c2" and not args.no_c2m:
+        # the same chain with the grammar mask stage, and the plain read of
+        # the same logits: both timed like the headline, on the same stream
+        line["c2m"] = sub_line(torch, Sampling("c2m", torch, tg, W), stream, steps, args, "c2m")
+        if os.path.exists(os.path.join(ROOT, "tinygpt_amd", "libtgs_floor.so")):
+            line["read_floor"] = sub_line(torch, FloorRead("read", torch, tg, W), stream, steps, args, "read")
     if isinstance(wl, SpecVerify):
         line["tokens_per_s"] = round(wl.tokens_per_step() / (ms_per_step * 1e-3), 1)
     if isinstance(wl, JsonDecode):

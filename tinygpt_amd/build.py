@@ -15,6 +15,10 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libtgs_sampler.so")
+# the plain-read floor kernel of bench.py --workload read (measurement only,
+# its own library: not part of the sampler's C ABI)
+FLOOR_SRC = "tgs_floor.hip"
+FLOOR_OUT = os.path.join(HERE, "libtgs_floor.so")
 SOURCES = ["tgs_kernels.hip", "tgs_k64.hip", "tgs_spec.hip", "tgs_topp.hip", "tgs_topk.hip", "tgs_logprob.hip",
            "tgs_mask.hip", "tgs_api.hip"]
 ARCH = os.environ.get("TGS_OFFLOAD_ARCH", "gfx950")
@@ -58,8 +62,9 @@ def build(verbose: bool = False) -> str:
         r = subprocess.run(cmd, capture_output=True, text=True)
         return src, obj, cmd, r
 
-    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        results = list(ex.map(compile_one, SOURCES))
+    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES) + 1)) as ex:
+        results = list(ex.map(compile_one, SOURCES + [FLOOR_SRC]))
+    floor = results.pop()
     msgs = []
     for src, obj, cmd, r in results:
         errors = "\n".join(l for l in (r.stderr or "").splitlines() if "packed-fp32-ops" not in l)
@@ -72,9 +77,18 @@ def build(verbose: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed ({r.returncode}):\n{' '.join(cmd)}\n{r.stderr}")
+    _, fobj, fcmd, fr = floor
+    if fr.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({fr.returncode}):\n{' '.join(fcmd)}\n{fr.stderr}")
+    ftmp = FLOOR_OUT + ".tmp"
+    r2 = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", fobj, "-o", ftmp], capture_output=True,
+                        text=True)
+    if r2.returncode != 0:
+        raise RuntimeError(f"link failed ({r2.returncode}):\n{r2.stderr}")
     if verbose and msgs:
         print("\n".join(msgs), file=sys.stderr)
     os.replace(tmp, OUT)
+    os.replace(ftmp, FLOOR_OUT)
     return OUT
 
 
