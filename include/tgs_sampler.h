@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define TGS_ABI_VERSION 3
+#define TGS_ABI_VERSION 4
 
 struct ihipStream_t;
 typedef struct ihipStream_t* tgs_stream;
@@ -163,7 +163,10 @@ int tgs_sample(tgs_handle h, const void* d_logits, tgs_dtype dt, int B, int V, i
  * ceil(mask_vocab / 32) words, mask_vocab >= V; NULL / 0 for none).  Its
  * workspace is a static device array of about 6 MiB that every GPU the
  * library runs on holds until the process ends; the first call on a device
- * also prepares that array (and synchronises the device once).  Limits:
+ * also prepares that array (and synchronises the device once), so it must
+ * not be made under graph capture (it then returns TGS_EINVAL): make it
+ * before capturing, with B = 0 if there is nothing to sample yet; every
+ * later call can be captured.  Limits:
  * B <= 256, V <= 262144, hist_cap <= 1024; beyond them it returns
  * TGS_ETOOBIG.  It calls no hipMalloc or hipFree.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (several streams,
@@ -205,7 +208,13 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
  *   d_trans      [n_dfa][n_cls] next state per class (-1 rejects)
  *   d_complete   [n_dfa] 1 for accepting states with no transition
  *   d_tok_off    [n_tokens + 1] offsets of each token's bytes in d_tok_bytes
+ *   d_tok_bytes  [n_bytes] the tokens' bytes (nullable when n_bytes = 0)
  *   d_states, d_rows [n] DFA states and the table rows to fill
+ * Token v's bytes are d_tok_bytes[off[v] .. off[v+1]); offsets are checked
+ * against the buffer on the device: a token whose range starts below 0,
+ * ends before it starts or ends past n_bytes is read as empty (never
+ * allowed), so no offset can make the kernels read outside d_tok_bytes.
+ * d_tok_off itself must hold n_tokens + 1 entries.
  * (the identity class map with n_cls = 256 passes a plain [n_dfa][256]
  * table).  The table (tgs_mask_table_set) must hold at least n_tokens ids;
  * bits of ids at or past n_tokens are cleared.  Rows outside the table are
@@ -215,8 +224,8 @@ int tgs_spec_verify(tgs_handle h, const void* d_target, const void* d_draft, tgs
  * one stream); allocates nothing. */
 int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int32_t* d_trans, int n_cls,
                            const uint8_t* d_complete, int n_dfa, const int32_t* d_tok_off,
-                           const uint8_t* d_tok_bytes, int n_tokens, int eos_id, const int32_t* d_states,
-                           const int32_t* d_rows, int n, tgs_stream stream);
+                           const uint8_t* d_tok_bytes, int64_t n_bytes, int n_tokens, int eos_id,
+                           const int32_t* d_states, const int32_t* d_rows, int n, tgs_stream stream);
 
 /* Log-probability of one given token per row under the softmax of the raw
  * logits: out_logprob[b] = x[b][tok[b]] - logsumexp(x[b]) (teacher-forced

@@ -12,7 +12,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "build", "libtgs_oracle.so")
+# TGS_ORACLE_LIB: another build of the same source (the sanitizer build of
+# tests/oracle_san), used as it is, without building
+LIB_PATH = os.environ.get("TGS_ORACLE_LIB") or os.path.join(HERE, "build", "libtgs_oracle.so")
 
 FLAG_GREEDY = 1
 
@@ -64,6 +66,8 @@ _lib = None
 
 def build() -> str:
     """Compile the oracle with its Makefile (gcc; no GPU needed)."""
+    if os.environ.get("TGS_ORACLE_LIB"):
+        return LIB_PATH
     subprocess.run(["make", "-s", "-C", HERE], check=True)
     return LIB_PATH
 

@@ -141,7 +141,7 @@ int main(int argc, char** argv) {
     if (rc) return 6;
     rc = tgs_mask_rows_from_dfa(h, (const uint8_t*)bcls.data(), (const int32_t*)trans.data(), n_cls,
                                 (const uint8_t*)comp.data(), n_dfa,
-                                (const int32_t*)off.data(), (const uint8_t*)bytes.data(), V, eos,
+                                (const int32_t*)off.data(), (const uint8_t*)bytes.data(), (int64_t)bytes.size(), V, eos,
                                 (const int32_t*)st.data(), (const int32_t*)rows.data(), n, nullptr);
     if (rc) { std::printf("maskbuild %d %s\n", rc, tgs_last_error(h)); return 7; }
     // read the rows back through greedy rows over zero logits

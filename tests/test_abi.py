@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.tgs_abi_version() == 3
+    assert lib.tgs_abi_version() == 4
     assert lib.tgs_status_string(0) == b"ok"
     assert b"invalid" in lib.tgs_status_string(-1)
     assert lib.tgs_status_string(12345) == b"unknown status"
@@ -57,7 +57,7 @@ def test_null_handle_calls_fail_cleanly(lib):
     assert lib.tgs_spec_verify(None, None, None, 0, None, 1, 1, 1, None, None, None, None, None, None) == -1
     assert lib.tgs_mask_table_set(None, None, 0, 1) == -1
     assert lib.tgs_token_logprobs(None, None, 0, 1, 1, 1, None, None, None, None) == -1
-    assert lib.tgs_mask_rows_from_dfa(None, None, None, 1, None, 1, None, None, 1, -1, None, None, 1, None) == -1
+    assert lib.tgs_mask_rows_from_dfa(None, None, None, 1, None, 1, None, None, 0, 1, -1, None, None, 1, None) == -1
     assert lib.tgs_last_error(None) == b"null handle"
     lib.tgs_destroy(None)
 

@@ -344,6 +344,51 @@ def test_mask_rows_from_dfa(sim, oracle):
 
 
 
+def test_mask_rows_offsets_outside_the_bytes(sim, oracle):
+    """Token offsets that do not give a range inside the byte buffer (a
+    negative start, a range that ends before it starts, an end past the
+    buffer, the last token running past it) read as empty tokens, never
+    allowed, under ASan with a byte buffer of exactly its length: no read
+    leaves it.  Every other token keeps the bytes its offsets give, and the
+    rows match the DFA replay oracle over those tokens, in both the LDS and
+    the global kernel."""
+    from tinygpt_amd import grammar as G
+
+    g = np.random.default_rng(82)
+    d = G.compile_gbnf(G.PACE_TOOL_TAGS)
+    pieces = [b"[", b"]", b"POINT", b":", b"none", b",", b"TYPE", b"up", b" ", b"12", b"x"]
+    toks = [b"".join(g.choice(pieces) for _ in range(g.integers(1, 4))) for _ in range(300)]
+    toks.append(b"[" + b"POINT:" * 4)  # longer than the bytes read up front
+    off, data = G.token_csr(toks)
+    off = off.astype(np.int64)
+    n = len(data)
+    off[10] = -5               # token 9 ends below 0, token 10 starts below 0
+    off[20] = off[19] - 1      # token 19 ends before it starts
+    off[30] = n + 1000         # token 29 ends past the buffer, token 30 starts past it
+    off[40] = off[42]          # token 39 longer, token 40 empty, token 41 intact
+    off[-1] = n + 7            # the last token runs past the buffer
+    off = off.astype(np.int32)
+    V = len(toks)
+    got_toks = []
+    for v in range(V):
+        s, e = int(off[v]), int(off[v + 1])
+        got_toks.append(bytes(data[s:e]) if 0 <= s < e <= n else b"")
+    for v in (9, 10, 19, 29, 30, 40, V - 1):
+        assert got_toks[v] == b""
+    hist = [b"", b"ok [", b"[POINT:1", b"[TYPE:ab", b"[POINT:none]"]
+    states = np.array([d.walk(0, h) for h in hist], np.int32)
+    rows = np.arange(len(hist), dtype=np.int32)
+    bc, ct = d.byte_classes()
+    want = oracle.dfa_mask_rows(d.trans, d.complete, got_toks, states, eos=3)
+    for byte_class, trans in ((bc, ct), (np.arange(256, dtype=np.uint8), d.trans)):
+        post = sim.run_maskbuild(byte_class, trans, d.complete.astype(np.uint8), off, data, states, rows,
+                                 n_rows=len(hist), eos=3)
+        for i in range(len(hist)):
+            allowed = np.array([(int(want[i, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
+            np.testing.assert_array_equal(post[i] == 0.0, allowed)
+            assert not allowed[[9, 10, 19, 29, 30, 40, V - 1]].any()
+
+
 def test_mask_rows_many_tool_tag_states(sim, oracle):
     """80 states of the tool-tag DFA (five workgroup rows of the LDS kernel,
     MASK_SPW_LDS = 16 states each, two of the global kernel, MASK_SPW = 64)

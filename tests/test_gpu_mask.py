@@ -126,9 +126,10 @@ def test_mask_build_rejects_bad_arguments(sampler):
     p = lambda t: C.c_void_p(t.data_ptr())
     ncls = ct.shape[1]
 
-    def call(byte_class=dbc, n_cls=ncls, n_dfa=d.n, n_tokens=len(toks), eos=-1, n=1):
+    def call(byte_class=dbc, n_cls=ncls, n_dfa=d.n, n_tokens=len(toks), eos=-1, n=1, n_bytes=ddata.numel()):
         return L.tgs_mask_rows_from_dfa(h, byte_class if byte_class is None else p(byte_class), p(dct), n_cls,
-                                        p(dcomp), n_dfa, p(doff), p(ddata), n_tokens, eos, p(dst), p(drow), n, None)
+                                        p(dcomp), n_dfa, p(doff), p(ddata), n_bytes, n_tokens, eos, p(dst), p(drow),
+                                        n, None)
 
     assert call() == 0
     assert call(n_cls=0) == -1
@@ -138,6 +139,7 @@ def test_mask_build_rejects_bad_arguments(sampler):
     assert call(eos=-2) == -1
     assert call(n=-1) == -1
     assert call(byte_class=None) == -1
+    assert call(n_bytes=-1) == -1
     assert call(n_tokens=100) != 0  # more tokens than the table's vocabulary
     assert call(n=0) == 0
     torch.cuda.synchronize()

@@ -91,3 +91,54 @@ def test_noalloc_mask_table_and_topk_path(sampler, oracle):
     c = W.config4(B=24)
     _same(sampler, oracle, "c4-24", c["logits"], c["params"], c["u"], c["hist"], c["hist_len"], kept_cap=1024,
           post=False, hint="auto")
+
+
+def test_noalloc_under_graph_capture(sampler, oracle):
+    """tgs_sample_noalloc captured in a HIP graph: one call with B = 0 sets
+    the device up outside any capture, then a graph holds one call on fixed
+    tensors.  Four replays, each after new inputs are copied into those
+    tensors, with eager tgs_sample calls and synchronisations between them;
+    every replay's ids match tgs_sample's on the same inputs bit for bit and
+    the oracle's."""
+    import torch
+
+    import tinygpt_amd as tg
+    from tinygpt_amd import workloads as W
+
+    dev = "cuda:0"
+    sets = [W.config2(B=32, V=50000, H=64, seed_offset=20 + i) for i in range(4)]
+    c0 = sets[0]
+    B, V = c0["logits"].shape
+    x, u = H.to_dev(c0["logits"]), H.to_dev(c0["u"])
+    hist, hl = H.to_dev(c0["hist"]), H.to_dev(c0["hist_len"])
+    pd = tg.params_to_device(c0["params"], dev)
+    out = torch.full((B,), -9, dtype=torch.int32, device=dev)
+    hint = tg.batch_hint(c0["params"], V)
+    for c in sets[1:]:
+        assert tg.batch_hint(c["params"], V) == hint
+    stream = torch.cuda.Stream(device=dev)
+    H.log("case noalloc capture: set-up call with B = 0")
+    tg.sample_noalloc(x[:0], pd, u, out=out, stream=stream.cuda_stream)
+    torch.cuda.synchronize()
+    H.log(f"case noalloc capture: capturing B={B} V={V}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+        tg.sample_noalloc(x, pd, u, hist=hist, hist_len=hl, out=out, hint=hint)
+    torch.cuda.synchronize()
+    for i, c in enumerate(sets):
+        H.log(f"case noalloc capture: replay {i}")
+        x.copy_(H.to_dev(c["logits"]))
+        u.copy_(H.to_dev(c["u"]))
+        hist.copy_(H.to_dev(c["hist"]))
+        hl.copy_(H.to_dev(c["hist_len"]))
+        pd.copy_(tg.params_to_device(c["params"], dev))
+        out.fill_(-9)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        eager = H.run_gpu(sampler, c["logits"], c["params"], c["u"], c["hist"], c["hist_len"], hint="auto")
+        np.testing.assert_array_equal(got, eager["ids"], err_msg=f"replay {i}: ids differ from tgs_sample")
+        ref = oracle.sample_batch(c["logits"], c["params"], c["u"], hist=c["hist"], hist_len=c["hist_len"])["ids"]
+        np.testing.assert_array_equal(got, ref, err_msg=f"replay {i}: ids differ from the oracle")
+    H.log("case noalloc capture: ok")

@@ -128,7 +128,7 @@ def load() -> C.CDLL:
     L.tgs_token_logprobs.restype = I
     L.tgs_token_logprobs.argtypes = [P, P, I, I, I, C.c_int64, P, P, P, P]
     L.tgs_mask_rows_from_dfa.restype = I
-    L.tgs_mask_rows_from_dfa.argtypes = [P, P, P, I, P, I, P, P, I, I, P, P, I, P]
+    L.tgs_mask_rows_from_dfa.argtypes = [P, P, P, I, P, I, P, P, C.c_int64, I, I, P, P, I, P]
     _lib = L
     return L
 

@@ -682,13 +682,14 @@ int tgs_sample_noalloc(int device, const void* d_logits, tgs_dtype dt, int B, in
 
 int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int32_t* d_trans, int n_cls,
                            const uint8_t* d_complete, int n_dfa, const int32_t* d_tok_off,
-                           const uint8_t* d_tok_bytes, int n_tokens, int eos_id, const int32_t* d_states,
-                           const int32_t* d_rows, int n, tgs_stream stream) {
+                           const uint8_t* d_tok_bytes, int64_t n_bytes, int n_tokens, int eos_id,
+                           const int32_t* d_states, const int32_t* d_rows, int n, tgs_stream stream) {
   if (!h) return TGS_EINVAL;
-  if (n < 0 || n_dfa < 1 || n_cls < 1 || n_cls > 256 || n_tokens < 0 || eos_id < -1 || eos_id >= n_tokens)
+  if (n < 0 || n_dfa < 1 || n_cls < 1 || n_cls > 256 || n_tokens < 0 || eos_id < -1 || eos_id >= n_tokens ||
+      n_bytes < 0)
     return fail(h, TGS_EINVAL, "mask build: bad arguments");
   if (n == 0) return TGS_OK;
-  if (!d_byte_class || !d_trans || !d_complete || !d_tok_off || (!d_tok_bytes && n_tokens > 0) || !d_states ||
+  if (!d_byte_class || !d_trans || !d_complete || !d_tok_off || (!d_tok_bytes && n_bytes > 0) || !d_states ||
       !d_rows)
     return fail(h, TGS_EINVAL, "null buffer");
   if (!h->mask_table || h->n_states < 1) return fail(h, TGS_EINVAL, "mask build: no mask table (tgs_mask_table_set)");
@@ -712,6 +713,8 @@ int tgs_mask_rows_from_dfa(tgs_handle h, const uint8_t* d_byte_class, const int3
   a.image = (uint16_t*)h->ws;
   a.tok_off = d_tok_off;
   a.tok_bytes = d_tok_bytes;
+  // offsets are int32: no token can end past INT32_MAX bytes
+  a.n_bytes = n_bytes < (int64_t)INT32_MAX ? (int)n_bytes : INT32_MAX;
   a.n_tokens = n_tokens;
   a.eos = eos_id;
   a.states = d_states;

@@ -87,7 +87,8 @@ struct MaskBuildArgs {
   int lds;                    // 1: the table fits LDS (16-bit row offsets, dead state, reject and stay columns)
   uint16_t* image;            // with lds: the LDS image (class offsets, then the table), written per call
   const int* tok_off;        // [n_tokens + 1]
-  const uint8_t* tok_bytes;
+  const uint8_t* tok_bytes;  // [n_bytes]
+  int n_bytes;               // a token's range outside [0, n_bytes) reads as empty
   int n_tokens;
   int eos;                   // token allowed in a complete state (-1: none)
   const int* states;         // [n]

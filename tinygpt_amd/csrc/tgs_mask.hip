@@ -23,8 +23,9 @@
 // a walk is a chain of branch-free LDS reads.  Otherwise the walk reads the
 // table from global memory (L2).
 // A class or next state outside the table rejects and rows outside the
-// table are skipped.  Token offsets are trusted: each token's bytes must
-// lie inside the byte buffer (tinygpt_amd.grammar.token_csr builds them so).
+// table are skipped.  A token whose offsets do not give a range inside the
+// byte buffer (negative, decreasing, or past its length) is read as empty,
+// so it is never allowed and no offset leads a read outside the buffer.
 #include "tgs_device.h"
 #include "tgs_kernels.h"
 
@@ -92,14 +93,20 @@ struct Tok {
   int p0, len;
   uint32_t raw[PRE];
 };
-__device__ __forceinline__ void tok_range(const MaskBuildArgs& a, int v, Tok& k) {
-  k.p0 = 0;
-  k.len = 0;
+// Token v's byte range [p0, p0 + len): empty for ids past n_tokens and for
+// offsets that do not lie in order inside the byte buffer.
+__device__ __forceinline__ void tok_span(const MaskBuildArgs& a, int v, int& p0, int& len) {
+  p0 = 0;
+  len = 0;
   if (v < a.n_tokens) {
-    k.p0 = a.tok_off[v];
-    k.len = a.tok_off[v + 1] - k.p0;
+    const int s = a.tok_off[v], e = a.tok_off[v + 1];
+    if (s >= 0 && e > s && e <= a.n_bytes) {
+      p0 = s;
+      len = e - s;
+    }
   }
 }
+__device__ __forceinline__ void tok_range(const MaskBuildArgs& a, int v, Tok& k) { tok_span(a, v, k.p0, k.len); }
 __device__ __forceinline__ void tok_bytes(const MaskBuildArgs& a, Tok& k) {
 #pragma unroll
   for (int j = 0; j < PRE; j++) k.raw[j] = j < k.len ? a.tok_bytes[k.p0 + j] : 0u;
@@ -238,11 +245,8 @@ __global__ __launch_bounds__(MT) void build_lds(MaskBuildArgs a) {
 __global__ __launch_bounds__(MT) void build_global(MaskBuildArgs a) {
   __shared__ uint8_t cls[256];
   const int v = blockIdx.x * MT + (int)threadIdx.x;
-  int p0 = 0, len = 0;
-  if (v < a.n_tokens) {
-    p0 = a.tok_off[v];
-    len = a.tok_off[v + 1] - p0;
-  }
+  int p0, len;
+  tok_span(a, v, p0, len);
   uint32_t raw[PRE];
 #pragma unroll
   for (int k = 0; k < PRE; k++) raw[k] = k < len ? a.tok_bytes[p0 + k] : 0u;

@@ -96,24 +96,75 @@ def _dtype_code(logits):
     raise TypeError("logits must be float32 or bfloat16")
 
 
+def _check_sample_inputs(fn, logits, params_dev, u, hist, hist_len, out, V, mask_table=None, mask_vocab=0):
+    """The tensors of one sampling call, checked before anything is
+    launched: the C ABI takes bare pointers, so a wrong dtype, a short
+    buffer or a tensor on another device would be read as garbage there.
+    Returns B."""
+    torch = _torch()
+
+    def bad(msg):
+        raise ValueError(f"{fn}: {msg}")
+
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        bad("logits must be [B, V] with unit stride along V")
+    _dtype_code(logits)
+    B = logits.shape[0]
+    if not 1 <= V <= logits.shape[1]:
+        bad(f"vocab {V} outside [1, {logits.shape[1]}]")
+    nb = ROW_PARAMS_DTYPE.itemsize * B
+    need = [("params", params_dev, (torch.uint8,), nb), ("u", u, (torch.float32,), B)]
+    if out is not None:
+        need.append(("out", out, (torch.int32,), B))
+    if hist_len is not None:
+        need.append(("hist_len", hist_len, (torch.int32,), B))
+    for name, t, dts, n in need:
+        if t is None:
+            bad(f"{name} is required")
+        if t.dtype not in dts or not t.is_contiguous() or t.numel() < n:
+            bad(f"{name} must be a contiguous {dts[0]} tensor of at least {n} elements")
+    if hist is not None:
+        if hist.dtype != torch.int32 or hist.dim() != 2 or not hist.is_contiguous() or hist.shape[0] < B:
+            bad("hist must be a contiguous int32 [B, hist_cap] tensor")
+    elif hist_len is not None:
+        bad("hist_len without hist")
+    if mask_table is not None:
+        if mask_table.dtype not in (torch.int32, torch.uint32) or mask_table.dim() != 2 \
+                or not mask_table.is_contiguous():
+            bad("mask_table must be a contiguous int32/uint32 [n_states, words] tensor")
+        if mask_vocab < V:
+            bad(f"mask_vocab {mask_vocab} is below the vocabulary {V}")
+        if mask_table.shape[1] != (mask_vocab + 31) // 32:
+            bad(f"mask_table rows hold {mask_table.shape[1]} words; mask_vocab {mask_vocab} needs "
+                f"{(mask_vocab + 31) // 32}")
+    for name, t in (("params", params_dev), ("u", u), ("out", out), ("hist", hist), ("hist_len", hist_len),
+                    ("mask_table", mask_table)):
+        if t is not None and t.device != logits.device:
+            bad(f"{name} is on {t.device}, logits on {logits.device}")
+    if logits.device.type != "cuda":
+        bad("tensors must be on a GPU")
+    return B
+
+
 def sample_noalloc(logits, params_dev, u, hist=None, hist_len=None, out=None, vocab=None, mask_table=None,
                    mask_vocab=None, debug=None, stream=None, hint=None):
     """tgs_sample_noalloc: Sampler.sample without a handle (the library's
     static device workspace; no allocation inside the call).  mask_table:
     uint32 device tensor [n_states, ceil(mask_vocab / 32)] or None.  `out`
     must be given by callers that cannot allocate (it is allocated here
-    otherwise)."""
+    otherwise).  Every tensor is checked (dtype, layout, length, device)
+    before the call."""
     torch = _torch()
-    if logits.dim() != 2 or logits.stride(1) != 1:
-        raise ValueError("logits must be [B, V] with unit stride along V")
-    B = logits.shape[0]
+    if logits.dim() != 2:
+        raise ValueError("tgs_sample_noalloc: logits must be [B, V]")
     V = logits.shape[1] if vocab is None else vocab
+    mv = (V if mask_vocab is None else mask_vocab) if mask_table is not None else 0
+    B = _check_sample_inputs("tgs_sample_noalloc", logits, params_dev, u, hist, hist_len, out, V, mask_table, mv)
     dt = _dtype_code(logits)
     if out is None:
         out = torch.empty(B, dtype=torch.int32, device=logits.device)
     hist_cap = 0 if hist is None else hist.shape[1]
     n_states = 0 if mask_table is None else mask_table.shape[0]
-    mv = (V if mask_vocab is None else mask_vocab) if mask_table is not None else 0
     dbg = _debug_struct(debug)
     hs = _hint_struct(hint)
     st = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
@@ -186,10 +237,10 @@ class Sampler:
         debug: dict of preallocated tensors (kept_ids, kept_probs, counts,
         mass, cut_ids, post_logits).  Returns the int32 [B] ids tensor."""
         torch = _torch()
-        if logits.dim() != 2 or logits.stride(1) != 1:
-            raise ValueError("logits must be [B, V] with unit stride along V")
-        B = logits.shape[0]
+        if logits.dim() != 2:
+            raise ValueError("tgs_sample: logits must be [B, V]")
         V = logits.shape[1] if vocab is None else vocab
+        B = _check_sample_inputs("tgs_sample", logits, params_dev, u, hist, hist_len, out, V)
         dt = _dtype_code(logits)
         if out is None:
             out = torch.empty(B, dtype=torch.int32, device=logits.device)
@@ -257,7 +308,7 @@ class Sampler:
         st = stream if stream is not None else torch.cuda.current_stream(trans.device).cuda_stream
         rc = self._L.tgs_mask_rows_from_dfa(
             self._h, _ptr(byte_class), _ptr(trans), n_cls, _ptr(complete), n_dfa, _ptr(tok_off), _ptr(tok_bytes),
-            V, int(eos), _ptr(states), _ptr(rows), n, C.c_void_p(st),
+            tok_bytes.numel(), V, int(eos), _ptr(states), _ptr(rows), n, C.c_void_p(st),
         )
         self._check(rc, "tgs_mask_rows_from_dfa")
 
