@@ -29,6 +29,7 @@ two characters (\\uXXXX: six), and length limits count those characters.
 """
 from __future__ import annotations
 
+import contextlib
 import json
 
 import numpy as np
@@ -730,11 +731,19 @@ class JsonSchemaConstraint:
         if new:
             dfa = local_dfa([s for s, _ in new], self.trie)
             bc, ct = dfa.byte_classes()
-            T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.device)
-            self._keep = (T(bc), T(ct), T(dfa.complete), T(np.array(dfa.roots, np.int32)),
-                          T(np.array([r for _, r in new], np.int32)))
-            self.sampler.mask_rows_from_dfa(self._keep[0], self._keep[1], self._keep[2], self._off, self._data,
-                                            self._keep[3], self._keep[4], eos=self.eos, stream=stream)
+            # The uploads are made and allocated on the stream the rows are built
+            # on: the build reads them in stream order, and the allocator does
+            # not hand their memory out again (when the next call replaces
+            # them) before that stream has passed the build.
+            on = torch.cuda.stream(torch.cuda.ExternalStream(stream)) if stream is not None \
+                else contextlib.nullcontext()
+            with on:
+                T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.device)
+                self._keep = (T(bc), T(ct), T(dfa.complete), T(np.array(dfa.roots, np.int32)),
+                              T(np.array([r for _, r in new], np.int32)))
+                self.sampler.mask_rows_from_dfa(self._keep[0], self._keep[1], self._keep[2], self._off,
+                                                self._data, self._keep[3], self._keep[4], eos=self.eos,
+                                                stream=stream)
             self.built += len(new)
         return out
 
