@@ -647,6 +647,12 @@ class JsonDecode:
         self.completed = 0
         self.stuck = 0  # documents no token could continue (id -1, nothing allowed)
         self.checks = []  # (prefix, id) pairs kept for the parity check
+        # per step, as the reference's per-token trace (InferenceTracer.addToken,
+        # native-mac/Sources/TinyGPTServe/InferenceTrace.swift:40-134) splits a
+        # token's time: the constraint (automaton snapshots interned as rows,
+        # new rows built on the device), the sampling call (parameters up, ids
+        # back) and the commit of the sampled ids to the automaton
+        self.trace = []
         self.alg_bytes = self.B * self.V * 4
         self.units_per_step = self.B
         self.unit = "tokens/s"
@@ -658,16 +664,44 @@ class JsonDecode:
 
     def launch(self, i, stream):
         tg = self.tg
+        st = self.torch.cuda.ExternalStream(stream)
+        t0 = time.perf_counter()
+        built0 = self.c.built
         try:
             rows = self.c.rows_for(self.snaps, stream=stream)
         except RuntimeError:  # the constraint's rows are used up: start over
             self.c.reset()
             rows = self.c.rows_for(self.snaps, stream=stream)
+        st.synchronize()
+        t1 = time.perf_counter()
         self.params["mask_state"] = rows
         pd = tg.params_to_device(self.params, "cuda:0")
         self.sampler.sample(self.d_logits[i % self.rot], pd, self.d_u[i % self.rot], out=self.out, stream=stream,
                             hint=tg.batch_hint(self.params, self.V))
-        ids = self.out.cpu().numpy()
+        with self.torch.cuda.stream(st):
+            ids = self.out.cpu().numpy()
+        t2 = time.perf_counter()
+        self._commit(ids)
+        t3 = time.perf_counter()
+        self.trace.append((len(self.trace), (t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3,
+                           self.c.built - built0))
+
+    def trace_summary(self, first=8):
+        """Per-step times in ms: mean / p50 / p90 of each part over the
+        steps, and the first steps as recorded."""
+        if not self.trace:
+            return None
+        a = np.array([t[1:4] for t in self.trace], np.float64)
+        out = {"steps": len(self.trace), "unit": "ms per step of 64 tokens"}
+        for j, name in enumerate(("constraint", "sample", "commit")):
+            out[name] = {"mean": round(float(a[:, j].mean()), 3), "p50": round(float(np.percentile(a[:, j], 50)), 3),
+                         "p90": round(float(np.percentile(a[:, j], 90)), 3)}
+        out["rows_built_per_step"] = round(float(np.mean([t[4] for t in self.trace])), 2)
+        out["first_steps"] = [{"index": t[0], "constraint_ms": round(t[1], 3), "sample_ms": round(t[2], 3),
+                               "commit_ms": round(t[3], 3), "rows_built": t[4]} for t in self.trace[:first]]
+        return out
+
+    def _commit(self, ids):
         for b in range(self.B):
             t = int(ids[b])
             if t < 0:  # no token of this vocabulary continues the document: start a new one
@@ -937,7 +971,10 @@ def main():
     steps = max(1, args.steps)
     if isinstance(wl, (JsonRows, JsonDecode)):
         steps = min(steps, 64 if isinstance(wl, JsonRows) else 200)  # host work in every call
+    if isinstance(wl, JsonDecode):
+        wl.trace = []  # the timed steps only
     ms_per_step, graph = time_calls(torch, wl, stream, steps, args.eager)
+    trace = wl.trace_summary() if isinstance(wl, JsonDecode) else None
 
     # per-call distribution: eager calls, each between two events
     n_calls = 16 if isinstance(wl, (JsonRows, JsonDecode)) else 256
@@ -1014,6 +1051,7 @@ def main():
     if isinstance(wl, SpecVerify):
         line["tokens_per_s"] = round(wl.tokens_per_step() / (ms_per_step * 1e-3), 1)
     if isinstance(wl, JsonDecode):
+        line["trace"] = trace
         line["documents_completed"] = wl.completed
         line["documents_stuck"] = wl.stuck
         line["mask_rows_built"] = wl.c.built

@@ -130,7 +130,9 @@ inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args
   const unsigned nt = block.x;
   const unsigned nblk = grid.x * grid.y;
   const bool conc = std::getenv("TGS_SIM_CONCURRENT") != nullptr;
-  const unsigned group = conc ? nblk : 1u;  // blocks started together
+  // blocks started together (a launch too large to run as threads at once,
+  // such as a set-up fill over a whole workspace, runs block by block)
+  const unsigned group = conc && (size_t)nblk * nt <= 16384 ? nblk : 1u;
   for (unsigned b0 = 0; b0 < nblk; b0 += group) {
     const unsigned nb = std::min(group, nblk - b0);
     std::vector<std::unique_ptr<BlockCtx>> ctxs(nb);

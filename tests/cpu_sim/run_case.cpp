@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -63,11 +64,32 @@ int main(int argc, char** argv) {
     // TGS_SIM_REPEAT=n: n calls on the same inputs, each of whose ids must
     // equal the first call's (the split kernel's state carries over calls)
     const char* rep_env = std::getenv("TGS_SIM_REPEAT");
-    const int reps = rep_env ? std::max(1, std::atoi(rep_env)) : 1;
+    int reps = rep_env ? std::max(1, std::atoi(rep_env)) : 1;
+    // TGS_SIM_FIRST_MERGE_SPINS=n: three more calls first, on the rows
+    // reversed (other candidates) and with the merge's poll limit n, so that
+    // merges give up and late lists stay behind in the workspace; their ids
+    // are not kept, and the calls after them must not take any of their
+    // entries
+    const char* fms = std::getenv("TGS_SIM_FIRST_MERGE_SPINS");
+    const int lead = fms ? 3 : 0;
+    int gave_up = 0;
+    std::vector<char> logits_rev;
+    if (fms) {
+      reps += lead;
+      const size_t es = dtype == 1 ? 2 : 4;
+      logits_rev = logits;
+      for (int b = 0; b < B; b++)
+        for (int v = 0; v < V; v++)
+          std::memcpy(logits_rev.data() + ((size_t)b * stride + v) * es,
+                      logits.data() + ((size_t)b * stride + (V - 1 - v)) * es, es);
+      setenv("TGS_MERGE_SPINS", fms, 1);
+    }
     std::vector<int32_t> first;
-    for (int it = 0; it < reps; it++) {
+    for (int it0 = 0; it0 < reps; it0++) {
+    const int it = it0 - lead;  // below 0: the leading calls
+    const char* lg = it < 0 ? logits_rev.data() : logits.data();
     if (std::getenv("TGS_SIM_NOALLOC")) {  // the allocation-free entry point (static workspace)
-      rc = tgs_sample_noalloc(0, logits.data(), (tgs_dtype)dtype, B, V, stride,
+      rc = tgs_sample_noalloc(0, lg, (tgs_dtype)dtype, B, V, stride,
                               hist_cap ? (const int32_t*)hist.data() : nullptr,
                               has_len ? (const int32_t*)hlen.data() : nullptr, hist_cap,
                               (const tgs_row_params*)params.data(), (const float*)u.data(), out.data(),
@@ -75,13 +97,19 @@ int main(int argc, char** argv) {
                               hint >= 0 ? &hb : nullptr, &dbg, nullptr);
       if (rc) { std::printf("sample_noalloc %d %s\n", rc, tgs_last_error(nullptr)); return 7; }
     } else {
-      rc = tgs_sample(h, logits.data(), (tgs_dtype)dtype, B, V, stride,
+      rc = tgs_sample(h, lg, (tgs_dtype)dtype, B, V, stride,
                       hist_cap ? (const int32_t*)hist.data() : nullptr,
                       has_len ? (const int32_t*)hlen.data() : nullptr, hist_cap, (const tgs_row_params*)params.data(),
                       (const float*)u.data(), out.data(), hint >= 0 ? &hb : nullptr, &dbg, nullptr);
       if (rc) { std::printf("sample %d %s\n", rc, tgs_last_error(h)); return 7; }
     }
-    if (it == 0) {
+    if (it < 0) {
+      for (int b = 0; b < B; b++) gave_up += out[b] == -4;
+      if (it == -1) {
+        std::printf("leading calls: %d rows gave up\n", gave_up);
+        unsetenv("TGS_MERGE_SPINS");
+      }
+    } else if (it == 0) {
       first = out;
     } else if (out != first) {
       std::printf("call %d: ids differ from the first call's\n", it);

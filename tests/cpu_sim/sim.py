@@ -97,6 +97,7 @@ def run_sample(logits, params, u, hist=None, hist_len=None, mask_table=None, V=N
                  cut_ids=rd("out_cut.bin", np.int32),
                  post_logits=rd("out_post.bin", np.float32).reshape(B, V) if post else None)
         r["launches"] = launches  # (grid, block) of every kernel launch, in order
+        r["stdout"] = p.stdout
         return r
 
 

@@ -269,6 +269,12 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
       const char* env = std::getenv("TGS_KEY_SPINS");
       a.key_spins = env ? std::max(0, std::atoi(env)) : 2048;
     }
+    // polls of the row's lists before the merging workgroup gives up and
+    // writes id -4 (TGS_MERGE_SPINS overrides: tests force the give-up)
+    {
+      const char* env = std::getenv("TGS_MERGE_SPINS");
+      a.merge_spins = env ? std::max(0, std::atoi(env)) : (1 << 18);
+    }
     // the chunks of a row on one XCD (workgroups are dealt out to the XCDs in
     // turn); TGS_XMAP=0 turns it off
     {

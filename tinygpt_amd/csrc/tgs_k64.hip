@@ -33,11 +33,15 @@
 //      (the larger of the two).
 //   3. Every vector whose maximum reaches cz is staged whole in its wave's
 //      LDS list.
-//   4. One staged vector per lane: the canonical logit y = z / T of each
-//      element (correctly rounded, tg_div_t), history ids left to their
-//      producers (the lane whose insertion created the id's LDS hash slot
-//      loads its logit at entry and adds its penalised value), the mask
-//      test, and a wave-aggregated append to the LDS candidate buffer.
+//   4. One staged vector per lane: every allowed element whose raw logit z
+//      reaches cz becomes a composite of z and its id, history ids left to
+//      their producers (the lane whose insertion created the id's LDS hash
+//      slot loads its logit at entry and appends its penalised value), the
+//      mask test, and a wave-aggregated append to the LDS candidate buffer.
+//      The temperature applies to candidates only: each composite becomes
+//      one of the canonical y = z / T (correctly rounded, tg_div_t) before
+//      any selection in the chunk, or, in an unsorted published list, in
+//      the merging workgroup (at most 64 divisions per row).
 //   5. An id left out is not a history id and has z < cz, so its y is at
 //      most yc = cz / T, while the k ids behind the bound have y at least
 //      y(B): when y(B) > yc, every id of the row's top k that lies in this
@@ -46,11 +50,13 @@
 //      its list holds, the chunk's exact top k comes from a radix selection
 //      over the chunk read again from memory instead.
 //
-// Rows split over S > 1 chunks.  Each workgroup counts itself in the row's
-// arrival counter at entry (a relaxed device atomic issued with the loads)
-// and reads the row's epoch word; the call's tag is that word plus one.
-// The workgroup that arrives last merges the row: every other workgroup of
-// the row has started by then.  The others publish their list with
+// Rows split over S > 1 chunks.  Each workgroup reads the row's epoch word
+// at entry (the call's tag is that word plus one) and counts itself in the
+// row's arrival counter (a relaxed device atomic) once its keys are out:
+// the last wave issues it after its history logits have landed, so that
+// no wait for a load queues behind it.  The workgroup that arrives last
+// merges the row: every other workgroup of the row is past its loads by
+// then.  The others publish their list with
 // agent-coherent stores (written through past the per-XCD L2s, which are
 // not coherent with each other) and exit: their candidates unsorted when
 // the row-wide bound left at most 64, else their sorted top k, then a count
@@ -62,8 +68,10 @@
 // tree of wave merges otherwise), finishes the row (masses, top-p, draw),
 // clears the entries it read (0: not written), and resets the counter and
 // advances the epoch for the next call.  Stale entries of an earlier call
-// carry another tag.  Every wait is bounded: a merge wait that runs out (it
-// cannot while every workgroup runs) writes id -4 for the row.  No fence is
+// carry another tag.  Every wait is bounded: a merge wait that runs out
+// after the launch's merge_spins polls (it cannot while every workgroup
+// runs; tests force it from the host) writes id -4 for the row, and lists
+// published after it stay behind under their call's tag.  No fence is
 // issued: on this part an agent-scope release or acquire fence writes back
 // or invalidates the whole L2 of the XCD.
 #include "tgs_device.h"
@@ -77,7 +85,6 @@ constexpr int NVT = K64_NVT;         // 16-byte vectors per thread
 constexpr int KM = 64;               // largest top_k served; longest published list
 constexpr int CAP = K64_CAP;         // candidate buffer entries
 constexpr u64 EMPTY = 0ull;          // list entry not written: a published entry never is 0
-constexpr int SPIN_LIMIT = 1 << 18;  // merge: polls of one list before the wait gives up
 constexpr uint32_t KEY_MIN = 0x00800000u;  // key of -FLT_MAX: below it only -inf and NaN
 constexpr uint32_t TAG_MASK = 0x3FFFu;     // epoch bits a list entry carries
 constexpr uint32_t ID_MASK = 0x3FFFFu;     // list entry id bits (V <= 2^18)
@@ -241,11 +248,11 @@ __device__ __forceinline__ u64 untag_entry(u64 e) {
 // lp), polled until it holds the call's tag (bounded), then cleared for the
 // next call.  Returns the composite (0 without act or after a timeout, which
 // sets *tmo).
-__device__ __forceinline__ u64 take_entry(u64* lp, bool act, uint32_t ep, bool* tmo) {
+__device__ __forceinline__ u64 take_entry(u64* lp, bool act, uint32_t ep, bool* tmo, int max_spins) {
   u64 e = act ? __hip_atomic_load(lp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : EMPTY;
   int spins = 0;
   while (__ballot(act && !entry_ok(e, ep)) != 0ull) {
-    if (++spins > SPIN_LIMIT) {
+    if (++spins > max_spins) {
       *tmo = true;
       break;
     }
@@ -931,7 +938,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
         if (ec[j] >= 0) pend = pend || !okc || (epo[j] < nce[j] && !entry_ok(ent[j], ep));
       }
       if (__ballot(pend) == 0ull) break;
-      if (spins >= SPIN_LIMIT) {
+      if (spins >= a.merge_spins) {
         tmo = true;
         break;
       }
@@ -1006,7 +1013,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       if (cc == c) {
         x = lane < n ? (raw_list ? buf[lane] : sh.own[lane]) : 0ull;
       } else {
-        x = take_entry(lists + (long long)cc * KM + lane, lane < n, ep, &tmo);
+        x = take_entry(lists + (long long)cc * KM + lane, lane < n, ep, &tmo, a.merge_spins);
       }
       if (sh.lz[cc]) x = z_to_y(x, r);
       if (!sh.lsort[cc]) x = wave_sort_desc(x);

@@ -65,6 +65,7 @@ struct SampleArgs {
   int kq;                // fused kernel: keys each wave publishes (S * 4 * kq <= K64_KEYS, >= 64)
   int xmap;              // fused kernel: a row's chunks are workgroups congruent mod 8 (B a multiple of 8)
   int key_spins;         // fused kernel: polls of the row's keys before a wave keeps its chunk's bound
+  int merge_spins;       // fused kernel: polls of the row's lists before the merge gives up (id -4)
   int full_rows;         // 1: full_kernel runs after the chunk kernels
   int hint_k;            // the launch hint's max_top_k (INT_MAX without a hint)
   int topp_all;          // 1: the top-p kernel alone serves the batch (its greedy rows too)
