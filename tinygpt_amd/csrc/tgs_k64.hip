@@ -22,8 +22,8 @@
 //        * Split rows whose whole grid is resident at once (the launch's
 //          exchange flag) also share a row-wide bound: each wave publishes
 //          the kq largest keys of its sort, tagged with the call's epoch,
-//          and every wave polls the row's S * waves * kq keys and takes
-//          their k-th largest (to 24 key bits).  Those keys belong to
+//          and wave 0 polls the row's S * waves * kq keys and takes their
+//          k-th largest (to 20 key bits).  Those keys belong to
 //          distinct threads, so k of them are k distinct qualifying ids.
 //          The row's k-th largest thread maximum lies close to its k-th
 //          largest logit, so a chunk collects a few ids instead of its own
