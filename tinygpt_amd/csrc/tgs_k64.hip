@@ -320,13 +320,15 @@ __device__ __forceinline__ T merge_waves(T acc, T (*slots)[64]) {
 }
 
 // The sorted top k of buf[0, n) (n <= CAP, unique composites) in wave 0's
-// lanes: ranking for short buffers, wave sorts of 64-entry slices merged
-// as a tree otherwise.  Ends with a barrier.
+// lanes: ranking for short buffers (n^2 <= 16 NTT: one round, at most 8
+// entry pairs read per thread), wave sorts of 64-entry slices merged as a
+// tree otherwise (ranking 256 entries in one wave took 13 us).  Ends with a
+// barrier.
 template <int NTT>
 __device__ __forceinline__ u64 select_top(u64* buf, int n, int k, u64 (*slots)[64]) {
   constexpr int NW = NTT / 64;
   const int w = threadIdx.x >> 6, lane = lane_id();
-  if (n <= 256) {
+  if (n * n <= 16 * NTT) {
     u64* top = slots[NW - 1];
     if (threadIdx.x < 64) top[threadIdx.x] = 0ull;
     __syncthreads();
