@@ -678,11 +678,34 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   // read from one sort per wave.  With the exchange, the wave's kq largest
   // keys go out to the row first.
   {
-    uint32_t hw = hpk[0];
+    uint32_t tk;
+    if constexpr (NTT == 64) {
+      // one wave: a thread's key is the largest logit of its own ids that
+      // are neither history ids nor masked out (with few threads, leaving
+      // out every thread whose maximum shares a vector with a history id
+      // left a byte-level row with 64 history ids too few keys for a bound,
+      // and every id became a candidate)
+      float t2 = -__builtin_inff();
 #pragma unroll
-    for (int q = 1; q < HPW; q++) hw = im * EPV / 32 == q ? hpk[q] : hw;
-    const bool hmax = ((hw >> (im * EPV % 32)) & GM) != 0u;
-    const uint32_t tk = (tm > -__builtin_inff() && !hmax) ? tg_key(tm) : 0u;
+      for (int i = 0; i < NVT; i++) {
+        const bool live = i < nfull || (int)threadIdx.x + i * NTT < nvec;
+        uint32_t x = 0u;
+        if constexpr (MASK) x = masked ? ~(mw[i] >> ((v0 + ((int)threadIdx.x + i * NTT) * EPV) & 31)) & GM : 0u;
+#pragma unroll
+        for (int e = 0; e < EPV; e++) {
+          const int bit = i * EPV + e;
+          const bool out = ((hpk[bit >> 5] >> (bit & 31)) & 1u) || ((x >> e) & 1u) || !live;
+          t2 = out ? t2 : fmaxf(t2, Elem<Tin>::get(raw[i], e));
+        }
+      }
+      tk = t2 > -__builtin_inff() ? tg_key(t2) : 0u;
+    } else {
+      uint32_t hw = hpk[0];
+#pragma unroll
+      for (int q = 1; q < HPW; q++) hw = im * EPV / 32 == q ? hpk[q] : hw;
+      const bool hmax = ((hw >> (im * EPV % 32)) & GM) != 0u;
+      tk = (tm > -__builtin_inff() && !hmax) ? tg_key(tm) : 0u;
+    }
     const uint32_t srt = wave_sort_desc(tk);  // lane i: the (i+1)-th largest
     // the call's tag: never 0 (the exchange memory starts zeroed, and the
     // epoch word never holds ~0)
