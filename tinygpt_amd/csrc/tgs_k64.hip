@@ -18,7 +18,9 @@
 //          waves of the wave's ceil(k / m)-th largest thread maximum (m
 //          waves hold that many at or above it each), read from one wave
 //          sort each.  In the sort a thread whose maximum lies in a vector
-//          holding a history id of the chunk takes the lowest key.
+//          holding a history id of the chunk takes the lowest key (in the
+//          one-wave instantiation a thread's key is the largest of its ids
+//          that are neither history ids nor masked).
 //        * Split rows whose whole grid is resident at once (the launch's
 //          exchange flag) also share a row-wide bound: each wave publishes
 //          the kq largest keys of its sort, tagged with the call's epoch,
@@ -32,7 +34,8 @@
 //      A wave collects from cz, 16 representable values below its bound
 //      (the larger of the two).
 //   3. Every vector whose maximum reaches cz is staged whole in its wave's
-//      LDS list.
+//      LDS list (a one-wave row of at most two vectors per thread skips the
+//      staging: each lane tests its own vectors in step 4).
 //   4. One staged vector per lane: every allowed element whose raw logit z
 //      reaches cz becomes a composite of z and its id, history ids left to
 //      their producers (the lane whose insertion created the id's LDS hash
@@ -688,6 +691,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       float t2 = -__builtin_inff();
 #pragma unroll
       for (int i = 0; i < NVT; i++) {
+        if (i * NTT >= nvec) break;  // (uniform) no thread holds vector i
         const bool live = i < nfull || (int)threadIdx.x + i * NTT < nvec;
         uint32_t x = 0u;
         if constexpr (MASK) x = masked ? ~(mw[i] >> ((v0 + ((int)threadIdx.x + i * NTT) * EPV) & 31)) & GM : 0u;
@@ -812,7 +816,33 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   for (int i = 0; i < NVT; i++)
     pm |= (vm[i] >= cz && vm[i] > -__builtin_inff()) ? (1u << i) : 0u;  // (cz may be -inf)
   const uint32_t PM = wave_or(pm);
-  {
+  bool direct = false;  // (uniform)
+  if constexpr (NTT == 64) {
+    // one wave over at most two vectors per thread: each lane tests its own
+    // vectors from its registers (no staging round trip through LDS)
+    if (nvec <= 2 * NTT) {
+      direct = true;
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        if (!(PM & (1u << i))) continue;  // uniform
+        const int j = (int)threadIdx.x + i * NTT, o = j * EPV;
+        const bool pass = ((pm >> i) & 1u) && j < nvec;
+        const uint32_t hw = (hpk[(i * EPV) >> 5] >> ((i * EPV) & 31)) & GM;
+        uint32_t xm = 0u;
+        if constexpr (MASK) xm = masked ? ~(mw[i] >> ((v0 + o) & 31)) & GM : 0u;
+        u64 x[EPV];
+        bool ok[EPV];
+#pragma unroll
+        for (int e = 0; e < EPV; e++) {
+          const float z = Elem<Tin>::get(raw[i], e);
+          ok[e] = pass && z >= cz && z > -__builtin_inff() && !((hw >> e) & 1u) && !((xm >> e) & 1u);
+          x[e] = comp_key(tg_key(z), v0 + o + e);
+        }
+        append_n<EPV>(x, ok, buf, &sh.nbuf);
+      }
+    }
+  }
+  if (!direct) {
     unsigned ns = 0;  // staged vectors of the wave (uniform)
 #pragma unroll
     for (int i = 0; i < NVT; i++) {
