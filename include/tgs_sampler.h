@@ -140,6 +140,13 @@ const char* tgs_last_error(tgs_handle h);
 int tgs_mask_table_set(tgs_handle h, const uint32_t* host_words, int n_states, int vocab);
 int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32_t* host_words,
                           int n);
+/* Rows [first, first + n) of the table copied to host_words (n rows of
+ * ceil(vocab/32) words), after all work queued on the handle's device has
+ * finished: the rows as tgs_mask_table_set / _update and
+ * tgs_mask_rows_from_dfa left them.  A readback for checks and
+ * diagnostics, not for the decode loop (it synchronises the device).  No
+ * reference counterpart: the reference's mask rows live in host arrays. */
+int tgs_mask_table_get(tgs_handle h, int first, int n, uint32_t* host_words);
 
 /* Sample one token per row.
  *   d_logits    [B] rows of V logits, row_stride elements apart (fp32 or bf16)

@@ -22,6 +22,17 @@ def to_dev(a, dev="cuda:0"):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
+def table_bits(sampler, rows, V):
+    """Allowed ids of mask-table rows read straight from the device table
+    (tgs_mask_table_get): bool [len(rows), V].  Bits past V must be clear."""
+    rows = np.asarray(rows, dtype=np.int64)
+    lo, hi = int(rows.min()), int(rows.max()) + 1
+    tab = sampler.mask_rows(lo, hi - lo)[rows - lo]
+    bits = np.unpackbits(np.ascontiguousarray(tab).view(np.uint8), axis=1, bitorder="little")
+    assert not bits[:, V:].any(), "bits past the vocabulary are set"
+    return bits[:, :V].astype(bool)
+
+
 def run_gpu(sampler, logits, params, u, hist=None, hist_len=None, mask_table=None, V=None,
             kept_cap=64, post=True, hint=None):
     """hint: None (general kernel), "auto" (computed from params) or an int."""

@@ -56,6 +56,7 @@ def test_null_handle_calls_fail_cleanly(lib):
     assert lib.tgs_sample(None, None, 0, 1, 1, 1, None, None, 0, None, None, None, None, None, None) == -1
     assert lib.tgs_spec_verify(None, None, None, 0, None, 1, 1, 1, None, None, None, None, None, None) == -1
     assert lib.tgs_mask_table_set(None, None, 0, 1) == -1
+    assert lib.tgs_mask_table_get(None, 0, 1, None) == -1
     assert lib.tgs_token_logprobs(None, None, 0, 1, 1, 1, None, None, None, None) == -1
     assert lib.tgs_mask_rows_from_dfa(None, None, None, 1, None, 1, None, None, 0, 1, -1, None, None, 1, None) == -1
     assert lib.tgs_last_error(None) == b"null handle"

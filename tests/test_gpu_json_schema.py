@@ -11,14 +11,15 @@ import pytest
 
 import json_fsm as O
 import json_schema_util as U
-from gpu_harness import log
+from gpu_harness import log, table_bits
 
 pytestmark = pytest.mark.gpu
 
 
 def read_rows(sampler, rows, V):
     """Allowed ids of mask-table rows, read back through greedy rows over
-    zero logits (post-mask logits: 0 allowed, -inf not)."""
+    zero logits (post-mask logits: 0 allowed, -inf not), and checked equal
+    to the table's words read straight from the device."""
     import torch
 
     import tinygpt_amd as tg
@@ -30,7 +31,9 @@ def read_rows(sampler, rows, V):
     sampler.sample(torch.zeros(B, V, device=dev), tg.params_to_device(params, dev), torch.zeros(B, device=dev),
                    vocab=V, debug={"post_logits": post})
     torch.cuda.synchronize()
-    return (post == 0).cpu().numpy()
+    got = (post == 0).cpu().numpy()
+    np.testing.assert_array_equal(got, table_bits(sampler, rows, V), err_msg="table words differ from the sampler's view")
+    return got
 
 
 def make_constraint(sampler, text, toks, eos=-1, n_rows=256):

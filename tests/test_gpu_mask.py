@@ -1,8 +1,9 @@
 """GPU parity of mask-table rows built on the device from a byte-level DFA
-(tgs_mask_rows_from_dfa) against the DFA replay oracle, read back through
-the sampler itself: a greedy row over zero logits with mask_state = the
-built row reports 0 for allowed ids and -inf for the rest in post_logits.
-Bit-exact."""
+(tgs_mask_rows_from_dfa) against the DFA replay oracle, read back two
+ways: the table's words straight from the device (tgs_mask_table_get), and
+through the sampler itself (a greedy row over zero logits with mask_state =
+the built row reports 0 for allowed ids and -inf for the rest in
+post_logits).  Bit-exact."""
 import numpy as np
 import pytest
 
@@ -64,10 +65,13 @@ def test_tool_tag_rows_built_on_device(sampler, oracle):
                    torch.zeros(R, dtype=torch.float32, device=dev), vocab=V, debug={"post_logits": post})
     torch.cuda.synchronize()
     got = post.cpu().numpy()
+    direct = H.table_bits(sampler, np.arange(R), V)  # the table's words themselves
     for i in range(2 * n):
         allowed = np.array([(int(want[i % n, v >> 5]) >> (v & 31)) & 1 for v in range(V)], dtype=bool)
         np.testing.assert_array_equal(got[i] == 0.0, allowed, err_msg=f"row {i} ({hist[i % n]!r})")
+        np.testing.assert_array_equal(direct[i], allowed, err_msg=f"table row {i} ({hist[i % n]!r})")
         assert np.all(np.isneginf(got[i][~allowed]))
+    assert direct[2 * n].all()
     assert (got[2 * n] == 0.0).all()  # the untouched last row still allows everything
     H.log("case mask build: ok")
 
@@ -157,6 +161,7 @@ def _read_rows(sampler, rows, V):
                    torch.zeros(len(rows), device=dev), vocab=V, debug={"post_logits": post})
     torch.cuda.synchronize()
     bits = (post == 0).cpu().numpy()
+    np.testing.assert_array_equal(bits, H.table_bits(sampler, rows, V), err_msg="table words differ from the sampler's view")
     return np.packbits(bits, axis=1, bitorder="little").view(np.uint8)
 
 

@@ -36,6 +36,7 @@ EXPORTS = (
     "tgs_last_error",
     "tgs_mask_table_set",
     "tgs_mask_table_update",
+    "tgs_mask_table_get",
     "tgs_sample",
     "tgs_sample_noalloc",
     "tgs_reserve_spec",
@@ -113,6 +114,8 @@ def load() -> C.CDLL:
     L.tgs_mask_table_set.argtypes = [P, P, I, I]
     L.tgs_mask_table_update.restype = I
     L.tgs_mask_table_update.argtypes = [P, P, P, I]
+    L.tgs_mask_table_get.restype = I
+    L.tgs_mask_table_get.argtypes = [P, I, I, P]
     L.tgs_sample.restype = I
     L.tgs_hint_from_params.restype = I
     L.tgs_hint_from_params.argtypes = [P, I, I, C.POINTER(TgsHint)]

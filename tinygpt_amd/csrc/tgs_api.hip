@@ -555,6 +555,20 @@ int tgs_mask_table_set(tgs_handle h, const uint32_t* host_words, int n_states, i
   return TGS_OK;
 }
 
+int tgs_mask_table_get(tgs_handle h, int first, int n, uint32_t* host_words) {
+  if (!h) return TGS_EINVAL;
+  if (first < 0 || n < 0 || first > h->n_states - n || (n > 0 && !host_words))
+    return fail(h, TGS_EINVAL, "mask table get: rows outside the table");
+  if (n == 0) return TGS_OK;
+  DeviceGuard g(h->device);
+  if (!g.ok) return fail(h, TGS_EHIP, "hipSetDevice");
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess)
+    e = hipMemcpy(host_words, h->mask_table + (size_t)first * h->mask_words,
+                  sizeof(uint32_t) * (size_t)h->mask_words * (size_t)n, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? TGS_OK : hip_fail(h, e, "mask table readback");
+}
+
 int tgs_mask_table_update(tgs_handle h, const int32_t* host_states, const uint32_t* host_words, int n) {
   if (!h) return TGS_EINVAL;
   if (n < 0 || (n > 0 && (!host_states || !host_words))) return fail(h, TGS_EINVAL, "mask update: bad arguments");

@@ -219,6 +219,7 @@ class Sampler:
         n_states = words.shape[0] if words.size else 0
         rc = self._L.tgs_mask_table_set(self._h, words.ctypes.data_as(C.c_void_p), n_states, vocab)
         self._check(rc, "tgs_mask_table_set")
+        self._mask_words = (int(vocab) + 31) // 32 if n_states else 0
 
     def update_mask_rows(self, states: np.ndarray, words: np.ndarray):
         states = np.ascontiguousarray(states, dtype=np.int32)
@@ -226,6 +227,15 @@ class Sampler:
         rc = self._L.tgs_mask_table_update(self._h, states.ctypes.data_as(C.c_void_p),
                                            words.ctypes.data_as(C.c_void_p), states.size)
         self._check(rc, "tgs_mask_table_update")
+
+    def mask_rows(self, first: int, n: int) -> np.ndarray:
+        """Rows [first, first + n) of the mask table as stored on the device
+        (uint32 [n, words]); waits for the device's queued work."""
+        words = int(getattr(self, "_mask_words", 0))
+        out = np.zeros((max(n, 0), words), dtype=np.uint32)
+        rc = self._L.tgs_mask_table_get(self._h, int(first), int(n), out.ctypes.data_as(C.c_void_p))
+        self._check(rc, "tgs_mask_table_get")
+        return out
 
     # -------------------------------------------------------------- sample
     def sample(self, logits, params_dev, u, hist=None, hist_len=None, out=None, vocab=None,
