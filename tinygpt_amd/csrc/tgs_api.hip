@@ -262,7 +262,9 @@ int sample_core(const SampleRes& res, std::string& err, const void* d_logits, tg
     // (at least 64 keys per row, at most K64_KEYS)
     a.xchg = a.S > 1 && k64_resident(res.num_cu, dt, a.whole_vec != 0, res.mask_table != nullptr && res.n_states > 0,
                                      lds, (long long)B * a.S);
+    // keys per wave: the row's S * waves * kq keys fit its K64_KEYS slots
     a.kq = a.S >= 4 ? 4 : 8;
+    while (a.kq > 1 && a.S * (tgs::K64_NT / 64) * a.kq > tgs::K64_KEYS) a.kq /= 2;
     // polls of the row's keys before a chunk keeps its own bound: far more
     // than a resident row needs (TGS_KEY_SPINS overrides: tests)
     {

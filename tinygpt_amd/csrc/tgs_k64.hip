@@ -137,16 +137,31 @@ struct HBits {
   __device__ static uint32_t of(const uint32_t* bits, int j) { return (bits[word(j)] >> shift(j)) & GM; }
 };
 
-// max over m = 1 .. NW of the m-th largest of wkey[m - 1][0, NW) (NW one or
-// four), in every lane: lanes 4 (m - 1) + i load wkey[m - 1][i], each group
-// of four lanes sorts itself descending (comparators (0,1) (2,3), (0,2)
-// (1,3), (1,2) as lane exchanges), and lane 5 (m - 1) then holds the m-th
-// largest of group m - 1.  The exchanges are DPP quad permutes.
+// max over m = 1 .. NW of the m-th largest of wkey[m - 1][0, NW) (NW one,
+// four or eight), in every lane.  Four waves: lanes 4 (m - 1) + i load
+// wkey[m - 1][i], each group of four lanes sorts itself descending
+// (comparators (0,1) (2,3), (0,2) (1,3), (1,2) as lane exchanges), and lane
+// 5 (m - 1) then holds the m-th largest of group m - 1 (the exchanges are
+// DPP quad permutes).  Eight waves: lanes 8 (m - 1) + i load wkey[m - 1][i],
+// each lane counts the entries of its group that rank above it (larger, or
+// equal at a lower index), and the lane of rank m - 1 in group m - 1 offers
+// its key to a wave maximum.
 template <int NW>
 __device__ __forceinline__ uint32_t bound_key(const uint32_t (*wkey)[NW], int lane) {
-  static_assert(NW == 1 || NW == 4, "waves per workgroup");
+  static_assert(NW == 1 || NW == 4 || NW == 8, "waves per workgroup");
   if constexpr (NW == 1) {
     return wkey[0][0];
+  } else if constexpr (NW == 8) {
+    const int g = lane >> 3, i = lane & 7;
+    const uint32_t x = wkey[g][i];
+    int rank = 0;
+#pragma unroll
+    for (int d = 1; d < 8; d++) {
+      const int j = (i + d) & 7;
+      const uint32_t y = __shfl(x, (g << 3) | j, 64);
+      rank += (y > x || (y == x && j < i)) ? 1 : 0;
+    }
+    return wave_max(rank == g ? x : 0u);
   } else {
     const int pos = lane & 3;
     uint32_t x = wkey[(lane >> 2) & 3][pos];

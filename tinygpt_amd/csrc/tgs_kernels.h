@@ -15,7 +15,7 @@ namespace tgs {
 // per-row exchange lines (word 0 the arrival counter, word 1 the epoch word,
 // from word K64_CNT_WORDS on one 64-bit count word per chunk), and the
 // bound-exchange keys per row.
-constexpr int K64_NT = 256;
+constexpr int K64_NT = 512;
 constexpr int K64_NVT = 16;
 constexpr int K64_MAX_HIST = 1024;
 constexpr int K64_SMALL_NT = 64;        // one-wave variant for rows of one small chunk
@@ -62,7 +62,7 @@ struct SampleArgs {
   unsigned long long* lists;  // fused kernel: [B][K64_MAX_SPLIT][64] chunk lists (entries 0 between calls)
   unsigned long long* keys;   // fused kernel: [B][K64_KEYS] bound-exchange keys
   int xchg;              // fused kernel: split rows share a row-wide bound (the grid is resident at once)
-  int kq;                // fused kernel: keys each wave publishes (S * 4 * kq <= K64_KEYS, >= 64)
+  int kq;                // fused kernel: keys each wave publishes (S * waves * kq <= K64_KEYS, >= 64)
   int xmap;              // fused kernel: a row's chunks are workgroups congruent mod 8 (B a multiple of 8)
   int key_spins;         // fused kernel: polls of the row's keys before a wave keeps its chunk's bound
   int merge_spins;       // fused kernel: polls of the row's lists before the merge gives up (id -4)
