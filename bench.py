@@ -742,7 +742,7 @@ class JsonDecode:
 class FloorRead:
     """read: the plain-read floor under the C2 headline.  The same 16
     rotating 64 x 128256 fp32 sets, read by libtgs_floor.so with the fused
-    top_k <= 64 kernel's grid and load pattern (8 chunks per row, 256
+    top_k <= 64 kernel's grid and load pattern (4 chunks per row, 512
     threads, 16 non-temporal 16-byte loads per thread at entry) and nothing
     computed but each chunk's maximum: the time the sampling chain adds its
     work to.  Not part of the sampler; no CPU baseline."""
@@ -751,7 +751,7 @@ class FloorRead:
         import ctypes as C
 
         dev = "cuda:0"
-        self.rot, self.B, self.V, self.S = 16, 64, 128256, 8
+        self.rot, self.B, self.V, self.S = 16, 64, 128256, 4
         lib = C.CDLL(os.path.join(ROOT, "tinygpt_amd", "libtgs_floor.so"))
         lib.tgs_floor_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_longlong, C.c_int, C.c_void_p, C.c_void_p]
         lib.tgs_floor_read.restype = C.c_int
@@ -760,7 +760,7 @@ class FloorRead:
                   for i in range(self.rot)]
         self.out = torch.empty(self.B * self.S, dtype=torch.float32, device=dev)
         self.config = {"workload": "read_floor_c2", "B": self.B, "V": self.V, "chunks_per_row": self.S,
-                       "threads_per_chunk": 256, "loads": "16 non-temporal 16-byte loads per thread"}
+                       "threads_per_chunk": 512, "loads": "16 non-temporal 16-byte loads per thread"}
         self.dtype = "f32"
         self.alg_bytes = 4 * self.V * self.B
         self.units_per_step = self.B

@@ -3,18 +3,20 @@
 // libtgs_floor.so, not into the sampler's C ABI).
 //
 // It reads [B] rows of V fp32 logits with the fused kernel's grid and load
-// pattern: S chunks per row of L ids, one workgroup of 256 threads per
-// chunk, thread t issuing its 16 non-temporal 16-byte loads (chunk vectors
-// t, t + 256, ...) at entry, and keeps only what the loads need to stay
-// live: the maximum of each chunk, written out.  The time of a launch is the
-// floor the sampling chain adds its work to.
+// pattern: S chunks per row of L ids, one workgroup of K64_NT threads per
+// chunk, thread t issuing its K64_NVT non-temporal 16-byte loads (chunk
+// vectors t, t + K64_NT, ...) at entry, and keeps only what the loads need to
+// stay live: the maximum of each chunk, written out.  The time of a launch is
+// the floor the sampling chain adds its work to.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "tgs_kernels.h"
+
 namespace {
 
-constexpr int NT = 256;
-constexpr int NVT = 16;
+constexpr int NT = tgs::K64_NT;
+constexpr int NVT = tgs::K64_NVT;
 
 __global__ __launch_bounds__(NT) void floor_read_kernel(const float* x, int V, long long stride, int S, int L,
                                                         float* out) {
@@ -39,7 +41,11 @@ __global__ __launch_bounds__(NT) void floor_read_kernel(const float* x, int V, l
   __shared__ float wm[NT / 64];
   if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
   __syncthreads();
-  if (threadIdx.x == 0) out[blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  if (threadIdx.x == 0) {
+    float r = wm[0];
+    for (int i = 1; i < NT / 64; i++) r = fmaxf(r, wm[i]);
+    out[blockIdx.x] = r;
+  }
 }
 
 }  // namespace
@@ -49,7 +55,7 @@ extern "C" {
 // Reads rows [B][V] (stride `stride` floats) of a 16-byte aligned fp32 array
 // in S chunks per row; out: [B * S] chunk maxima.  Returns 0, or -1 when the
 // shape does not fit the pattern (V and stride multiples of 4, a chunk of at
-// most 256 * 16 vectors), -2 on a launch error.
+// most K64_NT * K64_NVT vectors), -2 on a launch error.
 int tgs_floor_read(const float* x, int B, int V, long long stride, int S, float* out, void* stream) {
   if (!x || !out || B < 1 || V < 4 || V % 4 != 0 || stride < V || stride % 4 != 0 || S < 1) return -1;
   if ((uintptr_t)x % 16 != 0) return -1;
