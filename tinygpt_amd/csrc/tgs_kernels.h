@@ -77,7 +77,7 @@ struct SampleArgs {
 constexpr int MASK_NT = 256;
 constexpr int MASK_SPW = 64;             // requested states per workgroup (global-table kernel)
 constexpr int MASK_SPW_LDS = 16;         // requested states per workgroup (LDS-table kernel)
-constexpr int MASK_NSUB = 4;             // 256-token sub-chunks per LDS-table workgroup (whole lines per row)
+constexpr int MASK_NSUB = 2;             // 256-token sub-chunks per LDS-table workgroup (64-byte row segments)
 constexpr int MASK_LDS_TABLE = 60 * 1024;  // largest transition table held in LDS (16-bit row offsets)
 struct MaskBuildArgs {
   const uint8_t* byte_class;  // [256] class of each byte (>= n_cls rejects)

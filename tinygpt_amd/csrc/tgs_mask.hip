@@ -140,7 +140,7 @@ __global__ __launch_bounds__(MT) void prep_image(MaskBuildArgs a) {
 }
 
 // Workgroup (NSUB * MT tokens, SPWL requested states): every row it writes
-// gets NSUB * MT / 32 consecutive words (whole 128-byte lines), staged in
+// gets NSUB * MT / 32 consecutive words (64-byte segments), staged in
 // LDS and stored by adjacent lanes.
 __global__ __launch_bounds__(MT) void build_lds(MaskBuildArgs a) {
   TGS_DYN_SMEM(smem);
