@@ -527,16 +527,15 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   unsigned* cnt = a.cnt + (long long)b * K64_CNT_STRIDE;
 
   // ---- everything read first, in the order it is needed (a wave's loads
-  // return in order): the row's parameters, its history length and ids, the
-  // mask words, the chunk, then the row's arrival count and epoch word
+  // return in order): the row's parameters, its epoch word, its history
+  // length and ids, the mask words, then the chunk
   const tgs_row_params p = a.params[b];
   const float ub = a.u[b];
   const int hlr = *(a.hist_len ? a.hist_len + b : (const int*)a.params);
   const bool hv = a.hist && a.hist_cap > 0;
   const int* hp = hv ? a.hist + (long long)b * a.hist_cap : (const int*)a.params;
   const int hlast = hv ? a.hist_cap - 1 : 0;
-  // the row's epoch word (every wave reads it: one request per wave) and
-  // arrival count
+  // the row's epoch word (every wave reads it: one request per wave)
   const uint32_t epw = __hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int hid[NHID];  // this thread's share of the history: entries threadIdx.x + q NTT
 #pragma unroll
@@ -561,8 +560,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   }
   // Whole vectors: one unconditional load each (a vector past the chunk
   // reads its last one again and is left out in step 1).  With no branch
-  // among the loads the compiler waits exactly for the history ids and the
-  // arrival count, so the history hash is built while the chunk streams in.
+  // among the loads the compiler waits exactly for the history ids, so the
+  // history hash is built while the chunk streams in.
   uint4 raw[NVT];
 #pragma unroll
   for (int i = 0; i < NVT; i++) {
@@ -575,10 +574,6 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       raw[i] = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);  // NaN: never counted
     }
   }
-  // Behind the chunk: the row's arrival count (a device atomic queues far
-  // longer than a load, and a wave's loads return in order, so issued before
-  // the chunk it would hold the chunk's data back) and the epoch word (every
-  // wave reads it: one request per wave).
   const int hl = a.hist_len ? hlr : a.hist_cap;
 
   Row r;
