@@ -118,7 +118,6 @@ struct Shared {
   int fast;                    // merging workgroup: entries laid out in mer (-1: the merge tree)
   uint32_t rkey;               // the row-wide bound key (0: none)
   alignas(16) u64 mer[66];     // merging workgroup: the lists end to end (+ a pad entry)
-  u64 mer2[64];                // ... and ranked
   BlockScratch bs;
 };
 
@@ -965,9 +964,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   // list in one round of requests (two entries per lane), polled until each
   // count word and each entry below its count holds the call's tag.  When
   // the lists hold at most 64 entries, none beyond its first E, they are
-  // laid end to end in LDS and ranked there (an entry's rank is the number
-  // of entries above it); otherwise every wave takes part in a tree of wave
-  // merges over the lists read again.
+  // laid end to end in LDS and sorted by one wave; otherwise every wave
+  // takes part in a tree of wave merges over the lists read again.
   if (w == 0) {
     const int own_n = raw_list ? nb : __popcll(__ballot(acc != 0ull));
     if (!raw_list) sh.own[lane] = acc;
@@ -1054,19 +1052,9 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   const int nfast = sh.fast;
   if (nfast >= 0) {
     if (w == 0) {
-      const u64 x = sh.mer[lane];
-      int rk = 0;
-      const u64x2* q = (const u64x2*)sh.mer;
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        const u64x2 e = q[j];
-        rk += (e.x > x) + (e.y > x);
-      }
-      if (lane < nfast && x != 0ull) sh.mer2[rk] = x;
-      wave_lds_sync();
-      const int nv = __popcll(__ballot(lane < nfast && x != 0ull));  // entries left after z / T
-      const u64 y = lane < nv ? sh.mer2[lane] : 0ull;
-      finish_merged(a, r, y, k, false);
+      // the entries are distinct composites and the pads (and entries that
+      // z / T leaves out) are 0, below every one: one wave sort ranks them
+      finish_merged(a, r, wave_sort_desc(sh.mer[lane]), k, false);
     }
   } else {
     // a tree of wave merges: wave w takes lists w, w + NW, ...
