@@ -493,6 +493,20 @@ __device__ __forceinline__ void post_logits_chunk(const SampleArgs& a, const Row
   }
 }
 
+// Vector i of this thread's share of the chunk [v0, v1) (nvec vectors).
+template <typename Tin, int NTT, bool VEC>
+__device__ __forceinline__ uint4 chunk_vec(const Tin* rowp, int i, int v0, int v1, int nvec, bool aligned) {
+  constexpr int EPV = Elem<Tin>::EPV;
+  const int j = (int)threadIdx.x + i * NTT;
+  if constexpr (VEC) {
+    return tg_load_nt(rowp + v0 + (j < nvec ? j : nvec - 1) * EPV);
+  } else if (i * NTT < nvec) {  // whole-workgroup test: vectors wholly past the chunk are not read
+    return load_vec<Tin>(rowp, v0 + j * EPV, v1, aligned);
+  } else {
+    return make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);  // NaN: never counted
+  }
+}
+
 template <typename Tin, int NTT, bool VEC, bool MASK>
 __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   using G = Geo<Tin, NTT>;
@@ -527,7 +541,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
 
   // ---- everything read first, in the order it is needed (a wave's loads
   // return in order): the row's parameters, its epoch word, its history
-  // length and ids, the mask words, then the chunk
+  // length and ids, the chunk; with a mask table, its words between the
+  // chunk's first NPRE vectors and the rest
   const tgs_row_params p = a.params[b];
   const float ub = a.u[b];
   const int hlr = *(a.hist_len ? a.hist_len + b : (const int*)a.params);
@@ -542,9 +557,22 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
     const int j = (int)threadIdx.x + q * NTT;
     hid[q] = hp[j < hlast ? j : hlast];
   }
-  // the mask words depend on the parameters: requested before the chunk so
-  // that they do not queue behind it (a state out of range reads the first
-  // row, and the row is rejected below)
+  // Whole vectors: one unconditional load each (a vector past the chunk
+  // reads its last one again and is left out in step 1).  With no branch
+  // among the loads the compiler waits exactly for the history ids, so the
+  // history hash is built while the chunk streams in.
+  uint4 raw[NVT];
+  // The mask words depend on the parameters, whose first request takes
+  // about a microsecond to return: the chunk's first NPRE vectors go out
+  // before the words, so that the chunk's stream does not wait for the
+  // parameters, and the rest after them, so that the words do not queue
+  // behind the whole chunk (step 1 takes the vectors in order, each with its
+  // word).  A state out of range reads the first row, and the row is
+  // rejected below.
+  constexpr int NPRE = MASK ? K64_MASK_PRE : 0;
+  static_assert(NPRE >= 0 && NPRE <= NVT, "chunk vectors before the mask words");
+#pragma unroll
+  for (int i = 0; i < NPRE; i++) raw[i] = chunk_vec<Tin, NTT, VEC>(rowp, i, v0, v1, nvec, a.aligned);
   uint32_t mw[MASK ? NVT : 1];
   const uint32_t* mrow_any = a.mask_table;  // the row's mask row (the first row for a state out of range)
   if constexpr (MASK) {
@@ -557,22 +585,8 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       mw[i] = mrow[(v0 + (j < nvec ? j : nvec - 1) * EPV) >> 5];
     }
   }
-  // Whole vectors: one unconditional load each (a vector past the chunk
-  // reads its last one again and is left out in step 1).  With no branch
-  // among the loads the compiler waits exactly for the history ids, so the
-  // history hash is built while the chunk streams in.
-  uint4 raw[NVT];
 #pragma unroll
-  for (int i = 0; i < NVT; i++) {
-    const int j = (int)threadIdx.x + i * NTT;
-    if constexpr (VEC) {
-      raw[i] = tg_load_nt(rowp + v0 + (j < nvec ? j : nvec - 1) * EPV);
-    } else if (i * NTT < nvec) {  // whole-workgroup test: vectors wholly past the chunk are not read
-      raw[i] = load_vec<Tin>(rowp, v0 + j * EPV, v1, a.aligned);
-    } else {
-      raw[i] = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);  // NaN: never counted
-    }
-  }
+  for (int i = NPRE; i < NVT; i++) raw[i] = chunk_vec<Tin, NTT, VEC>(rowp, i, v0, v1, nvec, a.aligned);
   const int hl = a.hist_len ? hlr : a.hist_cap;
 
   Row r;

@@ -17,6 +17,7 @@ namespace tgs {
 // bound-exchange keys per row.
 constexpr int K64_NT = 512;
 constexpr int K64_NVT = 16;
+constexpr int K64_MASK_PRE = 2;  // with a mask table: chunk vectors requested before the mask words
 constexpr int K64_MAX_HIST = 1024;
 constexpr int K64_SMALL_NT = 64;        // one-wave variant for rows of one small chunk
 constexpr int K64_SMALL_MAX_HIST = 256;  // its longest history
@@ -30,6 +31,7 @@ constexpr int K64_KEYS = 256;
 // ids of one histogram bucket ranked in LDS.
 constexpr int TOPP_NT = 1024;
 constexpr int TOPP_CAP = 1024;
+constexpr int TOPP_MASK_PRE = 2;  // register-resident row vectors requested before the mask words
 
 // Top-k kernel (1 <= top_k <= KMAX, the row held in registers): threads per
 // workgroup and candidate capacity.

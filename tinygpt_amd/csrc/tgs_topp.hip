@@ -92,39 +92,46 @@ struct RowView {
     }
   }
 
-  // the row's vectors of this thread.  Rows of whole aligned vectors read
-  // every vector with one unconditional load (a vector past the row end
-  // reads the last one again; vec_y drops its ids), so no load waits for an
-  // earlier one: a divergent fallback beside the loads makes the compiler
-  // wait for the loads already issued before reusing their registers.
+  // the row's vectors J0 .. J1 - 1 of this thread.  Rows of whole aligned
+  // vectors read every vector with one unconditional load (a vector past
+  // the row end reads the last one again; vec_y drops its ids), so no load
+  // waits for an earlier one: a divergent fallback beside the loads makes
+  // the compiler wait for the loads already issued before reusing their
+  // registers.
+  template <int J0, int J1>
   __device__ __forceinline__ static void fetch(const SampleArgs& a, const Tin* p, uint4 (&raw)[NV]) {
     if constexpr (RES) {
       if (a.aligned && a.V >= EPV && a.V % EPV == 0) {
         const int last = a.V / EPV - 1;
 #pragma unroll
-        for (int j = 0; j < NV; j++) {
+        for (int j = J0; j < J1; j++) {
           const int vi = (int)threadIdx.x + j * BT;
           raw[j] = tg_load_nt(p + (vi < last ? vi : last) * EPV);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < NV; j++) raw[j] = load_vec<Tin>(p, (threadIdx.x + j * BT) * EPV, a.V, a.aligned);
+        for (int j = J0; j < J1; j++) raw[j] = load_vec<Tin>(p, (threadIdx.x + j * BT) * EPV, a.V, a.aligned);
+      }
+    }
+  }
+
+  // the mask word of each of this thread's register-resident vectors (all
+  // ones without a mask row, 0 past the row end)
+  __device__ __forceinline__ static void mask_words(const SampleArgs& a, const Row& r, uint32_t (&mw)[NV]) {
+    if constexpr (RES) {
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        const int v = ((int)threadIdx.x + j * BT) * EPV;
+        mw[j] = v >= a.V ? 0u : r.mrow ? r.mrow[v >> 5] : 0xFFFFFFFFu;
       }
     }
   }
 
   // y of the register-resident vectors, specialised on what is uniform over
   // the row (penalties present, a power-of-two temperature) so that the
-  // per-element code carries no branch for the cases the row does not have;
-  // every mask word is requested before the first element is evaluated
+  // per-element code carries no branch for the cases the row does not have
   template <bool PEN, bool POW2>
-  __device__ __forceinline__ void load_t(const uint4 (&raw)[NV]) {
-    uint32_t mw[NV];
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-      const int v = ((int)threadIdx.x + j * BT) * EPV;
-      mw[j] = v >= a.V ? 0u : r.mrow ? r.mrow[v >> 5] : 0xFFFFFFFFu;
-    }
+  __device__ __forceinline__ void load_t(const uint4 (&raw)[NV], const uint32_t (&mw)[NV]) {
 #pragma unroll
     for (int j = 0; j < NV; j++) {
       const int v = ((int)threadIdx.x + j * BT) * EPV;
@@ -142,11 +149,11 @@ struct RowView {
     }
   }
 
-  __device__ __forceinline__ void load(const uint4 (&raw)[NV]) {
+  __device__ __forceinline__ void load(const uint4 (&raw)[NV], const uint32_t (&mw)[NV]) {
     if constexpr (RES) {
-      if (r.use_pen) load_t<true, false>(raw);
-      else if (r.tdiv == TDIV_POW2) load_t<false, true>(raw);
-      else load_t<false, false>(raw);
+      if (r.use_pen) load_t<true, false>(raw, mw);
+      else if (r.tdiv == TDIV_POW2) load_t<false, true>(raw, mw);
+      else load_t<false, false>(raw, mw);
     }
   }
 
@@ -412,7 +419,8 @@ __device__ __forceinline__ void topp_rest(const SampleArgs& a, const Row& r, con
 
 template <typename Tin, bool RES>
 __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned char* smem, Scratch& ts,
-                                         BlockScratch& bs, const uint4 (&raw)[RowView<Tin, RES>::NV]) {
+                                         BlockScratch& bs, const uint4 (&raw)[RowView<Tin, RES>::NV],
+                                         const uint32_t (&mw)[RowView<Tin, RES>::NV]) {
   const int b = r.b;
   const int bw = a.TS > 0 ? (a.V + 31) / 32 : 0;
   uint32_t* hbits = (uint32_t*)smem;
@@ -431,7 +439,7 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
   r.v1 = a.V;
   if (r.use_pen) hash_build<BT>(a, r, hash, hbits, bw);
   RowView<Tin, RES> rv(a, r, hash, hbits, (const Tin*)a.logits + (long long)b * a.row_stride);
-  rv.load(raw);
+  rv.load(raw, mw);
   if (a.dbg.post_logits) {
     float* post = a.dbg.post_logits + (long long)b * a.V;
     for (int v = threadIdx.x; v < a.V; v += BT) post[v] = -__builtin_inff();
@@ -527,12 +535,19 @@ __global__ __launch_bounds__(BT) void topp_kernel(SampleArgs a) {
   const int b = blockIdx.x;
   if (b >= a.B) return;
   // the row's parameters (scalar loads) requested before its vectors, so
-  // that they arrive first and the mask words can be requested early
+  // that they arrive first.  The mask words wait for them (the first request
+  // takes about a microsecond): the row's first NPRE vectors go out before
+  // the words, the rest after them, so that neither the row's stream waits
+  // for the parameters nor the words for the whole row (the vectors are
+  // evaluated in order, each with its word).
+  using RV = RowView<Tin, RES>;
+  constexpr int NPRE = RV::NV < TOPP_MASK_PRE ? RV::NV : TOPP_MASK_PRE;
   const tgs_row_params p = a.params[b];
   const float ub = a.u[b];
   const int hl = a.hist_len ? a.hist_len[b] : a.hist_cap;
-  uint4 raw[RowView<Tin, RES>::NV];
-  RowView<Tin, RES>::fetch(a, (const Tin*)a.logits + (long long)b * a.row_stride, raw);
+  const Tin* rowp = (const Tin*)a.logits + (long long)b * a.row_stride;
+  uint4 raw[RV::NV];
+  RV::template fetch<0, NPRE>(a, rowp, raw);
   Row r;
   const bool valid = row_setup_from(a, b, 0, p, ub, hl, r);
   const bool mine = valid && (r.mode == 2 ? !(r.k >= 1 && r.k < a.V) : (r.mode == 0 && a.topp_all));
@@ -545,7 +560,10 @@ __global__ __launch_bounds__(BT) void topp_kernel(SampleArgs a) {
     }
     return;
   }
-  topp_row<Tin, RES>(a, r, smem, ts, bs, raw);
+  uint32_t mw[RV::NV];
+  RV::mask_words(a, r, mw);
+  RV::template fetch<NPRE, RV::NV>(a, rowp, raw);
+  topp_row<Tin, RES>(a, r, smem, ts, bs, raw, mw);
 }
 
 }  // namespace topp
