@@ -72,6 +72,7 @@ struct RowView {
   const uint32_t* hbits;
   const Tin* rowp;
   float y[RES ? RES_EPT : 1];
+  unsigned nallowed = 0;  // this thread's allowed ids among y (set by load)
 
   __device__ __forceinline__ RowView(const SampleArgs& a_, const Row& r_, const int2* h_, const uint32_t* hb_,
                                      const Tin* p_)
@@ -128,9 +129,10 @@ struct RowView {
   }
 
   // y of the register-resident vectors, specialised on what is uniform over
-  // the row (penalties present, a power-of-two temperature) so that the
-  // per-element code carries no branch for the cases the row does not have
-  template <bool PEN, bool POW2>
+  // the row (penalties present, a power-of-two temperature, T = 1: y = z
+  // exactly) so that the per-element code carries no branch or operation for
+  // the cases the row does not have
+  template <bool PEN, bool POW2, bool ONE = false>
   __device__ __forceinline__ void load_t(const uint4 (&raw)[NV], const uint32_t (&mw)[NV]) {
 #pragma unroll
     for (int j = 0; j < NV; j++) {
@@ -143,8 +145,12 @@ struct RowView {
         if constexpr (PEN) {
           if ((hw >> (id & 31)) & 1u) z = penalise(z, hash_count(hash, a.TS, a.ts_shift, id), r);
         }
-        const float yy = POW2 ? z * r.rT : row_y(r, z);
-        y[j * EPV + e] = (((mw[j] >> (id & 31)) & 1u) && yy > -__builtin_inff() && id < a.V) ? yy : -__builtin_inff();
+        // (an id past the row end needs no test: its vector's mask word is
+        // 0, or, in a vector that straddles the end, load_vec read it as NaN)
+        const float yy = ONE ? z : POW2 ? z * r.rT : row_y(r, z);
+        const bool ok = ((mw[j] >> (id & 31)) & 1u) && yy > -__builtin_inff();
+        y[j * EPV + e] = ok ? yy : -__builtin_inff();
+        nallowed += ok ? 1u : 0u;
       }
     }
   }
@@ -152,6 +158,7 @@ struct RowView {
   __device__ __forceinline__ void load(const uint4 (&raw)[NV], const uint32_t (&mw)[NV]) {
     if constexpr (RES) {
       if (r.use_pen) load_t<true, false>(raw, mw);
+      else if (r.tdiv == TDIV_POW2 && r.rT == 1.0f) load_t<false, true, true>(raw, mw);
       else if (r.tdiv == TDIV_POW2) load_t<false, true>(raw, mw);
       else load_t<false, false>(raw, mw);
     }
@@ -309,15 +316,30 @@ __device__ __forceinline__ void topp_rest(const SampleArgs& a, const Row& r, con
                                           unsigned nv, Scratch& ts, BlockScratch& bs) {
   const int b = r.b;
   const float m = tl.m;
-  // pass 2: count and exact-mass histogram over the buckets below m
-  rv.each([&](int, float y) {
-    const int bq = bucket::of(y, m);
-    atomicAdd(&tl.CI[bq], 1u);
-    if (bq < NB) {
-      const u64 q = bucket::mass(y, m);
-      if (q) atomicAdd(&tl.MI[bq], q);
-    }
-  });
+  // pass 2: count and exact-mass histogram over the buckets below m.  With
+  // a finite maximum, x = y - m is +-0 exactly at y == m, where bucket 0 and
+  // weight 1 follow from x itself (tg_expf_nonpos(+-0) = 1), so the test for
+  // y == m that an infinite maximum needs is left out.
+  if (m < __builtin_inff()) {
+    rv.each([&](int, float y) {
+      const float x = y - m;
+      const int bq = !(x > -32.0f) ? NB : (int)(-x * 32.0f);
+      atomicAdd(&tl.CI[bq], 1u);
+      if (bq < NB) {
+        const u64 q = tg_q40(tg_expf_nonpos(x));
+        if (q) atomicAdd(&tl.MI[bq], q);
+      }
+    });
+  } else {
+    rv.each([&](int, float y) {
+      const int bq = bucket::of(y, m);
+      atomicAdd(&tl.CI[bq], 1u);
+      if (bq < NB) {
+        const u64 q = bucket::mass(y, m);
+        if (q) atomicAdd(&tl.MI[bq], q);
+      }
+    });
+  }
   __syncthreads();
   bucket::prefix<BT>(tl.CI, tl.MI, ts.red32, ts.red64);
   const u64 S = tl.MI[NB - 1];
@@ -453,19 +475,20 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
   unsigned nvl = 0;
   if constexpr (RES) {
     // branch free over the registers: a thread's ids rise with the index,
-    // so a strict > keeps the smallest id among its equal maxima
+    // so a strict > keeps the smallest id among its equal maxima (the slot
+    // is tracked, and its id formed once)
+    constexpr int EPV = RowView<Tin, RES>::EPV;
     float mx = -__builtin_inff();
-    int mid = 0;
+    int mq = 0;
 #pragma unroll
     for (int q = 0; q < RES_EPT; q++) {
       const float y = rv.y[q];
       const bool gt = y > mx;
-      mid = gt ? ((int)threadIdx.x + (q / RowView<Tin, RES>::EPV) * BT) * RowView<Tin, RES>::EPV +
-                     q % RowView<Tin, RES>::EPV
-               : mid;
+      mq = gt ? q : mq;
       mx = gt ? y : mx;
-      nvl += (uint32_t)(y > -__builtin_inff());
     }
+    nvl = rv.nallowed;
+    const int mid = ((int)threadIdx.x + (mq / EPV) * BT) * EPV + mq % EPV;
     mcl = mx > -__builtin_inff() ? comp_key(tg_key(mx), mid) : 0ull;
   } else {
     rv.each([&](int id, float y) {
@@ -517,8 +540,8 @@ __device__ __forceinline__ void topp_row(const SampleArgs& a, Row& r, unsigned c
       // allowed ids only)
       // (in wave order: a thread's slots follow the allowed ids of the
       // waves and lanes before it)
-      unsigned off = wbase + wincl - nown;
-      rv.each([&](int id, float y) { tl.E[off++] = Packed{y, id}; });
+      Packed* dst = tl.E + (wbase + wincl - nown);
+      rv.each([&](int id, float y) { *dst++ = Packed{y, id}; });
       __syncthreads();
       topp_rest(a, r, CompactView{tl.E, (int)nv}, tl, Mc, nv, ts, bs);
       return;
