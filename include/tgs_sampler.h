@@ -23,6 +23,9 @@
  * written into the row's output id:
  *     id >= 0   sampled token
  *     id == -1  no token is allowed (all masked / -inf / NaN)   [TGS_EALLMASKED]
+ *               (NaN logits are expected quiet, as arithmetic makes them; a
+ *               signaling-NaN logit may hide the other ids of its 16-byte
+ *               vector, since the kernels' maxima follow fmaxf)
  *     id == -2  invalid row parameters (see tgs_row_params)
  *     id == -3  row outside the tgs_batch_hint given to the call
  *     id == -4  a device-side wait between the workgroups of a row ran out
