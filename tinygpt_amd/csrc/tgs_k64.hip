@@ -107,7 +107,7 @@ template <int NW>
 struct Shared {
   u64 slots[NW][64];      // wave lists (merges, the ranked top k)
   uint4 svec[NW][64];     // per wave: vectors whose maximum reaches the collection threshold
-  int sidx[NW][64];       // their vector index in the chunk
+  int sidx[NW][64];       // their vector index in the chunk (with a mask: forbidden-id bits above bit 16)
   u64 own[64];            // merging workgroup: its own sorted top k
   uint32_t wkey[NW][NW];  // [m - 1][wave]: the wave's ceil(k / m)-th largest thread maximum key
   unsigned nbuf;          // candidates appended
@@ -676,6 +676,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
   float vm[NVT];
   float tm = -__builtin_inff();
   int im = 0;
+  uint32_t xpk[MASK ? HPW : 1] = {};  // forbidden-id bits of the thread's vectors (vector i at bit i * EPV)
 #pragma unroll
   for (int i = 0; i < NVT; i++) {
     float m;
@@ -684,6 +685,7 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       // 0xFFC00000, through the sign-extended bit of x), which the maximum
       // ignores: two operations per id instead of a test and a select
       const uint32_t x = masked ? ~(mw[i] >> ((v0 + ((int)threadIdx.x + i * NTT) * EPV) & 31)) : 0u;
+      xpk[(i * EPV) >> 5] |= (x & GM) << ((i * EPV) & 31);
       m = -__builtin_inff();
 #pragma unroll
       for (int e = 0; e < EPV; e++) {
@@ -882,7 +884,10 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       const unsigned sl = ns + lanes_below(bal);
       if (pass && sl < (unsigned)SCAP) {
         sh.svec[w][sl] = raw[i];
-        sh.sidx[w][sl] = (int)threadIdx.x + i * NTT;
+        // the vector index, with its forbidden-id bits above bit 16
+        int sx = (int)threadIdx.x + i * NTT;
+        if constexpr (MASK) sx |= (int)(((xpk[(i * EPV) >> 5] >> ((i * EPV) & 31)) & GM) << 16);
+        sh.sidx[w][sl] = sx;
       }
       ns += (unsigned)__popcll(bal);
     }
@@ -897,15 +902,15 @@ __global__ __launch_bounds__(NTT) void k64_kernel(SampleArgs a) {
       u64 x[EPV];
       bool ok[EPV];
       uint4 v = make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u);
-      int j = 0;
+      int sx = 0;
       if (si < nst) {
         v = sh.svec[w][si];
-        j = sh.sidx[w][si];
+        sx = sh.sidx[w][si];
       }
+      const int j = MASK ? sx & 0xFFFF : sx;
       const int o = j * EPV;
       const uint32_t hw = (pen && si < nst) ? HB::of(bitmap, j) : 0u;
-      uint32_t xm = 0u;
-      if constexpr (MASK) xm = (masked && si < nst) ? ~(r.mrow[(v0 + o) >> 5] >> ((v0 + o) & 31)) : 0u;
+      const uint32_t xm = MASK ? (uint32_t)sx >> 16 : 0u;  // the forbidden-id bits staged with the index
 #pragma unroll
       for (int e = 0; e < EPV; e++) {
         const float z = Elem<Tin>::get(v, e);
