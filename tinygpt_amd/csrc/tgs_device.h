@@ -92,6 +92,29 @@ __device__ __forceinline__ float tg_expf_nonpos(float x_in) {
   return (x_in >= -32.0f) ? e : 0.0f;
 }
 
+// tg_expf_nonpos(x) for -32 < x <= 0 (a caller that has tested the range):
+// the same operations without the clamp to -32 and the final select, which
+// are the identity there.
+__device__ __forceinline__ float tg_expf_nonpos_in(float x) {
+  const float log2e = 0x1.715476p+0f;
+  const float ln2_hi = 0x1.62ep-1f;
+  const float ln2_lo = 0x1.0bfbe8p-15f;
+  const float shifter = 12582912.0f;
+  float t = x * log2e;
+  float n = (t + shifter) - shifter;
+  float r = __builtin_fmaf(n, -ln2_hi, x);
+  r = __builtin_fmaf(n, -ln2_lo, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
 // floor(e * 2^40) of a weight e in [0, 1] as an integer-valued double: the
 // per-lane sums of a few dozen such terms stay exact (below 2^53) and
 // convert to the same u64 as summing tg_q40 terms.

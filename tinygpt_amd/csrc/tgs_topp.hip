@@ -325,8 +325,8 @@ __device__ __forceinline__ void topp_rest(const SampleArgs& a, const Row& r, con
       const float x = y - m;
       const int bq = !(x > -32.0f) ? NB : (int)(-x * 32.0f);
       atomicAdd(&tl.CI[bq], 1u);
-      if (bq < NB) {
-        const u64 q = tg_q40(tg_expf_nonpos(x));
+      if (bq < NB) {  // -32 < x <= 0
+        const u64 q = tg_q40(tg_expf_nonpos_in(x));
         if (q) atomicAdd(&tl.MI[bq], q);
       }
     });
