@@ -16,14 +16,15 @@
 #pragma once
 
 #include <atomic>
-#include <barrier>
 #include <cmath>
+#include <condition_variable>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <memory>
+#include <mutex>
 #include <thread>
 #include <type_traits>
 #include <vector>
@@ -75,13 +76,46 @@ enum {
 
 namespace hipcpu {
 
+// A reusable barrier over n threads, with arrive_and_drop for a thread that
+// leaves (a mutex and a condition variable: GCC 11's std::barrier hung now
+// and then here when threads dropped out while others waited).
+class Barrier {
+ public:
+  explicit Barrier(unsigned n) : expected_(n), count_(n) {}
+  void arrive_and_wait() {
+    std::unique_lock<std::mutex> lk(m_);
+    const unsigned long g = gen_;
+    if (--count_ == 0) {
+      next_phase();
+    } else {
+      cv_.wait(lk, [&] { return gen_ != g; });
+    }
+  }
+  void arrive_and_drop() {
+    std::lock_guard<std::mutex> lk(m_);
+    --expected_;
+    if (--count_ == 0) next_phase();
+  }
+
+ private:
+  void next_phase() {
+    ++gen_;
+    count_ = expected_;
+    cv_.notify_all();
+  }
+  std::mutex m_;
+  std::condition_variable cv_;
+  unsigned expected_, count_;
+  unsigned long gen_ = 0;
+};
+
 struct WaveCtx {
-  std::unique_ptr<std::barrier<>> bar;
+  std::unique_ptr<Barrier> bar;
   uint64_t buf[64];
 };
 constexpr size_t kStaticSmem = 65536;  // per-block static LDS object (TGS_STATIC_SMEM) at most
 struct BlockCtx {
-  std::unique_ptr<std::barrier<>> bar;
+  std::unique_ptr<Barrier> bar;
   std::vector<WaveCtx> waves;
   std::vector<unsigned char> smem;
   std::vector<unsigned char> ssmem;
@@ -138,11 +172,11 @@ inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args
     std::vector<std::unique_ptr<BlockCtx>> ctxs(nb);
     for (unsigned i = 0; i < nb; i++) {
       auto ctx = std::make_unique<BlockCtx>();
-      ctx->bar = std::make_unique<std::barrier<>>(nt);
+      ctx->bar = std::make_unique<Barrier>(nt);
       ctx->waves.resize((nt + 63) / 64);
       for (unsigned w = 0; w < ctx->waves.size(); w++) {
         const unsigned n = std::min(64u, nt - 64 * w);
-        ctx->waves[w].bar = std::make_unique<std::barrier<>>(n);
+        ctx->waves[w].bar = std::make_unique<Barrier>(n);
       }
       ctx->smem.assign(shmem ? shmem : 1, 0xA5);
       ctx->ssmem.assign(kStaticSmem, 0xA5);

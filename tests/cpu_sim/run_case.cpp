@@ -10,6 +10,8 @@
 #include <string>
 #include <vector>
 
+#include <unistd.h>
+
 #include "../../include/tgs_sampler.h"
 
 static std::vector<char> slurp(const std::string& path) {
@@ -32,6 +34,10 @@ static void dump(const std::string& path, const void* p, size_t n) {
 
 int main(int argc, char** argv) {
   if (argc < 3) return 2;
+  // a simulated run that has not ended after this long is stopped by
+  // SIGALRM (a deadlock in a simulated kernel ends the test, not the suite)
+  const char* al = std::getenv("TGS_SIM_ALARM");
+  alarm(al ? (unsigned)std::atoi(al) : 900u);
   const std::string mode = argv[1], dir = argv[2];
   FILE* m = std::fopen((dir + "/meta.txt").c_str(), "r");
   if (!m) return 3;
