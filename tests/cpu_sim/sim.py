@@ -22,7 +22,7 @@ def build():
     os.makedirs(os.path.join(HERE, "build"), exist_ok=True)
     with open(os.path.join(HERE, "build", ".lock"), "w") as lk:
         fcntl.flock(lk, fcntl.LOCK_EX)
-        subprocess.run(["make", "-s", "-C", HERE], check=True)
+        subprocess.run(["make", "-s", f"-j{min(8, os.cpu_count() or 1)}", "-C", HERE], check=True)
 
 
 def _san_env():
