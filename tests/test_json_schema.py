@@ -283,6 +283,28 @@ def test_local_dfa_rows_equal_token_replay(si):
     assert checked >= 10
 
 
+@pytest.mark.parametrize("si", range(len(SCHEMAS)))
+def test_local_dfa_cache_gives_the_same_automaton(si):
+    """local_dfa with a step cache kept across calls (as JsonSchemaConstraint
+    keeps it) builds the same automaton as a fresh build: the same
+    transitions, completion flags and roots, call after call."""
+    text = SCHEMAS[si]
+    toks = U.json_vocab()
+    trie = J.TokenTrie(toks)
+    fsm = J.JsonSchemaFSM(J.schema_from_json(text))
+    g = np.random.default_rng(500 + si)
+    cache = {}
+    for _ in range(4):
+        _, snaps = U.random_document(fsm, g, max_steps=300, partial=True)
+        picks = sorted(set(g.choice(len(snaps), size=min(8, len(snaps)), replace=False).tolist()))
+        want = J.local_dfa([snaps[i] for i in picks], J.TokenTrie(toks))
+        got = J.local_dfa([snaps[i] for i in picks], trie, cache=cache)
+        np.testing.assert_array_equal(got.trans, want.trans)
+        np.testing.assert_array_equal(got.complete, want.complete)
+        assert got.roots == want.roots
+    assert cache
+
+
 def test_canonical_keys_merge_equivalent_snapshots():
     """Free strings of different contents with the same counted length share
     a key; so do any-object keys no required name extends; enum prefixes

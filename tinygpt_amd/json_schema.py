@@ -547,9 +547,25 @@ class TokenTrie:
         special = (arr >= 0) & ((arr < 0x20) | (arr == 0x22) | (arr == 0x5C))
         self.last_special = np.where(special, np.arange(L, dtype=np.int16)[None, :], -1).max(axis=1)
         self.n = len(toks)
+        self._kids = {}  # (lo, hi, d) -> children: the trie never changes, and walks revisit its nodes
+        self._spec = {}  # (lo, hi) -> last depth holding a quote, backslash or control byte
 
     def children(self, lo, hi, d):
         """(byte, lo, hi) of each child of the node (range [lo, hi), depth d)."""
+        key = (lo, hi, d)
+        kids = self._kids.get(key)
+        if kids is None:
+            kids = self._kids[key] = self._children(lo, hi, d)
+        return kids
+
+    def last_special_of(self, lo, hi):
+        """The deepest quote, backslash or control byte of tokens [lo, hi) (-1: none)."""
+        v = self._spec.get((lo, hi))
+        if v is None:
+            v = self._spec[(lo, hi)] = int(self.last_special[lo:hi].max())
+        return v
+
+    def _children(self, lo, hi, d):
         if d >= self.max_len:
             return []
         col = self.arr[lo:hi, d]
@@ -597,7 +613,7 @@ class LocalDfa:
         return s
 
 
-def local_dfa(snaps, trie: TokenTrie, max_states: int = 200000) -> LocalDfa:
+def local_dfa(snaps, trie: TokenTrie, max_states: int = 200000, cache=None) -> LocalDfa:
     """Device form of the snapshots: a byte-level DFA whose walk of every
     vocabulary token from the snapshot's root state rejects exactly when
     the automaton rejects one of the token's bytes.
@@ -608,19 +624,27 @@ def local_dfa(snaps, trie: TokenTrie, max_states: int = 200000) -> LocalDfa:
     whole row at once (three byte groups) along the chain of counted
     characters, and the trie walk under it descends only into subtrees
     holding a quote, a backslash or a control byte.  Transitions no token
-    reaches stay -1.  Raises ValueError past max_states."""
+    reaches stay -1.  Raises ValueError past max_states.
+
+    cache: a dict kept by the caller across calls, holding each (state key,
+    byte) -> (successor key, successor snapshot) step and each state's byte
+    groups, so that later calls do not drive the automaton again for steps
+    an earlier call took (snapshots of one canonical key behave alike, the
+    premise of the interning).  The result is the same with or without it."""
     ids = {}
-    reps, rows, done, full = [], [], [], []
+    reps, rows, done, full, keys = [], [], [], [], []
     chain = []  # free strings: depth of plain bytes whose rows are complete
 
-    def intern(s):
-        key = canonical_key(s)
+    def intern(s, key=None):
+        if key is None:
+            key = canonical_key(s)
         i = ids.get(key)
         if i is None:
             i = len(reps)
             if i >= max_states:
                 raise ValueError(f"local automaton exceeds {max_states} states")
             ids[key] = i
+            keys.append(key)
             reps.append(s)
             rows.append(np.full(256, -1, dtype=np.int32))
             done.append(np.zeros(256, dtype=bool))
@@ -630,14 +654,27 @@ def local_dfa(snaps, trie: TokenTrie, max_states: int = 200000) -> LocalDfa:
 
     def step(i, b):
         if not done[i][b]:
-            nxt = _drive(reps[i], b)
-            rows[i][b] = -1 if nxt is None else intern(nxt)
+            hit = cache.get((keys[i], b)) if cache is not None else None
+            if hit is None:
+                nxt = _drive(reps[i], b)
+                hit = (None, None) if nxt is None else (canonical_key(nxt), nxt)
+                if cache is not None:
+                    cache[(keys[i], b)] = hit
+            rows[i][b] = -1 if hit[0] is None else intern(hit[1], hit[0])
             done[i][b] = True
         return int(rows[i][b])
 
+    def groups(i):
+        if cache is None:
+            return _byte_groups(reps[i])
+        g = cache.get(("groups", keys[i]))
+        if g is None:
+            g = cache[("groups", keys[i])] = _byte_groups(reps[i])
+        return g
+
     def fill(i):
         if not full[i]:
-            for rep, group in _byte_groups(reps[i]):
+            for rep, group in groups(i):
                 j = step(i, rep)
                 rows[i][group] = j
                 done[i][group] = True
@@ -664,7 +701,7 @@ def local_dfa(snaps, trie: TokenTrie, max_states: int = 200000) -> LocalDfa:
             if free:
                 ensure_chain(i, L - d)
             for c, clo, chi in trie.children(lo, hi, d):
-                if free and 0x20 <= c and c != 0x22 and c != 0x5C and int(trie.last_special[clo:chi].max()) <= d:
+                if free and 0x20 <= c and c != 0x22 and c != 0x5C and trie.last_special_of(clo, chi) <= d:
                     continue  # plain bytes only from here: the chain's rows hold them
                 j = int(rows[i][c]) if free else step(i, c)
                 if j >= 0:
@@ -697,6 +734,7 @@ class JsonSchemaConstraint:
         self.row0, self.n_rows = int(row0), int(n_rows)
         self.device = device
         self.rows = {}  # canonical key -> table row
+        self._dfa_cache = {}  # automaton steps kept across calls (local_dfa's cache)
         off, data = token_csr(self.tokens)
         import torch
 
@@ -729,7 +767,7 @@ class JsonSchemaConstraint:
                 new.append((s, r))
             out[i] = r
         if new:
-            dfa = local_dfa([s for s, _ in new], self.trie)
+            dfa = local_dfa([s for s, _ in new], self.trie, cache=self._dfa_cache)
             bc, ct = dfa.byte_classes()
             # The uploads are made and allocated on the stream the rows are built
             # on: the build reads them in stream order, and the allocator does
