@@ -302,6 +302,14 @@ def test_local_dfa_cache_gives_the_same_automaton(si):
         np.testing.assert_array_equal(got.trans, want.trans)
         np.testing.assert_array_equal(got.complete, want.complete)
         assert got.roots == want.roots
+        # byte classes: equal columns share a class, numbered by first byte
+        # (checked against a sort of the columns, np.unique)
+        bc, ct = got.byte_classes()
+        _, first, inv = np.unique(got.trans.T, axis=0, return_index=True, return_inverse=True)
+        rank = np.empty(len(first), dtype=np.int64)
+        rank[np.argsort(first)] = np.arange(len(first))
+        np.testing.assert_array_equal(bc, rank[inv.reshape(-1)].astype(np.uint8))
+        np.testing.assert_array_equal(ct, got.trans[:, np.sort(first)])
     assert cache
 
 

@@ -593,13 +593,18 @@ class LocalDfa:
         return self.trans.shape[0]
 
     def byte_classes(self):
-        """(byte_class uint8 [256], trans int32 [n, n_cls]) as tinygpt_amd.grammar.Dfa.byte_classes."""
-        _, first, inv = np.unique(self.trans.T, axis=0, return_index=True, return_inverse=True)
-        order = np.argsort(first)
-        rank = np.empty_like(order)
-        rank[order] = np.arange(len(order))
-        byte_class = rank[inv.reshape(-1)].astype(np.uint8)
-        ctrans = np.ascontiguousarray(self.trans[:, np.sort(first)], dtype=np.int32)
+        """(byte_class uint8 [256], trans int32 [n, n_cls]) as tinygpt_amd.grammar.Dfa.byte_classes:
+        bytes with equal columns share a class, classes numbered in the order
+        of their first byte (columns compared by their bytes, one pass)."""
+        cols = np.ascontiguousarray(self.trans.T)
+        seen, firsts = {}, []
+        byte_class = np.empty(256, dtype=np.uint8)
+        for b in range(256):
+            c = seen.setdefault(cols[b].tobytes(), len(firsts))
+            if c == len(firsts):
+                firsts.append(b)
+            byte_class[b] = c
+        ctrans = np.ascontiguousarray(self.trans[:, firsts], dtype=np.int32)
         return byte_class, ctrans
 
     def walk(self, state, data):
@@ -669,7 +674,7 @@ def local_dfa(snaps, trie: TokenTrie, max_states: int = 200000, cache=None) -> L
             return _byte_groups(reps[i])
         g = cache.get(("groups", keys[i]))
         if g is None:
-            g = cache[("groups", keys[i])] = _byte_groups(reps[i])
+            g = cache[("groups", keys[i])] = [(r, np.asarray(grp, dtype=np.intp)) for r, grp in _byte_groups(reps[i])]
         return g
 
     def fill(i):
