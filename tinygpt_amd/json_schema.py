@@ -727,6 +727,8 @@ class JsonSchemaConstraint:
     device in one tgs_mask_rows_from_dfa call; `commit` replays the sampled
     token's bytes (LogitsMasker.commit, ConstrainedGen.swift:827-830)."""
 
+    DFA_CACHE_MAX = 1 << 21  # automaton steps kept across calls before the cache starts over
+
     def __init__(self, sampler, schema: SchemaNode, tokens, eos: int = -1, row0: int = 0, n_rows: int = 1024,
                  device="cuda:0"):
         from .grammar import token_csr
@@ -772,6 +774,8 @@ class JsonSchemaConstraint:
                 new.append((s, r))
             out[i] = r
         if new:
+            if len(self._dfa_cache) > self.DFA_CACHE_MAX:  # bounded memory over a long-lived constraint
+                self._dfa_cache.clear()
             dfa = local_dfa([s for s, _ in new], self.trie, cache=self._dfa_cache)
             bc, ct = dfa.byte_classes()
             # The uploads are made and allocated on the stream the rows are built
