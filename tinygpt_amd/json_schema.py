@@ -252,6 +252,21 @@ def _step_array(f, b):
     return _REJ
 
 
+_PREFIX_SETS = {}
+
+
+def _prefixes(names):
+    """Every prefix of every string of names (a tuple or frozenset), as a
+    set, built once per collection: s is a prefix of some member exactly when
+    s is in it."""
+    p = _PREFIX_SETS.get(names)
+    if p is None:
+        if len(_PREFIX_SETS) > 100000:
+            _PREFIX_SETS.clear()
+        p = _PREFIX_SETS[names] = frozenset(e[:i] for e in names for i in range(len(e) + 1))
+    return p
+
+
 def _step_string(f, b):
     _, st, digits, enum, mn, mx, content, is_key = f
     if st == S_BODY:
@@ -270,7 +285,7 @@ def _step_string(f, b):
         nc = content + chr(b)
         if mx is not None and len(nc) > mx:
             return _REJ
-        if enum is not None and not any(e.startswith(nc) for e in enum):
+        if enum is not None and nc not in _prefixes(enum):
             return _REJ
         return (_REPLACE, ("S", S_BODY, 0, enum, mn, mx, nc, is_key))
     if st == S_ESC:
@@ -449,7 +464,7 @@ def _canon_frame(f, below):
             c = content
         elif is_key:
             req = below[1].required if below is not None and below[0] == "O" else frozenset()
-            c = content if any(r.startswith(content) for r in req) else _OTHER
+            c = content if content in _prefixes(req) else _OTHER
         else:
             cap = max(mn or 0, (mx + 1) if mx is not None else 0)
             c = min(len(content), cap)
