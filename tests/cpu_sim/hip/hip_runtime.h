@@ -17,17 +17,19 @@
 
 #include <atomic>
 #include <cmath>
-#include <condition_variable>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <memory>
-#include <mutex>
 #include <thread>
 #include <type_traits>
 #include <vector>
+
+#include <linux/futex.h>
+#include <sys/syscall.h>
+#include <unistd.h>
 
 #define __global__
 #define __device__
@@ -77,36 +79,40 @@ enum {
 namespace hipcpu {
 
 // A reusable barrier over n threads, with arrive_and_drop for a thread that
-// leaves (a mutex and a condition variable: GCC 11's std::barrier hung now
-// and then here when threads dropped out while others waited).
+// leaves.  Arrivals count down one word; the last arrival resets the count,
+// advances the generation word and wakes every waiter with one futex call,
+// and a waiter sleeps on the generation word until it moves (no mutex, so the
+// woken threads do not queue for a lock; GCC 11's std::barrier hung now and
+// then here when threads dropped out while others waited).  A thread reads
+// the generation before it arrives: the generation cannot move before its own
+// arrival, and a futex wait on a stale value returns at once.
 class Barrier {
  public:
   explicit Barrier(unsigned n) : expected_(n), count_(n) {}
   void arrive_and_wait() {
-    std::unique_lock<std::mutex> lk(m_);
-    const unsigned long g = gen_;
-    if (--count_ == 0) {
+    const uint32_t g = __atomic_load_n(&gen_, __ATOMIC_ACQUIRE);
+    if (__atomic_sub_fetch(&count_, 1u, __ATOMIC_ACQ_REL) == 0) {
       next_phase();
-    } else {
-      cv_.wait(lk, [&] { return gen_ != g; });
+      return;
     }
+    while (__atomic_load_n(&gen_, __ATOMIC_ACQUIRE) == g)
+      syscall(SYS_futex, &gen_, FUTEX_WAIT_PRIVATE, g, nullptr, nullptr, 0);
   }
   void arrive_and_drop() {
-    std::lock_guard<std::mutex> lk(m_);
-    --expected_;
-    if (--count_ == 0) next_phase();
+    // the expected count drops before this arrival counts, so the arrival
+    // that completes the phase reads it
+    __atomic_sub_fetch(&expected_, 1u, __ATOMIC_ACQ_REL);
+    if (__atomic_sub_fetch(&count_, 1u, __ATOMIC_ACQ_REL) == 0) next_phase();
   }
 
  private:
   void next_phase() {
-    ++gen_;
-    count_ = expected_;
-    cv_.notify_all();
+    __atomic_store_n(&count_, __atomic_load_n(&expected_, __ATOMIC_ACQUIRE), __ATOMIC_RELAXED);
+    __atomic_add_fetch(&gen_, 1u, __ATOMIC_RELEASE);
+    syscall(SYS_futex, &gen_, FUTEX_WAKE_PRIVATE, INT32_MAX, nullptr, nullptr, 0);
   }
-  std::mutex m_;
-  std::condition_variable cv_;
-  unsigned expected_, count_;
-  unsigned long gen_ = 0;
+  uint32_t expected_, count_;
+  uint32_t gen_ = 0;
 };
 
 struct WaveCtx {
@@ -167,36 +173,61 @@ inline void launch(void (*k)(Args...), dim3 grid, dim3 block, size_t shmem, Args
   // blocks started together (a launch too large to run as threads at once,
   // such as a set-up fill over a whole workspace, runs block by block)
   const unsigned group = conc && (size_t)nblk * nt <= 16384 ? nblk : 1u;
+  auto make_ctx = [&]() {
+    auto ctx = std::make_unique<BlockCtx>();
+    ctx->bar = std::make_unique<Barrier>(nt);
+    ctx->waves.resize((nt + 63) / 64);
+    for (unsigned w = 0; w < ctx->waves.size(); w++) {
+      const unsigned n = std::min(64u, nt - 64 * w);
+      ctx->waves[w].bar = std::make_unique<Barrier>(n);
+    }
+    ctx->smem.assign(shmem ? shmem : 1, 0xA5);
+    ctx->ssmem.assign(kStaticSmem, 0xA5);
+    return ctx;
+  };
+  auto run_thread = [=](BlockCtx* ctx, unsigned t, unsigned bi) {
+    t_ctx = ctx;
+    t_thread = dim3(t);
+    t_block = dim3(bi % grid.x, bi / grid.x);
+    k(args...);
+    ctx->waves[t / 64].bar->arrive_and_drop();
+    ctx->bar->arrive_and_drop();
+  };
+  if (group == 1) {
+    // block by block on one set of nt threads (creating threads costs more
+    // than the kernels here): the host thread sets each block up, a gate
+    // lets the threads into it, and a second gate waits for all of them
+    std::unique_ptr<BlockCtx> cur;
+    Barrier gate(nt + 1);
+    std::vector<std::thread> th;
+    th.reserve(nt);
+    for (unsigned t = 0; t < nt; t++)
+      th.emplace_back([&, t]() {
+        for (unsigned bi = 0; bi < nblk; bi++) {
+          gate.arrive_and_wait();
+          run_thread(cur.get(), t, bi);
+          gate.arrive_and_wait();
+        }
+      });
+    for (unsigned bi = 0; bi < nblk; bi++) {
+      cur = make_ctx();
+      std::memset(__start_tgs_lds, 0xA5, (size_t)(__stop_tgs_lds - __start_tgs_lds));
+      gate.arrive_and_wait();
+      gate.arrive_and_wait();
+    }
+    for (auto& x : th) x.join();
+    return;
+  }
   for (unsigned b0 = 0; b0 < nblk; b0 += group) {
     const unsigned nb = std::min(group, nblk - b0);
     std::vector<std::unique_ptr<BlockCtx>> ctxs(nb);
-    for (unsigned i = 0; i < nb; i++) {
-      auto ctx = std::make_unique<BlockCtx>();
-      ctx->bar = std::make_unique<Barrier>(nt);
-      ctx->waves.resize((nt + 63) / 64);
-      for (unsigned w = 0; w < ctx->waves.size(); w++) {
-        const unsigned n = std::min(64u, nt - 64 * w);
-        ctx->waves[w].bar = std::make_unique<Barrier>(n);
-      }
-      ctx->smem.assign(shmem ? shmem : 1, 0xA5);
-      ctx->ssmem.assign(kStaticSmem, 0xA5);
-      ctxs[i] = std::move(ctx);
-    }
+    for (unsigned i = 0; i < nb; i++) ctxs[i] = make_ctx();
     std::memset(__start_tgs_lds, 0xA5, (size_t)(__stop_tgs_lds - __start_tgs_lds));
     std::vector<std::thread> th;
     th.reserve((size_t)nb * nt);
     for (unsigned i = 0; i < nb; i++) {
-      const unsigned bi = b0 + i, bx = bi % grid.x, by = bi / grid.x;
       BlockCtx* ctx = ctxs[i].get();
-      for (unsigned t = 0; t < nt; t++)
-        th.emplace_back([=]() {
-          t_ctx = ctx;
-          t_thread = dim3(t);
-          t_block = dim3(bx, by);
-          k(args...);
-          ctx->waves[t / 64].bar->arrive_and_drop();
-          ctx->bar->arrive_and_drop();
-        });
+      for (unsigned t = 0; t < nt; t++) th.emplace_back([=]() { run_thread(ctx, t, b0 + i); });
     }
     for (auto& x : th) x.join();
   }
